@@ -1,0 +1,28 @@
+"""MI355X-native (gfx950) DeLS-Spec draft-token selection path.
+
+Public surface (mirrors the reference's interface for this path):
+  * ``DeLSGraphRunner``          -- drop-in hipGraph suffix-rollout runner
+  * ``DeLSLocalHead``            -- local-head module the runner consumes
+  * ``parse_scalar_schedule``, ``load_unigram_log_prior``
+  * ``fused_argmax``, ``lowrank_argmax``, ``rank_proj``, ``gru_step`` -- the
+    per-step operators, each a thin wrapper over the C ABI in include/dels.h
+"""
+
+from .local_head import (DeLSLocalHead, load_unigram_log_prior, parse_scalar_schedule,
+                         unigram_log_prior_from_counts)
+from .ops import fused_argmax, gru_step, lowrank_argmax, rank_proj
+from .runner import DeLSGraphRunner
+from . import synth
+
+__all__ = [
+    "DeLSGraphRunner",
+    "DeLSLocalHead",
+    "parse_scalar_schedule",
+    "load_unigram_log_prior",
+    "unigram_log_prior_from_counts",
+    "fused_argmax",
+    "lowrank_argmax",
+    "rank_proj",
+    "gru_step",
+    "synth",
+]

@@ -1,0 +1,116 @@
+"""ctypes binding of the gfx950 C-ABI library (include/dels.h).
+
+The library is built in-tree by ``build.py`` into ``_lib/libdels_mi355x.so``.
+There is no fallback: if the library is missing or cannot be loaded, every
+operation raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  -- loads torch's HIP runtime first, so the library binds to it
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
+
+DELS_OK = 0
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+ACT_IDENTITY, ACT_SILU = 0, 1
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_ptr = ctypes.c_void_p
+_sz = ctypes.c_size_t
+_fptr = ctypes.c_void_p
+
+
+class RolloutParams(ctypes.Structure):
+    """Mirror of ``struct dels_rollout`` in include/dels.h."""
+
+    _fields_ = [
+        ("gi_table", _ptr), ("ld_gi", _i64), ("table_rows", _i64),
+        ("w_hh", _ptr), ("b_hh", _ptr),
+        ("rank_w", _ptr), ("rank_b", _ptr), ("act", _int),
+        ("lm_w", _ptr),
+        ("prior", _ptr), ("prior_dtype", _int),
+        ("alpha", _fptr), ("beta", _fptr),
+        ("batch", _i64), ("steps", _i64), ("G", _i64), ("r", _i64), ("V", _i64),
+        ("prefix_ids", _ptr),
+        ("base", _ptr), ("base_dtype", _int),
+        ("out_ids", _ptr), ("out_scores", _ptr),
+        ("h_a", _ptr), ("h_b", _ptr),
+        ("rank", _ptr),
+        ("ws", _ptr), ("ws_bytes", _sz),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/dels.h declares.
+SIGNATURES = {
+    "dels_abi_version": (_int, []),
+    "dels_strerror": (ctypes.c_char_p, [_int]),
+    "dels_last_error": (ctypes.c_char_p, []),
+    "dels_workspace_init": (_int, [_ptr, _sz, _ptr]),
+    "dels_rank_proj_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_rank_proj": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_fused_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_fused_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _int, _ptr, _int, _fptr, _i64, _fptr, _i64,
+                                 _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_lowrank_argmax_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "dels_lowrank_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _int, _ptr, _i64, _ptr, _i64, _int, _ptr, _int,
+                                   _fptr, _i64, _fptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz,
+                                   _ptr]),
+    "dels_gru_step_ws_bytes": (_sz, [_i64, _i64]),
+    "dels_gru_step": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr,
+                             _sz, _ptr]),
+    "dels_rollout_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "dels_rollout_enqueue": (_int, [ctypes.POINTER(RolloutParams), _ptr]),
+    "dels_graph_create": (_int, [ctypes.POINTER(RolloutParams), ctypes.POINTER(_ptr)]),
+    "dels_graph_launch": (_int, [_ptr, _ptr]),
+    "dels_graph_destroy": (_int, [_ptr]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class DelsError(RuntimeError):
+    """A nonzero status returned by the C ABI."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load the library once and attach the argument/return types."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"DeLS HIP library not found at {LIB_PATH}; build it with "
+                "`python dels-spec_amd/build.py` (or __graft_entry__.build()).")
+        lib = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.dels_abi_version() != 1:
+            raise RuntimeError("DeLS HIP library ABI version mismatch")
+        _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise ``DelsError`` for a nonzero C-ABI status."""
+    if status != DELS_OK:
+        lib = load()
+        name = lib.dels_strerror(status).decode()
+        detail = lib.dels_last_error().decode()
+        raise DelsError(status, f"{what} failed ({name}): {detail}")

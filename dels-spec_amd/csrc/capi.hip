@@ -1,0 +1,482 @@
+// C ABI of the DeLS draft-token selection path (declared in include/dels.h).
+//
+// Host-side argument checking, workspace layout and kernel dispatch.  Nothing
+// here allocates device memory or synchronises the caller's stream; the only
+// objects the library creates are the hipGraph/hipGraphExec (and the capture
+// stream) owned by a dels_graph_create handle.
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/dels.h"
+#include "dels_internal.h"
+
+namespace dels {
+
+static thread_local std::string g_last_error;
+
+static int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+static int hip_fail(hipError_t e, const char* what) {
+    return fail(DELS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int device_cu_count() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 1;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
+__global__ void fill_zero_kernel(uint32_t* p, size_t words) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < words; i += (size_t)gridDim.x * blockDim.x)
+        p[i] = 0u;
+}
+
+hipError_t launch_fill_zero(void* ws, size_t bytes, hipStream_t s) {
+    const size_t words = bytes / 4;
+    if (words == 0) return hipSuccess;
+    const int blocks = (int)std::min<size_t>(1024, (words + 255) / 256);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, s, static_cast<uint32_t*>(ws), words);
+    return hipGetLastError();
+}
+
+static inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+static inline bool valid_dtype(int d) { return d == DELS_DTYPE_F32 || d == DELS_DTYPE_BF16 || d == DELS_DTYPE_F16; }
+static inline size_t dtype_size(int d) { return d == DELS_DTYPE_F32 ? 4 : 2; }
+
+// Checks of a bf16 row-major operand: non-null, 16-byte aligned, ld % 8 == 0, ld >= cols.
+static int check_bf16_matrix(const void* p, int64_t ld, int64_t cols, const char* name) {
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+    if (ld < cols) return fail(DELS_ERR_INVALID_ARGUMENT, "%s: leading dimension %lld < columns %lld", name,
+                               (long long)ld, (long long)cols);
+    if (!aligned16(p) || (ld % 8) != 0)
+        return fail(DELS_ERR_ALIGNMENT, "%s must be 16-byte aligned with a leading dimension divisible by 8", name);
+    return DELS_OK;
+}
+
+// ---- workspace layouts -------------------------------------------------------
+
+struct LowrankLayout {
+    size_t argmax_off, rank_off, skinny_off, total;
+    SkinnyPlan plan;
+};
+
+static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) {
+    LowrankLayout L{};
+    L.plan = plan_skinny(M, d, r, false);
+    L.argmax_off = 0;
+    L.rank_off = align256(argmax_ws_bytes(M, r, V));
+    L.skinny_off = L.rank_off + align256((size_t)M * r * 2);
+    L.total = L.skinny_off + skinny_ws_bytes(L.plan);
+    return L;
+}
+
+struct RolloutLayout {
+    size_t argmax_off, rank_off, gru_off, total;
+    SkinnyPlan rank_plan, gru_plan;
+};
+
+static RolloutLayout rollout_layout(int64_t batch, int64_t G, int64_t r, int64_t V) {
+    RolloutLayout L{};
+    L.rank_plan = plan_skinny(batch, G, r, false);
+    L.gru_plan = plan_skinny(batch, G, G, true);
+    L.argmax_off = 0;
+    L.rank_off = align256(argmax_ws_bytes(batch, r, V));
+    L.gru_off = L.rank_off + align256(skinny_ws_bytes(L.rank_plan));
+    L.total = L.gru_off + align256(skinny_ws_bytes(L.gru_plan));
+    return L;
+}
+
+// ---- argument checks shared by several entry points ----------------------------
+
+static int check_argmax_args(const void* rank, int64_t ldrank, const void* B, int64_t ldb,
+                             const void* base, int64_t ldbase, int base_dtype,
+                             const void* prior, int prior_dtype,
+                             const float* alpha, int64_t alpha_stride,
+                             const float* beta, int64_t beta_stride,
+                             int64_t M, int64_t r, int64_t V,
+                             const int64_t* out_ids, int64_t ld_out, bool check_rank) {
+    if (M < 0 || r <= 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape M=%lld r=%lld V=%lld",
+                                               (long long)M, (long long)r, (long long)V);
+    if (V >= INT32_MAX || M >= INT32_MAX) return fail(DELS_ERR_UNSUPPORTED, "M and V must be < 2^31-1");
+    if (r % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "rank dimension r=%lld must be a multiple of 8", (long long)r);
+    if (!argmax_supported(M, r, V)) return fail(DELS_ERR_UNSUPPORTED, "rank dimension r=%lld not supported (8..512)",
+                                                (long long)r);
+    if (M == 0) return DELS_OK;   // nothing to read or write
+    int rc;
+    if (check_rank && (rc = check_bf16_matrix(rank, ldrank, r, "rank")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(B, ldb, r, "B (low-rank LM head)")) != DELS_OK) return rc;
+    if (!base) return fail(DELS_ERR_INVALID_ARGUMENT, "base logits pointer is NULL");
+    if (!valid_dtype(base_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown base dtype %d", base_dtype);
+    if (M > 1 && ldbase < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
+                                         (long long)ldbase, (long long)V);
+    if (prior && !valid_dtype(prior_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown prior dtype %d", prior_dtype);
+    if (!alpha || !beta) return fail(DELS_ERR_INVALID_ARGUMENT, "alpha/beta pointers must be non-NULL");
+    if (alpha_stride < 0 || beta_stride < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "negative alpha/beta stride");
+    if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+    if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    return DELS_OK;
+}
+
+static int check_ws(const void* ws, size_t ws_bytes, size_t need) {
+    if (need == 0) return DELS_OK;
+    if (!ws) return fail(DELS_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", need);
+    if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return fail(DELS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    if (ws_bytes < need) return fail(DELS_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
+    return DELS_OK;
+}
+
+static int check_gru_args(const void* gi_table, int64_t ld_gi, int64_t table_rows, const int64_t* tokens,
+                          const void* h_in, int64_t ldh_in, const void* w_hh, int64_t batch, int64_t G,
+                          const void* h_out, int64_t ldh_out) {
+    if (batch < 0 || G <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad GRU shape batch=%lld G=%lld",
+                                         (long long)batch, (long long)G);
+    if (batch > 64) return fail(DELS_ERR_UNSUPPORTED, "GRU step supports batch <= 64 (got %lld)", (long long)batch);
+    if (G >= (1 << 24)) return fail(DELS_ERR_UNSUPPORTED, "GRU hidden size too large");
+    if (G % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "GRU hidden size %lld must be a multiple of 8", (long long)G);
+    if (batch == 0) return DELS_OK;
+    if (!gi_table || table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "GRU input table is NULL or empty");
+    if (ld_gi < 3 * G) return fail(DELS_ERR_INVALID_ARGUMENT, "GRU input table leading dimension < 3G");
+    if (!tokens) return fail(DELS_ERR_INVALID_ARGUMENT, "token ids pointer is NULL");
+    int rc;
+    if (h_in && (rc = check_bf16_matrix(h_in, ldh_in, G, "h_in")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(w_hh, G, G, "W_hh")) != DELS_OK) return rc;
+    if (!h_out) return fail(DELS_ERR_INVALID_ARGUMENT, "h_out is NULL");
+    if (batch > 1 && ldh_out < G) return fail(DELS_ERR_INVALID_ARGUMENT, "h_out leading dimension < G");
+    if (h_in && h_in == h_out) return fail(DELS_ERR_INVALID_ARGUMENT, "h_in and h_out must not alias");
+    return DELS_OK;
+}
+
+// ---- rollout ---------------------------------------------------------------------
+
+static int check_rollout(const dels_rollout* p) {
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout parameters are NULL");
+    if (p->steps <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires steps > 0, got %lld", (long long)p->steps);
+    if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires batch > 0");
+    if (p->act != DELS_ACT_IDENTITY && p->act != DELS_ACT_SILU)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "unknown rank activation %d", p->act);
+    int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
+                            p->batch, p->G, p->h_b, p->G);
+    if (rc != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->h_b, p->G, p->G, "h_b")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->rank_w, p->G, p->G, "rank_w")) != DELS_OK) return rc;
+    if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->base, p->steps * p->V, p->base_dtype, p->prior,
+                                p->prior_dtype, p->alpha, 0, p->beta, 0, p->batch, p->r, p->V, p->out_ids,
+                                p->steps, true)) != DELS_OK)
+        return rc;
+    const RolloutLayout L = rollout_layout(p->batch, p->G, p->r, p->V);
+    return check_ws(p->ws, p->ws_bytes, L.total);
+}
+
+static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
+    const RolloutLayout L = rollout_layout(p->batch, p->G, p->r, p->V);
+    char* ws = static_cast<char*>(p->ws);
+    const int B = (int)p->batch, G = (int)p->G, r = (int)p->r, V = (int)p->V;
+
+    GruArgs g{};
+    g.gi_table = static_cast<const uint16_t*>(p->gi_table);
+    g.ld_gi = p->ld_gi;
+    g.table_rows = p->table_rows;
+    g.w_hh = static_cast<const uint16_t*>(p->w_hh);
+    g.b_hh = static_cast<const uint16_t*>(p->b_hh);
+    g.batch = B;
+    g.G = G;
+
+    // h0 = GRU(gi_table[prefix], 0)   (code/kernel/dels.py:426-433)
+    g.tokens = p->prefix_ids;
+    g.tok_stride = 1;
+    g.h_in = nullptr;
+    g.ldh_in = G;
+    g.h_out = static_cast<uint16_t*>(p->h_a);
+    g.ldh_out = G;
+    hipError_t e = launch_gru_step(g, L.gru_plan, ws + L.gru_off, s);
+    if (e != hipSuccess) return hip_fail(e, "GRU step launch");
+
+    uint16_t* h_cur = static_cast<uint16_t*>(p->h_a);
+    uint16_t* h_next = static_cast<uint16_t*>(p->h_b);
+    const size_t esz = dtype_size(p->base_dtype);
+    for (int step = 0; step < p->steps; ++step) {
+        RankArgs ra{};
+        ra.h = h_cur; ra.ldh = G;
+        ra.A = static_cast<const uint16_t*>(p->rank_w); ra.lda = G;
+        ra.bias = static_cast<const uint16_t*>(p->rank_b); ra.act = p->act;
+        ra.M = B; ra.d = G; ra.r = r;
+        ra.rank = static_cast<uint16_t*>(p->rank); ra.ldrank = r;
+        e = launch_rank_proj(ra, L.rank_plan, ws + L.rank_off, s);
+        if (e != hipSuccess) return hip_fail(e, "rank projection launch");
+
+        ArgmaxArgs aa{};
+        aa.rank = static_cast<const uint16_t*>(p->rank); aa.ldrank = r;
+        aa.B = static_cast<const uint16_t*>(p->lm_w); aa.ldb = r;
+        aa.base = static_cast<const char*>(p->base) + (size_t)step * V * esz;
+        aa.ldbase = p->steps * (int64_t)V;
+        aa.base_dtype = p->base_dtype;
+        aa.prior = p->prior; aa.prior_dtype = p->prior_dtype;
+        aa.alpha = p->alpha + step; aa.alpha_stride = 0;
+        aa.beta = p->beta + step; aa.beta_stride = 0;
+        aa.M = B; aa.r = r; aa.V = V;
+        aa.out_ids = p->out_ids + step;
+        aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
+        aa.ld_out = p->steps;
+        e = launch_fused_argmax(aa, ws + L.argmax_off, s);
+        if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
+
+        if (step + 1 < p->steps) {
+            g.tokens = p->out_ids + step;
+            g.tok_stride = p->steps;
+            g.h_in = h_cur;
+            g.h_out = h_next;
+            e = launch_gru_step(g, L.gru_plan, ws + L.gru_off, s);
+            if (e != hipSuccess) return hip_fail(e, "GRU step launch");
+            std::swap(h_cur, h_next);
+        }
+    }
+    return DELS_OK;
+}
+
+struct GraphHandle {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+}  // namespace dels
+
+using namespace dels;
+
+extern "C" {
+
+int dels_abi_version(void) { return DELS_ABI_VERSION; }
+
+const char* dels_strerror(int status) {
+    switch (status) {
+        case DELS_OK: return "success";
+        case DELS_ERR_INVALID_ARGUMENT: return "invalid argument";
+        case DELS_ERR_UNSUPPORTED: return "unsupported shape or type";
+        case DELS_ERR_ALIGNMENT: return "misaligned operand";
+        case DELS_ERR_WORKSPACE: return "workspace missing, misaligned or too small";
+        case DELS_ERR_HIP: return "HIP runtime error";
+        default: return "unknown status";
+    }
+}
+
+const char* dels_last_error(void) { return g_last_error.c_str(); }
+
+int dels_workspace_init(void* ws, size_t ws_bytes, void* stream) {
+    if (ws_bytes == 0) return DELS_OK;
+    if (!ws) return fail(DELS_ERR_WORKSPACE, "workspace is NULL");
+    if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0 || (ws_bytes % 4) != 0)
+        return fail(DELS_ERR_WORKSPACE, "workspace must be 256-byte aligned with a size divisible by 4");
+    hipError_t e = launch_fill_zero(ws, ws_bytes, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "workspace fill launch");
+}
+
+size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r) {
+    return skinny_ws_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1), std::max<int64_t>(r, 1), false));
+}
+
+int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, const void* bias, int act,
+                   int64_t M, int64_t d, int64_t r, void* rank, int64_t ldrank, void* ws, size_t ws_bytes,
+                   void* stream) {
+    if (M < 0 || d <= 0 || r <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad rank projection shape");
+    if (M >= (1 << 24) || d >= (1 << 26) || r >= (1 << 24)) return fail(DELS_ERR_UNSUPPORTED, "shape too large");
+    if (d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a multiple of 8", (long long)d);
+    if (act != DELS_ACT_IDENTITY && act != DELS_ACT_SILU)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
+    if (M == 0) return DELS_OK;
+    int rc;
+    if ((rc = check_bf16_matrix(h, ldh, d, "h")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(A, lda, d, "A (rank projection)")) != DELS_OK) return rc;
+    if (!rank) return fail(DELS_ERR_INVALID_ARGUMENT, "rank output is NULL");
+    if (ldrank < r) return fail(DELS_ERR_INVALID_ARGUMENT, "rank leading dimension < r");
+    const SkinnyPlan p = plan_skinny(M, d, r, false);
+    if ((rc = check_ws(ws, ws_bytes, skinny_ws_bytes(p))) != DELS_OK) return rc;
+    RankArgs ra{};
+    ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
+    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda;
+    ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
+    ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
+    ra.rank = static_cast<uint16_t*>(rank); ra.ldrank = ldrank;
+    hipError_t e = launch_rank_proj(ra, p, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "rank projection launch");
+}
+
+size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) { return argmax_ws_bytes(M, r, V); }
+
+int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb, const void* base,
+                      int64_t ldbase, int base_dtype, const void* prior, int prior_dtype, const float* alpha,
+                      int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t r,
+                      int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
+                      void* stream) {
+    int rc = check_argmax_args(rank, ldrank, B, ldb, base, ldbase, base_dtype, prior, prior_dtype, alpha,
+                               alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, true);
+    if (rc != DELS_OK) return rc;
+    if (M == 0) return DELS_OK;
+    if ((rc = check_ws(ws, ws_bytes, argmax_ws_bytes(M, r, V))) != DELS_OK) return rc;
+    ArgmaxArgs a{};
+    a.rank = static_cast<const uint16_t*>(rank); a.ldrank = ldrank;
+    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb;
+    a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
+    a.prior = prior; a.prior_dtype = prior_dtype;
+    a.alpha = alpha; a.alpha_stride = alpha_stride;
+    a.beta = beta; a.beta_stride = beta_stride;
+    a.M = (int)M; a.r = (int)r; a.V = (int)V;
+    a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
+    hipError_t e = launch_fused_argmax(a, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
+}
+
+size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) {
+    return lowrank_layout(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1), std::max<int64_t>(r, 1),
+                          std::max<int64_t>(V, 1)).total;
+}
+
+int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, const void* bias, int act,
+                        const void* B, int64_t ldb, const void* base, int64_t ldbase, int base_dtype,
+                        const void* prior, int prior_dtype, const float* alpha, int64_t alpha_stride,
+                        const float* beta, int64_t beta_stride, int64_t M, int64_t d, int64_t r, int64_t V,
+                        int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
+                        void* stream) {
+    int rc = check_argmax_args(nullptr, r, B, ldb, base, ldbase, base_dtype, prior, prior_dtype, alpha,
+                               alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, false);
+    if (rc != DELS_OK) return rc;
+    if (d <= 0 || d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8",
+                                          (long long)d);
+    if (act != DELS_ACT_IDENTITY && act != DELS_ACT_SILU)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
+    if (M == 0) return DELS_OK;
+    if ((rc = check_bf16_matrix(h, ldh, d, "h")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(A, lda, d, "A (rank projection)")) != DELS_OK) return rc;
+    const LowrankLayout L = lowrank_layout(M, d, r, V);
+    if ((rc = check_ws(ws, ws_bytes, L.total)) != DELS_OK) return rc;
+    char* w = static_cast<char*>(ws);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t* rank = reinterpret_cast<uint16_t*>(w + L.rank_off);
+
+    RankArgs ra{};
+    ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
+    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda;
+    ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
+    ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
+    ra.rank = rank; ra.ldrank = r;
+    hipError_t e = launch_rank_proj(ra, L.plan, w + L.skinny_off, s);
+    if (e != hipSuccess) return hip_fail(e, "rank projection launch");
+
+    ArgmaxArgs a{};
+    a.rank = rank; a.ldrank = r;
+    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb;
+    a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
+    a.prior = prior; a.prior_dtype = prior_dtype;
+    a.alpha = alpha; a.alpha_stride = alpha_stride;
+    a.beta = beta; a.beta_stride = beta_stride;
+    a.M = (int)M; a.r = (int)r; a.V = (int)V;
+    a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
+    e = launch_fused_argmax(a, w + L.argmax_off, s);
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
+}
+
+size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {
+    return skinny_ws_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1), std::max<int64_t>(G, 1), true));
+}
+
+int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const int64_t* tokens,
+                  int64_t tok_stride, const void* h_in, int64_t ldh_in, const void* w_hh, const void* b_hh,
+                  int64_t batch, int64_t G, void* h_out, int64_t ldh_out, void* ws, size_t ws_bytes,
+                  void* stream) {
+    int rc = check_gru_args(gi_table, ld_gi, table_rows, tokens, h_in, ldh_in, w_hh, batch, G, h_out, ldh_out);
+    if (rc != DELS_OK) return rc;
+    if (batch == 0) return DELS_OK;
+    const SkinnyPlan p = plan_skinny(batch, G, G, true);
+    if ((rc = check_ws(ws, ws_bytes, skinny_ws_bytes(p))) != DELS_OK) return rc;
+    GruArgs g{};
+    g.gi_table = static_cast<const uint16_t*>(gi_table); g.ld_gi = ld_gi; g.table_rows = table_rows;
+    g.tokens = tokens; g.tok_stride = tok_stride;
+    g.h_in = static_cast<const uint16_t*>(h_in); g.ldh_in = ldh_in;
+    g.w_hh = static_cast<const uint16_t*>(w_hh); g.b_hh = static_cast<const uint16_t*>(b_hh);
+    g.batch = (int)batch; g.G = (int)G;
+    g.h_out = static_cast<uint16_t*>(h_out); g.ldh_out = ldh_out;
+    hipError_t e = launch_gru_step(g, p, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "GRU step launch");
+}
+
+size_t dels_rollout_ws_bytes(int64_t batch, int64_t G, int64_t r, int64_t V) {
+    return rollout_layout(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1), std::max<int64_t>(r, 1),
+                          std::max<int64_t>(V, 1)).total;
+}
+
+int dels_rollout_enqueue(const dels_rollout* p, void* stream) {
+    int rc = check_rollout(p);
+    if (rc != DELS_OK) return rc;
+    return enqueue_rollout(p, static_cast<hipStream_t>(stream));
+}
+
+int dels_graph_create(const dels_rollout* p, void** graph_out) {
+    if (!graph_out) return fail(DELS_ERR_INVALID_ARGUMENT, "graph_out is NULL");
+    *graph_out = nullptr;
+    int rc = check_rollout(p);
+    if (rc != DELS_OK) return rc;
+    hipStream_t cs = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "capture stream creation");
+    // One eager pass first: resolves per-kernel launch configuration outside capture.
+    rc = enqueue_rollout(p, cs);
+    if (rc == DELS_OK && (e = hipStreamSynchronize(cs)) != hipSuccess) rc = hip_fail(e, "warm-up rollout");
+    hipGraph_t graph = nullptr;
+    if (rc == DELS_OK) {
+        e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "hipStreamBeginCapture");
+        } else {
+            rc = enqueue_rollout(p, cs);
+            hipError_t e2 = hipStreamEndCapture(cs, &graph);
+            if (rc == DELS_OK && e2 != hipSuccess) rc = hip_fail(e2, "hipStreamEndCapture");
+        }
+    }
+    hipGraphExec_t exec = nullptr;
+    if (rc == DELS_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+        rc = hip_fail(e, "hipGraphInstantiate");
+    hipStreamDestroy(cs);
+    if (rc != DELS_OK) {
+        if (graph) hipGraphDestroy(graph);
+        return rc;
+    }
+    GraphHandle* hdl = new GraphHandle{graph, exec};
+    *graph_out = hdl;
+    return DELS_OK;
+}
+
+int dels_graph_launch(void* graph, void* stream) {
+    if (!graph) return fail(DELS_ERR_INVALID_ARGUMENT, "graph handle is NULL");
+    GraphHandle* h = static_cast<GraphHandle*>(graph);
+    hipError_t e = hipGraphLaunch(h->exec, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "hipGraphLaunch");
+}
+
+int dels_graph_destroy(void* graph) {
+    if (!graph) return DELS_OK;
+    GraphHandle* h = static_cast<GraphHandle*>(graph);
+    hipError_t e1 = h->exec ? hipGraphExecDestroy(h->exec) : hipSuccess;
+    hipError_t e2 = h->graph ? hipGraphDestroy(h->graph) : hipSuccess;
+    delete h;
+    if (e1 != hipSuccess) return hip_fail(e1, "hipGraphExecDestroy");
+    if (e2 != hipSuccess) return hip_fail(e2, "hipGraphDestroy");
+    return DELS_OK;
+}
+
+}  // extern "C"

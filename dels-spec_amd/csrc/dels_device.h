@@ -1,0 +1,91 @@
+// Device-side helpers shared by the gfx950 kernels of the DeLS draft path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dels {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+struct bf16_t { uint16_t bits; };   // storage tag for bf16 base/prior
+struct f16_t { uint16_t bits; };    // storage tag for fp16 base/prior
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// float -> bf16 bits, round to nearest even; NaN stays a quiet NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+// Scalar element loads of base logits / prior, widened to fp32.
+__device__ __forceinline__ float load_f32(const float* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ float load_f32(const bf16_t* p) {
+    return bf16_bits_to_f32(__builtin_nontemporal_load(&p->bits));
+}
+__device__ __forceinline__ float load_f32(const f16_t* p) {
+    uint16_t b = __builtin_nontemporal_load(&p->bits);
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+// 16-byte operand loads: eight bf16 values.
+__device__ __forceinline__ bf16x8 load_bf16x8(const uint16_t* p) {
+    u32x4 v = *reinterpret_cast<const u32x4*>(p);
+    return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ bf16x8 load_bf16x8_nt(const uint16_t* p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ bf16x8 zero_bf16x8() { return __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u}); }
+
+// Order-preserving map float -> uint32 (a < b  <=>  key(a) < key(b) for non-NaN).
+// -0.0 is folded onto +0.0 so that equal scores compare equal.
+__device__ __forceinline__ uint32_t f32_order_key(float f) {
+    if (f == 0.0f) f = 0.0f;
+    uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float f32_from_order_key(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+// (score, index) packed so that a larger key is a larger score, or the same
+// score at a smaller index: unsigned 64-bit max is then the argmax with the
+// lowest-index tie rule.  Key 0 is below every real candidate.
+__device__ __forceinline__ unsigned long long pack_argmax(float v, uint32_t idx) {
+    return ((unsigned long long)f32_order_key(v) << 32) | (unsigned long long)(~idx);
+}
+
+// Candidate (v, i) beats (bv, bi): larger value, or equal value and lower index.
+__device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
+    return (v > bv) || (v == bv && i < bi);
+}
+
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+// Agent-scope atomics used by the "last workgroup finishes" reductions.
+__device__ __forceinline__ unsigned long long atomic_load_u64(unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_store_u64(unsigned long long* p, unsigned long long v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_store_u32(unsigned int* p, unsigned int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace dels

@@ -1,0 +1,289 @@
+// Skinny bf16 GEMM on gfx950 MFMA: C[M, N] = X[M, K] . W[N, K]^T with few rows.
+//
+// Used for the rank projection rank = bf16(act(bf16(h . A^T + bias)))
+// (code/kernel/dels.py:437-443) and, with three gate tiles per column tile and
+// a fused gate epilogue, for the GRU step gh = bf16(h . W_hh^T + b_hh) followed
+// by the (r, z, n) gates (code/kernel/dels.py:140-211, 359-373).
+//
+// Work decomposition: a workgroup (4 wave64s) owns a (16*WM) x (16*WN) output
+// tile and a slice of K; its waves interleave over the slice's 32-wide K
+// steps with v_mfma_f32_16x16x32_bf16 (operands loaded straight from global
+// memory in MFMA layout: lane l reads 16 bytes of row l%16 at k-group l/16).
+// Waves are summed through LDS in a fixed order.  When K is split across
+// KSPLIT workgroups, each writes its fp32 partial tile to the workspace and the
+// last one to arrive (atomic counter) sums all partials in split order -- so
+// the result is deterministic -- runs the epilogue and resets the counter.
+#include <algorithm>
+
+#include "dels_device.h"
+#include "dels_internal.h"
+
+namespace dels {
+
+enum : int { EPI_RANK = 0, EPI_GRU = 1 };
+
+struct SkinnyKArgs {
+    const uint16_t* x; int64_t ldx;     // [M, K]; NULL means an all-zero X (GRU zero state)
+    const uint16_t* w; int64_t ldw;     // [wrows, K]
+    int M, K, wrows;
+    int ncols;                          // output columns (N for rank, G for GRU)
+    int ksteps, ksplit;
+    float* partial;                     // [ksplit][m_wg][n_wg][WM*WN*256]
+    unsigned int* counters;             // [m_wg][n_wg]
+    // rank epilogue
+    const uint16_t* bias; int act;
+    uint16_t* out; int64_t ldout;
+    // GRU epilogue
+    const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
+    const int64_t* tokens; int64_t tok_stride;
+};
+
+// Column (row of W) of gate/sub-tile j for a workgroup whose first column is c0.
+template <int EPI>
+__device__ __forceinline__ int wcol(int c0, int j, int ncols) {
+    return EPI == EPI_GRU ? c0 + j * ncols : c0 + j * 16;
+}
+
+template <int WM, int WN, int EPI>
+__device__ __forceinline__ void skinny_epilogue(const SkinnyKArgs& a, const float* vals,
+                                                int m0, int c0) {
+#pragma clang fp contract(off)
+    constexpr int T = WM * WN;
+    (void)T;
+    if constexpr (EPI == EPI_RANK) {
+        // vals: [WM][WN][64 lanes][4]
+        for (int e = threadIdx.x; e < WM * WN * 256; e += blockDim.x) {
+            const int q = e & 3, lane = (e >> 2) & 63, t = e >> 8;
+            const int i = t / WN, j = t % WN;
+            const int m = m0 + i * 16 + 4 * (lane >> 4) + q;
+            const int n = c0 + j * 16 + (lane & 15);
+            if (m < a.M && n < a.ncols) {
+                float v = vals[e];
+                if (a.bias) v = v + bf16_bits_to_f32(a.bias[n]);
+                v = round_bf16(v);
+                if (a.act == 1) v = round_bf16(silu_f32(v));
+                a.out[(int64_t)m * a.ldout + n] = f32_to_bf16_bits(v);
+            }
+        }
+    } else {
+        // GRU: WN == 3 gate tiles (r, z, n) sharing one lane layout.
+        const int G = a.ncols;
+        for (int e = threadIdx.x; e < WM * 256; e += blockDim.x) {
+            const int q = e & 3, lane = (e >> 2) & 63, i = e >> 8;
+            const int b = m0 + i * 16 + 4 * (lane >> 4) + q;
+            const int g = c0 + (lane & 15);
+            if (b >= a.M || g >= G) continue;
+            const int base_e = (i * WN) * 256 + lane * 4 + q;
+            float ghr = vals[base_e], ghz = vals[base_e + 256], ghn = vals[base_e + 512];
+            if (a.bias) {
+                ghr = ghr + bf16_bits_to_f32(a.bias[g]);
+                ghz = ghz + bf16_bits_to_f32(a.bias[G + g]);
+                ghn = ghn + bf16_bits_to_f32(a.bias[2 * G + g]);
+            }
+            ghr = round_bf16(ghr);
+            ghz = round_bf16(ghz);
+            ghn = round_bf16(ghn);
+            int64_t tok = a.tokens[(int64_t)b * a.tok_stride];
+            tok = tok < 0 ? 0 : (tok >= a.table_rows ? a.table_rows - 1 : tok);
+            const uint16_t* gi = a.gi_table + tok * a.ld_gi;
+            const float gir = bf16_bits_to_f32(gi[g]);
+            const float giz = bf16_bits_to_f32(gi[G + g]);
+            const float gin = bf16_bits_to_f32(gi[2 * G + g]);
+            const float hp = a.x ? bf16_bits_to_f32(a.x[(int64_t)b * a.ldx + g]) : 0.0f;
+            const float rg = sigmoid_f32(gir + ghr);
+            const float zg = sigmoid_f32(giz + ghz);
+            const float ng = 2.0f * sigmoid_f32(2.0f * (gin + rg * ghn)) - 1.0f;
+            const float hn = (1.0f - zg) * ng + zg * hp;
+            a.out[(int64_t)b * a.ldout + g] = f32_to_bf16_bits(hn);
+        }
+    }
+}
+
+template <int WM, int WN, int EPI>
+__global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
+    constexpr int T = WM * WN;
+    __shared__ float red[4 * T * 256];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int lrow = lane & 15;        // row within a 16-row operand tile
+    const int kg = lane >> 4;          // k-group (8 elements) within a 32-wide step
+    const int m0 = blockIdx.y * (16 * WM);
+    const int c0 = blockIdx.x * (EPI == EPI_GRU ? 16 : 16 * WN);
+    const int z = blockIdx.z;
+
+    f32x4 acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (a.x != nullptr) {
+        const int sps = (a.ksteps + a.ksplit - 1) / a.ksplit;
+        const int ks0 = z * sps;
+        const int ks1 = min(a.ksteps, ks0 + sps);
+        // Row pointers, clamped in range; out-of-range rows load zeros.
+        const uint16_t* xp[WM];
+        bool xok[WM];
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+            const int m = m0 + i * 16 + lrow;
+            xok[i] = m < a.M;
+            xp[i] = a.x + (int64_t)(xok[i] ? m : 0) * a.ldx + kg * 8;
+        }
+        const uint16_t* wp[WN];
+        bool wok[WN];
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+            const int n = wcol<EPI>(c0, j, a.ncols) + lrow;
+            wok[j] = (n - (EPI == EPI_GRU ? j * a.ncols : 0)) < a.ncols && n < a.wrows;
+            wp[j] = a.w + (int64_t)(wok[j] ? n : 0) * a.ldw + kg * 8;
+        }
+        for (int s = ks0 + wave; s < ks1; s += 4) {
+            const int k = s * 32;
+            const bool kok = (k + kg * 8) < a.K;
+            bf16x8 xv[WM], wv[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) xv[i] = (kok && xok[i]) ? load_bf16x8(xp[i] + k) : zero_bf16x8();
+#pragma unroll
+            for (int j = 0; j < WN; ++j) wv[j] = (kok && wok[j]) ? load_bf16x8_nt(wp[j] + k) : zero_bf16x8();
+#pragma unroll
+            for (int i = 0; i < WM; ++i)
+#pragma unroll
+                for (int j = 0; j < WN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[i], wv[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // Sum the four waves in a fixed order through LDS.
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+            *reinterpret_cast<f32x4*>(&red[((wave * T) + i * WN + j) * 256 + lane * 4]) = acc[i][j];
+    __syncthreads();
+    for (int e = threadIdx.x; e < T * 256; e += blockDim.x) {
+        float v = red[e];
+        v += red[T * 256 + e];
+        v += red[2 * T * 256 + e];
+        v += red[3 * T * 256 + e];
+        red[e] = v;
+    }
+    __syncthreads();
+
+    if (a.ksplit == 1) {
+        skinny_epilogue<WM, WN, EPI>(a, red, m0, c0);
+        return;
+    }
+
+    // Split K: publish the partial tile, the last workgroup reduces.
+    const int tile_id = blockIdx.y * gridDim.x + blockIdx.x;
+    const int ntile = gridDim.x * gridDim.y;
+    float* mine = a.partial + ((int64_t)z * ntile + tile_id) * (T * 256);
+    for (int e = threadIdx.x; e < T * 256; e += blockDim.x) mine[e] = red[e];
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(&a.counters[tile_id], 1u);
+        s_last = (prev == (unsigned)(a.ksplit - 1));
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int e = threadIdx.x; e < T * 256; e += blockDim.x) {
+        float v = 0.f;
+        for (int zz = 0; zz < a.ksplit; ++zz)
+            v += __hip_atomic_load(a.partial + ((int64_t)zz * ntile + tile_id) * (T * 256) + e,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        red[e] = v;
+    }
+    if (threadIdx.x == 0) atomic_store_u32(&a.counters[tile_id], 0u);
+    __syncthreads();
+    skinny_epilogue<WM, WN, EPI>(a, red, m0, c0);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
+    SkinnyPlan p{};
+    if (gru) {
+        p.wn = 3;
+        p.wm = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
+    } else if (rows <= 16) {
+        p.wm = 1; p.wn = 1;
+    } else if (rows <= 32) {
+        p.wm = 2; p.wn = 2;
+    } else {
+        p.wm = 4; p.wn = 4;
+    }
+    p.m_wg = (int)cdiv(rows, 16 * p.wm);
+    p.n_wg = (int)cdiv(cols, gru ? 16 : 16 * p.wn);
+    p.ksteps = (int)cdiv(K, 32);
+    const int tiles = p.m_wg * p.n_wg;
+    // Aim for about 256 workgroups with at least one K step per wave.
+    int ks = (int)std::max<int64_t>(1, 256 / std::max(tiles, 1));
+    ks = std::min(ks, std::max(1, p.ksteps / 4));
+    p.ksplit = ks;
+    p.counter_bytes = p.ksplit > 1 ? (size_t)tiles * sizeof(unsigned int) : 0;
+    p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * tiles * p.wm * p.wn * 256 * sizeof(float) : 0;
+    return p;
+}
+
+static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t skinny_ws_bytes(const SkinnyPlan& p) {
+    return align256(p.counter_bytes) + align256(p.partial_bytes);
+}
+
+template <int WM, int WN, int EPI>
+static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, hipStream_t s) {
+    dim3 grid(p.n_wg, p.m_wg, p.ksplit);
+    hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI>), grid, dim3(256), 0, s, ka);
+    return hipGetLastError();
+}
+
+static void fill_ws(SkinnyKArgs& ka, const SkinnyPlan& p, void* ws) {
+    char* w = static_cast<char*>(ws);
+    ka.counters = p.counter_bytes ? reinterpret_cast<unsigned int*>(w) : nullptr;
+    ka.partial = p.partial_bytes ? reinterpret_cast<float*>(w + align256(p.counter_bytes)) : nullptr;
+    ka.ksteps = p.ksteps;
+    ka.ksplit = p.ksplit;
+}
+
+hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s) {
+    SkinnyKArgs ka{};
+    ka.x = a.h; ka.ldx = a.ldh;
+    ka.w = a.A; ka.ldw = a.lda;
+    ka.M = a.M; ka.K = a.d; ka.wrows = a.r; ka.ncols = a.r;
+    ka.bias = a.bias; ka.act = a.act;
+    ka.out = a.rank; ka.ldout = a.ldrank;
+    fill_ws(ka, p, ws);
+    if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, s);
+    if (p.wm == 2) return launch_skinny<2, 2, EPI_RANK>(ka, p, s);
+    return launch_skinny<4, 4, EPI_RANK>(ka, p, s);
+}
+
+hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s) {
+    SkinnyKArgs ka{};
+    ka.x = a.h_in; ka.ldx = a.ldh_in;
+    ka.w = a.w_hh; ka.ldw = a.G;
+    ka.M = a.batch; ka.K = a.G; ka.wrows = 3 * a.G; ka.ncols = a.G;
+    ka.bias = a.b_hh; ka.act = 0;
+    ka.out = a.h_out; ka.ldout = a.ldh_out;
+    ka.gi_table = a.gi_table; ka.ld_gi = a.ld_gi; ka.table_rows = a.table_rows;
+    ka.tokens = a.tokens; ka.tok_stride = a.tok_stride;
+    // A zero state needs no K loop: every workgroup runs the epilogue alone.
+    SkinnyPlan q = p;
+    if (a.h_in == nullptr) q.ksplit = 1;
+    fill_ws(ka, q, ws);
+    if (q.wm == 1) return launch_skinny<1, 3, EPI_GRU>(ka, q, s);
+    if (q.wm == 2) return launch_skinny<2, 3, EPI_GRU>(ka, q, s);
+    return launch_skinny<4, 3, EPI_GRU>(ka, q, s);
+}
+
+}  // namespace dels

@@ -1,0 +1,310 @@
+"""Torch-facing operators of the DeLS draft path, backed by the gfx950 kernels.
+
+Each operator validates its tensors, then calls the C ABI on the current HIP
+stream.  There is no CPU or eager-PyTorch fallback: a missing library or a
+non-GPU tensor raises.
+
+Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
+  * ``fused_argmax``   -- _fused_low_rank_argmax_kernel + _reduce_argmax_kernel,
+                          code/kernel/dels.py:15-138, launched at 375-423
+  * ``rank_proj``      -- F.linear(h, rank_weight, rank_bias) (+ F.silu),
+                          code/kernel/dels.py:437-443
+  * ``lowrank_argmax`` -- the two above, one draft step, code/kernel/dels.py:437-446
+  * ``gru_step``       -- _gru_cell / _fused_gru_cell_kernel with the input-table
+                          gather, code/kernel/dels.py:140-211, 359-373, 432, 461
+"""
+
+from __future__ import annotations
+
+import threading
+from typing import Iterable, Optional, Sequence, Union
+
+import torch
+
+from . import _lib
+
+_ACTS = {"identity": _lib.ACT_IDENTITY, "silu": _lib.ACT_SILU}
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+Scalars = Union[float, int, Sequence[float], torch.Tensor]
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a GPU tensor (got device {t.device}); the DeLS path has no CPU fallback")
+
+
+def _require_bf16_matrix(t: torch.Tensor, name: str, rows: Optional[int] = None,
+                         cols: Optional[int] = None) -> None:
+    _require_cuda(t, name)
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16, got {t.dtype}")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if rows is not None and t.shape[0] != rows:
+        raise ValueError(f"{name} has {t.shape[0]} rows, expected {rows}")
+    if cols is not None and t.shape[1] != cols:
+        raise ValueError(f"{name} has {t.shape[1]} columns, expected {cols}")
+    if t.shape[1] > 1 and t.stride(1) != 1:
+        raise ValueError(f"{name} must have unit column stride")
+
+
+class _Workspaces:
+    """Zero-initialised scratch buffers, one per (device, stream), grown on demand.
+
+    The kernels return every workspace byte to zero before they finish, so a
+    buffer is cleared only when it is (re)allocated.  Calls on one stream are
+    ordered and may share it; each stream gets its own buffer.
+    """
+
+    def __init__(self):
+        self._bufs = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, nbytes: int) -> torch.Tensor:
+        key = (device.index, _stream_ptr(device))
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                size = max(nbytes, 1 << 16)
+                size = (size + 255) // 256 * 256
+                buf = torch.zeros(size, dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_WORKSPACES = _Workspaces()
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The shared zero-initialised workspace for ``device`` and its current stream."""
+    return _WORKSPACES.get(device, nbytes)
+
+
+def new_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """A private zero-initialised workspace (e.g. for a captured graph)."""
+    size = (max(int(nbytes), 256) + 255) // 256 * 256
+    return torch.zeros(size, dtype=torch.uint8, device=device)
+
+
+def _rows_param(x: Scalars, M: int, device: torch.device, name: str) -> tuple[torch.Tensor, int]:
+    """alpha/beta as a device fp32 array and a per-row stride (0 = broadcast)."""
+    if isinstance(x, torch.Tensor):
+        t = x
+        if t.device.type != "cuda":
+            t = t.to(device)
+        if t.dtype != torch.float32:
+            t = t.float()
+        t = t.reshape(-1)
+        if t.numel() == 1:
+            return t.contiguous(), 0
+        if t.numel() != M:
+            raise ValueError(f"{name} has {t.numel()} entries, expected 1 or {M}")
+        return t, t.stride(0)
+    if isinstance(x, (float, int)):
+        return torch.full((1,), float(x), dtype=torch.float32, device=device), 0
+    vals = [float(v) for v in x]
+    if len(vals) == 1:
+        return torch.tensor(vals, dtype=torch.float32, device=device), 0
+    if len(vals) != M:
+        raise ValueError(f"{name} has {len(vals)} entries, expected 1 or {M}")
+    return torch.tensor(vals, dtype=torch.float32, device=device), 1
+
+
+def _base_view(base: torch.Tensor, M: int, V: int) -> torch.Tensor:
+    _require_cuda(base, "base_logits")
+    if base.dtype not in _DTYPES:
+        raise TypeError(f"base_logits dtype {base.dtype} not supported (float32, bfloat16, float16)")
+    if base.dim() == 3 and base.shape[1] == 1:
+        base = base[:, 0, :]
+    if base.dim() != 2 or tuple(base.shape) != (M, V):
+        raise ValueError(f"base_logits must be [{M}, {V}], got {tuple(base.shape)}")
+    if V > 1 and base.stride(1) != 1:
+        raise ValueError("base_logits must have unit stride along the vocabulary")
+    return base
+
+
+def _prior_view(prior: Optional[torch.Tensor], V: int) -> Optional[torch.Tensor]:
+    if prior is None:
+        return None
+    _require_cuda(prior, "baseline_logits")
+    if prior.dtype not in _DTYPES:
+        raise TypeError(f"baseline_logits dtype {prior.dtype} not supported")
+    if prior.numel() != V:
+        raise ValueError(f"DeLS graph baseline vocab size mismatch: baseline={prior.numel()}, vocab={V}.")
+    prior = prior.reshape(-1)
+    if not prior.is_contiguous():
+        prior = prior.contiguous()
+    return prior
+
+
+def _outputs(out_ids, out_score, M, dev):
+    """Output buffers (allocated if not given) and their shared row stride."""
+    if out_ids is None:
+        out_ids = torch.empty(M, dtype=torch.int64, device=dev)
+    if out_score is None:
+        out_score = torch.empty(M, dtype=torch.float32, device=dev)
+    if out_ids.dtype != torch.int64 or out_score.dtype != torch.float32:
+        raise TypeError("out_ids must be int64 and out_score float32")
+    if out_ids.numel() != M or out_score.numel() != M:
+        raise ValueError(f"output buffers must hold {M} rows")
+    ld = out_ids.stride(-1) if M > 1 else 1
+    if M > 1 and out_score.stride(-1) != ld:
+        raise ValueError("out_ids and out_score must share one row stride")
+    return out_ids, out_score, ld
+
+
+def rank_proj(h: torch.Tensor, rank_weight: torch.Tensor, rank_bias: Optional[torch.Tensor] = None,
+              act: str = "identity", *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``rank = act(F.linear(h, rank_weight, rank_bias))`` in bf16 (code/kernel/dels.py:437-443)."""
+    if act not in _ACTS:
+        raise ValueError(f"Unsupported DeLS rank_activation={act!r}.")
+    if h.dim() == 1:
+        h = h.unsqueeze(0)
+    M, d = h.shape
+    _require_bf16_matrix(h, "h", cols=d)
+    _require_bf16_matrix(rank_weight, "rank_weight", cols=d)
+    r = rank_weight.shape[0]
+    if rank_bias is not None:
+        _require_cuda(rank_bias, "rank_bias")
+        if rank_bias.dtype != torch.bfloat16 or rank_bias.numel() != r:
+            raise ValueError("rank_bias must be a bfloat16 vector of length r")
+        rank_bias = rank_bias.contiguous()
+    if out is None:
+        out = torch.empty(M, r, dtype=torch.bfloat16, device=h.device)
+    else:
+        _require_bf16_matrix(out, "out", rows=M, cols=r)
+    lib = _lib.load()
+    nbytes = lib.dels_rank_proj_ws_bytes(M, d, r)
+    ws = workspace(h.device, nbytes)
+    _lib.check(lib.dels_rank_proj(h.data_ptr(), h.stride(0), rank_weight.data_ptr(), rank_weight.stride(0),
+                                  rank_bias.data_ptr() if rank_bias is not None else None, _ACTS[act],
+                                  M, d, r, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(),
+                                  _stream_ptr(h.device)), "dels_rank_proj")
+    return out
+
+
+def fused_argmax(rank: torch.Tensor, lm_head_weight: torch.Tensor, base_logits: torch.Tensor,
+                 baseline_logits: Optional[torch.Tensor] = None, alpha: Scalars = 1.0, beta: Scalars = 0.0,
+                 *, out_ids: Optional[torch.Tensor] = None,
+                 out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row argmax of ``rank.B^T * alpha + base - beta * prior`` (code/kernel/dels.py:15-138).
+
+    ``rank`` [M, r] bf16; ``lm_head_weight`` B [V, r] bf16; ``base_logits`` an
+    [M, V] view (any row stride) in fp32/bf16/fp16; ``baseline_logits`` the
+    prior [V] (or None); ``alpha``/``beta`` scalars, length-M sequences or
+    device tensors.  Returns ``(ids int64[M], score fp32[M])``.
+    """
+    if rank.dim() == 1:
+        rank = rank.unsqueeze(0)
+    M, r = rank.shape
+    _require_bf16_matrix(rank, "rank", cols=r)
+    _require_bf16_matrix(lm_head_weight, "lm_head_weight", cols=r)
+    V = lm_head_weight.shape[0]
+    base = _base_view(base_logits, M, V)
+    prior = _prior_view(baseline_logits, V)
+    dev = rank.device
+    a, a_s = _rows_param(alpha, M, dev, "alpha")
+    b, b_s = _rows_param(beta, M, dev, "beta")
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_fused_argmax_ws_bytes(M, r, V))
+    _lib.check(lib.dels_fused_argmax(
+        rank.data_ptr(), rank.stride(0), lm_head_weight.data_ptr(), lm_head_weight.stride(0),
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
+        prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
+        a.data_ptr(), a_s, b.data_ptr(), b_s, M, r, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_fused_argmax")
+    return out_ids, out_score
+
+
+def lowrank_argmax(h: torch.Tensor, rank_weight: torch.Tensor, lm_head_weight: torch.Tensor,
+                   base_logits: torch.Tensor, baseline_logits: Optional[torch.Tensor] = None,
+                   alpha: Scalars = 1.0, beta: Scalars = 0.0, act: str = "identity",
+                   rank_bias: Optional[torch.Tensor] = None, *, out_ids: Optional[torch.Tensor] = None,
+                   out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One DeLS draft step: rank projection of ``h`` then the fused argmax.
+
+    ``h`` [M, d] bf16, ``rank_weight`` A [r, d] bf16, ``lm_head_weight`` B [V, r]
+    bf16 (code/kernel/dels.py:437-446).  Returns ``(ids int64[M], score fp32[M])``.
+    """
+    if act not in _ACTS:
+        raise ValueError(f"Unsupported DeLS rank_activation={act!r}.")
+    if h.dim() == 1:
+        h = h.unsqueeze(0)
+    M, d = h.shape
+    _require_bf16_matrix(h, "h", cols=d)
+    _require_bf16_matrix(rank_weight, "rank_weight", cols=d)
+    r = rank_weight.shape[0]
+    _require_bf16_matrix(lm_head_weight, "lm_head_weight", cols=r)
+    V = lm_head_weight.shape[0]
+    base = _base_view(base_logits, M, V)
+    prior = _prior_view(baseline_logits, V)
+    if rank_bias is not None:
+        _require_cuda(rank_bias, "rank_bias")
+        if rank_bias.dtype != torch.bfloat16 or rank_bias.numel() != r:
+            raise ValueError("rank_bias must be a bfloat16 vector of length r")
+        rank_bias = rank_bias.contiguous()
+    dev = h.device
+    a, a_s = _rows_param(alpha, M, dev, "alpha")
+    b, b_s = _rows_param(beta, M, dev, "beta")
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_lowrank_argmax_ws_bytes(M, d, r, V))
+    _lib.check(lib.dels_lowrank_argmax(
+        h.data_ptr(), h.stride(0), rank_weight.data_ptr(), rank_weight.stride(0),
+        rank_bias.data_ptr() if rank_bias is not None else None, _ACTS[act],
+        lm_head_weight.data_ptr(), lm_head_weight.stride(0),
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
+        prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
+        a.data_ptr(), a_s, b.data_ptr(), b_s, M, d, r, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_lowrank_argmax")
+    return out_ids, out_score
+
+
+def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.Tensor],
+             w_hh: torch.Tensor, b_hh: Optional[torch.Tensor] = None, *,
+             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``h_out = GRUCell(gi_table[tokens], h_in)`` with bf16 state (code/kernel/dels.py:359-373).
+
+    ``gi_table`` [rows, 3G] bf16 is ``F.linear(E, W_ih, b_ih)``; ``tokens`` [B]
+    int64 (a strided view is fine); ``h_in`` [B, G] bf16 or None for zeros;
+    ``w_hh`` [3G, G] bf16; ``b_hh`` [3G] bf16 or None.
+    """
+    _require_cuda(tokens, "tokens")
+    if tokens.dtype != torch.int64:
+        raise TypeError("tokens must be int64")
+    tokens = tokens.reshape(-1) if tokens.dim() != 1 else tokens
+    nb = tokens.numel()
+    G = w_hh.shape[1]
+    _require_bf16_matrix(w_hh, "w_hh", rows=3 * G, cols=G)
+    if not w_hh.is_contiguous():
+        raise ValueError("w_hh must be contiguous")
+    _require_bf16_matrix(gi_table, "gi_table", cols=3 * G)
+    if h_in is not None:
+        _require_bf16_matrix(h_in, "h_in", rows=nb, cols=G)
+    if b_hh is not None:
+        if b_hh.dtype != torch.bfloat16 or b_hh.numel() != 3 * G:
+            raise ValueError("b_hh must be a bfloat16 vector of length 3G")
+        b_hh = b_hh.contiguous()
+    dev = w_hh.device
+    if out is None:
+        out = torch.empty(nb, G, dtype=torch.bfloat16, device=dev)
+    else:
+        _require_bf16_matrix(out, "out", rows=nb, cols=G)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_gru_step_ws_bytes(nb, G))
+    _lib.check(lib.dels_gru_step(
+        gi_table.data_ptr(), gi_table.stride(0), gi_table.shape[0], tokens.data_ptr(), tokens.stride(0),
+        h_in.data_ptr() if h_in is not None else None, h_in.stride(0) if h_in is not None else G,
+        w_hh.data_ptr(), b_hh.data_ptr() if b_hh is not None else None, nb, G,
+        out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_gru_step")
+    return out

@@ -1,0 +1,188 @@
+/*
+ * dels.h -- C ABI of the MI355X (gfx950) draft-token selection path of DeLS-Spec.
+ *
+ * The path: for each draft row m,
+ *     rank_m  = bf16(act(bf16(h_m . A^T + bias)))
+ *     s[m, v] = fp32(rank_m . B[v]) * alpha_m + base[m, v] - beta_m * prior[v]
+ *     id_m    = lowest v attaining max_v s[m, v];  score_m = s[m, id_m]
+ * without writing the [M, V] logits to memory, plus the GRU local-head step
+ * that feeds the next draft position and a hipGraph of the whole suffix
+ * rollout.  Paths cited below are relative to the dt-3t/DeLS-Spec repository.
+ *
+ * Conventions
+ *  - Every pointer argument except `ws` scratch bookkeeping is a device
+ *    pointer owned by the caller; the library never allocates, frees or keeps
+ *    a pointer past the call (graph handles excepted, see dels_graph_*).
+ *  - Matrices are row-major with a leading dimension (`ld*`, in elements) and
+ *    unit column stride.  bf16 operands (h, A, B, rank, GRU weights) must be
+ *    16-byte aligned with ld % 8 == 0.
+ *  - `stream` is a hipStream_t (pass torch.cuda.current_stream().cuda_stream);
+ *    all work is stream-ordered, nothing synchronises the host, so every entry
+ *    point may be captured into a hipGraph.
+ *  - Workspace (`ws`): caller-owned device memory of at least the size the
+ *    matching *_ws_bytes() function returns, 256-byte aligned, zero-filled
+ *    once before first use (dels_workspace_init).  Kernels return it to all
+ *    zeros before they finish.  Calls that share one workspace must not
+ *    overlap in time (same stream is fine).
+ *  - Return value: DELS_OK (0) or a negative DELS_ERR_* code; no exception
+ *    crosses the ABI.  dels_strerror() names a code, dels_last_error() gives
+ *    the detail of the calling thread's last failure.
+ */
+#ifndef DELS_H
+#define DELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DELS_ABI_VERSION 1
+
+/* status codes */
+#define DELS_OK 0
+#define DELS_ERR_INVALID_ARGUMENT (-1)
+#define DELS_ERR_UNSUPPORTED (-2)
+#define DELS_ERR_ALIGNMENT (-3)
+#define DELS_ERR_WORKSPACE (-4)
+#define DELS_ERR_HIP (-5)
+
+/* element types of base logits / prior */
+#define DELS_DTYPE_F32 0
+#define DELS_DTYPE_BF16 1
+#define DELS_DTYPE_F16 2
+
+/* rank activations (code/dels.py:14) */
+#define DELS_ACT_IDENTITY 0
+#define DELS_ACT_SILU 1
+
+int dels_abi_version(void);
+const char* dels_strerror(int status);
+const char* dels_last_error(void);
+
+/* Zero-fill a workspace on `stream` with a fill kernel (capture-safe). */
+int dels_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Rank projection rank = bf16(act(bf16(h . A^T + bias)))  [M, r] bf16.
+ * Replaces F.linear(h_state, rank_weight, rank_bias) + F.silu in
+ * DeLSGraphRunner._forward_impl (code/kernel/dels.py:437-443) and
+ * DeLSLocalHead.logits_from_hidden's rank_proj (code/dels.py:334-339).
+ *   h [M, d] bf16 (ldh), A [r, d] bf16 (lda), bias [r] bf16 or NULL.
+ */
+size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r);
+int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda,
+                   const void* bias, int act, int64_t M, int64_t d, int64_t r,
+                   void* rank, int64_t ldrank, void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Fused low-rank LM-head combine + vocabulary argmax, given rank.
+ * Replaces _fused_low_rank_argmax_kernel + _reduce_argmax_kernel as launched
+ * by DeLSGraphRunner._argmax_step_triton (code/kernel/dels.py:15-138, 375-423).
+ *   rank  [M, r] bf16 (ldrank)          B     [V, r] bf16 (ldb)
+ *   base  [M, V] base_dtype (ldbase)    prior [V] prior_dtype, or NULL
+ *   alpha/beta: fp32 device arrays read at alpha[m*alpha_stride] (stride 0
+ *   broadcasts one value).  The prior term is applied to row m only when
+ *   prior != NULL and beta_m != 0 (code/kernel/dels.py:81-88, 382).
+ *   out_ids[m*ld_out] int64, out_score[m*ld_out] fp32 (out_score may be NULL).
+ * Ties go to the lowest vocabulary index; a row whose scores are all -inf
+ * returns id 0 with score -inf.
+ */
+size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V);
+int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb,
+                      const void* base, int64_t ldbase, int base_dtype,
+                      const void* prior, int prior_dtype,
+                      const float* alpha, int64_t alpha_stride,
+                      const float* beta, int64_t beta_stride,
+                      int64_t M, int64_t r, int64_t V,
+                      int64_t* out_ids, float* out_score, int64_t ld_out,
+                      void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Rank projection followed by the fused argmax: one draft step of the
+ * reference's Triton path (code/kernel/dels.py:437-446).  The bf16 rank
+ * lives in the workspace.
+ */
+size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V);
+int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda,
+                        const void* bias, int act,
+                        const void* B, int64_t ldb,
+                        const void* base, int64_t ldbase, int base_dtype,
+                        const void* prior, int prior_dtype,
+                        const float* alpha, int64_t alpha_stride,
+                        const float* beta, int64_t beta_stride,
+                        int64_t M, int64_t d, int64_t r, int64_t V,
+                        int64_t* out_ids, float* out_score, int64_t ld_out,
+                        void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * One GRU local-head step h_out = GRUCell(gi_table[tokens], h_in).
+ * Replaces DeLSGraphRunner._gru_cell / _fused_gru_cell_kernel plus the
+ * input-table gather (code/kernel/dels.py:140-211, 359-373, 432, 461).
+ *   gi_table [table_rows, 3G] bf16 (ld_gi) = F.linear(E, W_ih, b_ih);
+ *   tokens[b*tok_stride] int64 (clamped to [0, table_rows) before use);
+ *   h_in [batch, G] bf16 (ldh_in) or NULL for a zero state;
+ *   w_hh [3G, G] bf16, b_hh [3G] bf16 or NULL; h_out [batch, G] bf16.
+ * Gate order (r, z, n) as torch.nn.GRU; gh = bf16(h . W_hh^T + b_hh).
+ */
+size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G);
+int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows,
+                  const int64_t* tokens, int64_t tok_stride,
+                  const void* h_in, int64_t ldh_in,
+                  const void* w_hh, const void* b_hh,
+                  int64_t batch, int64_t G,
+                  void* h_out, int64_t ldh_out,
+                  void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * The DeLS suffix rollout of DeLSGraphRunner._forward_impl
+ * (code/kernel/dels.py:425-467): h = GRU(gi_table[prefix], 0); then for each
+ * step s: rank projection, fused argmax against base[:, s, :] with
+ * alpha[s]/beta[s], out_ids[:, s] = id, and a GRU step on that id unless s is
+ * the last step.  All buffers are caller-owned device memory.
+ */
+typedef struct dels_rollout {
+    const void* gi_table;   /* [table_rows, 3G] bf16 */
+    int64_t ld_gi;
+    int64_t table_rows;
+    const void* w_hh;       /* [3G, G] bf16 */
+    const void* b_hh;       /* [3G] bf16 or NULL */
+    const void* rank_w;     /* [r, G] bf16 */
+    const void* rank_b;     /* [r] bf16 or NULL */
+    int act;                /* DELS_ACT_* */
+    const void* lm_w;       /* [V, r] bf16 */
+    const void* prior;      /* [V] or NULL */
+    int prior_dtype;
+    const float* alpha;     /* [steps] fp32 */
+    const float* beta;      /* [steps] fp32 */
+    int64_t batch, steps, G, r, V;
+    const int64_t* prefix_ids; /* [batch] int64 */
+    const void* base;       /* [batch, steps, V] */
+    int base_dtype;
+    int64_t* out_ids;       /* [batch, steps] int64 */
+    float* out_scores;      /* [batch, steps] fp32 or NULL */
+    void* h_a;              /* [batch, G] bf16 state buffers (ping-pong) */
+    void* h_b;
+    void* rank;             /* [batch, r] bf16 */
+    void* ws;
+    size_t ws_bytes;
+} dels_rollout;
+
+size_t dels_rollout_ws_bytes(int64_t batch, int64_t G, int64_t r, int64_t V);
+int dels_rollout_enqueue(const dels_rollout* p, void* stream);
+
+/*
+ * hipGraph of the rollout: replaces the torch.cuda.CUDAGraph capture and
+ * replay of DeLSGraphRunner (code/kernel/dels.py:320-329, 477).  The graph
+ * bakes in the pointers of `p`; the handle owns only the graph objects.
+ */
+int dels_graph_create(const dels_rollout* p, void** graph_out);
+int dels_graph_launch(void* graph, void* stream);
+int dels_graph_destroy(void* graph);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELS_H */

@@ -1,0 +1,368 @@
+"""GPU parity: the gfx950 kernels (through the C ABI) against the CPU oracle.
+
+Parity rule: ids bit-exact wherever the oracle's top-2 margin exceeds 1e-3
+relative; elsewhere the device's pick must be a near-maximum under the oracle;
+the winning score within 1e-2 absolute.  bf16 outputs (rank, GRU state) may
+differ from the oracle by one bf16 ulp only where fp32 accumulation order
+straddles a rounding boundary.
+"""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def from_bits(b, dev):
+    return torch.from_numpy(np.ascontiguousarray(b).astype(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def assert_parity(ids, score, rank_np, B_np, base_np, prior_np, alpha, beta, ref=None):
+    ids = ids.cpu().numpy()
+    score = score.cpu().numpy()
+    if ref is None:
+        ref = oracle.fused_argmax(rank_np, B_np, base_np, prior_np, alpha, beta)
+    rid, rsc, rsec = ref
+    pick = oracle.score_at(rank_np, B_np, base_np, prior_np, alpha, beta, np.clip(ids, 0, B_np.shape[0] - 1))
+    res = oracle.check_parity(ids, score, rid, rsc, rsec, pick)
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["score_bad"] == 0, res
+    assert res["unpinned_far_pick"] == 0, res
+    return res
+
+
+def bf16_ulps(a, b):
+    """Distance in bf16 ulps between two arrays of bf16-representable fp32 values."""
+    ia = oracle.f32_to_bf16_bits(a).astype(np.int32)
+    ib = oracle.f32_to_bf16_bits(b).astype(np.int32)
+    # map sign-magnitude to a monotone integer line
+    ia = np.where(ia & 0x8000, -(ia & 0x7FFF), ia)
+    ib = np.where(ib & 0x8000, -(ib & 0x7FFF), ib)
+    return np.abs(ia - ib)
+
+
+# ------------------------------------------------------------------ fused argmax
+
+ARGMAX_CASES = [
+    # M, r, V, base dtype, prior dtype (None: no prior), per-row alpha/beta
+    (1, 64, 1000, torch.float32, torch.float32, True),
+    (4, 8, 17, torch.bfloat16, torch.bfloat16, True),
+    (3, 96, 4099, torch.bfloat16, None, True),
+    (16, 256, 151936, torch.float32, torch.float32, False),
+    (16, 512, 151936, torch.float32, torch.float32, True),
+    (17, 128, 5000, torch.float16, torch.float32, True),
+    (40, 512, 20011, torch.bfloat16, torch.bfloat16, True),
+]
+
+
+@pytest.mark.parametrize("M,r,V,bdt,pdt,per_row", ARGMAX_CASES)
+def test_fused_argmax_random(pkg, dev, M, r, V, bdt, pdt, per_row):
+    print(f"case fused_argmax M={M} r={r} V={V} base={bdt} prior={pdt}", flush=True)
+    x = pkg.synth.lowrank_inputs(M, 64, r, V, base_dtype=bdt, prior_dtype=pdt or torch.float32,
+                                 per_position=per_row, seed=M * 7 + r)
+    rank = (torch.randn(M, r, generator=torch.Generator().manual_seed(M + V)) * 2).to(torch.bfloat16)
+    prior = x.prior if pdt is not None else None
+    ids, score = pkg.fused_argmax(rank.to(dev), x.B.to(dev), x.base.to(dev),
+                                  None if prior is None else prior.to(dev), x.alpha.to(dev), x.beta.to(dev))
+    torch.cuda.synchronize()
+    assert_parity(ids, score, f(rank), f(x.B), f(x.base), None if prior is None else f(prior),
+                  f(x.alpha), f(x.beta))
+
+
+def test_fused_argmax_strided_base_and_outputs(pkg, dev):
+    g = torch.Generator().manual_seed(5)
+    nb, steps, V, r = 3, 5, 3001, 64
+    base3 = (torch.randn(nb, steps, V, generator=g) * 3).to(torch.bfloat16)
+    B = (torch.randn(V, r, generator=g) * 0.05).to(torch.bfloat16)
+    rank = torch.randn(nb, r, generator=g).to(torch.bfloat16)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0).to(torch.bfloat16)
+    out_ids = torch.full((nb, steps), -1, dtype=torch.int64, device=dev)
+    out_sc = torch.zeros(nb, steps, dtype=torch.float32, device=dev)
+    base_d = base3.to(dev)
+    for s in range(steps):
+        pkg.fused_argmax(rank.to(dev), B.to(dev), base_d[:, s, :], prior.to(dev), 0.3, 0.2,
+                         out_ids=out_ids[:, s], out_score=out_sc[:, s])
+    torch.cuda.synchronize()
+    for s in range(steps):
+        assert_parity(out_ids[:, s], out_sc[:, s], f(rank), f(B), f(base3[:, s, :]), f(prior), 0.3, 0.2)
+
+
+def test_fused_argmax_ties_inf_and_skipped_prior(pkg, dev):
+    g = torch.Generator().manual_seed(6)
+    M, r, V = 6, 128, 151936
+    B = (torch.randn(V, r, generator=g) * 0.02).to(torch.bfloat16)
+    rank = torch.randn(M, r, generator=g).to(torch.bfloat16)
+    base = torch.randn(M, V, generator=g) * 3
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0)
+    alpha = torch.full((M,), 0.3)
+    beta = torch.full((M,), 0.4)
+    planted = [5, 77777, 150000, V - 1]
+    B[planted] = 0
+    prior[planted] = 0
+    base[0, 5] = base[0, 150000] = 100.0      # tie across far-apart workgroups -> 5
+    base[1, V - 1] = 100.0                    # last vocabulary entry
+    base[2, :] = float("-inf")                # all -inf -> id 0, score -inf
+    alpha[2] = 0.0
+    base[3, 77777] = base[3, 150000] = 100.0  # tie -> 77777
+    prior_inf = prior.clone()
+    prior_inf[1234] = float("inf")            # poisons only rows whose beta is used
+    beta[4] = 0.0
+    ids, score = pkg.fused_argmax(rank.to(dev), B.to(dev), base.to(dev), prior_inf.to(dev), alpha.to(dev),
+                                  beta.to(dev))
+    ids, score = ids.cpu(), score.cpu()
+    assert ids[0].item() == 5 and ids[1].item() == V - 1 and ids[3].item() == 77777
+    assert ids[2].item() == 0 and score[2].item() == float("-inf")
+    assert score[0].item() == 100.0
+    ref = oracle.fused_argmax(f(rank), f(B), f(base), f(prior_inf), f(alpha), f(beta))
+    assert ids[4].item() == ref[0][4] and abs(score[4].item() - ref[1][4]) < 1e-2 and np.isfinite(score[4].item())
+
+
+def test_fused_argmax_repeated_calls_reset_workspace(pkg, dev):
+    x = pkg.synth.lowrank_inputs(16, 64, 256, 30000, seed=9)
+    rank = torch.randn(16, 256, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16).to(dev)
+    args = (x.B.to(dev), x.base.to(dev), x.prior.to(dev), x.alpha.to(dev), x.beta.to(dev))
+    first = pkg.fused_argmax(rank, *args)
+    first = (first[0].clone(), first[1].clone())
+    for _ in range(4):
+        again = pkg.fused_argmax(rank, *args)
+        torch.testing.assert_close(again[0], first[0], rtol=0, atol=0)
+        torch.testing.assert_close(again[1], first[1], rtol=0, atol=0)
+    # a smaller problem right after a larger one on the same workspace
+    small = pkg.fused_argmax(rank[:3], x.B[:100].to(dev), x.base[:3, :100].to(dev), x.prior[:100].to(dev),
+                             x.alpha[:3].to(dev), x.beta[:3].to(dev))
+    torch.cuda.synchronize()
+    assert_parity(small[0], small[1], f(rank[:3]), f(x.B[:100]), f(x.base[:3, :100]), f(x.prior[:100]),
+                  f(x.alpha[:3]), f(x.beta[:3]))
+
+
+def test_fused_argmax_vocab_of_one_and_empty_batch(pkg, dev):
+    rank = torch.ones(2, 8, dtype=torch.bfloat16, device=dev)
+    B = torch.ones(1, 8, dtype=torch.bfloat16, device=dev)
+    base = torch.tensor([[1.0], [-2.0]], device=dev)
+    ids, score = pkg.fused_argmax(rank, B, base, None, 0.5, 0.0)
+    assert ids.tolist() == [0, 0] and score.tolist() == [5.0, 2.0]
+    ids, score = pkg.fused_argmax(rank[:0], B, base[:0], None, 0.5, 0.0)
+    assert ids.numel() == 0
+
+
+# ------------------------------------------------------------------ rank projection
+
+@pytest.mark.parametrize("M,d,r,act,bias", [(16, 4096, 512, "identity", False), (16, 2560, 256, "silu", False),
+                                            (5, 1024, 64, "silu", True), (40, 512, 136, "identity", True),
+                                            (512, 4096, 512, "silu", False)])
+def test_rank_proj(pkg, dev, M, d, r, act, bias):
+    print(f"case rank_proj M={M} d={d} r={r} act={act} bias={bias}", flush=True)
+    g = torch.Generator().manual_seed(M + d + r)
+    h = torch.randn(M, d, generator=g).to(torch.bfloat16)
+    A = (torch.randn(r, d, generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(r, generator=g) * 0.1).to(torch.bfloat16) if bias else None
+    got = f(pkg.rank_proj(h.to(dev), A.to(dev), None if b is None else b.to(dev), act))
+    ref = oracle.rank_proj(f(h), f(A), None if b is None else f(b), act)
+    ulps = bf16_ulps(got, ref)
+    assert ulps.max() <= 1
+    assert (ulps > 0).mean() < 2e-3
+
+
+# ------------------------------------------------------------------ end-to-end draft step
+
+@pytest.mark.parametrize("name", ["qwen3_4b_m16", "qwen3_8b_m16"])
+def test_lowrank_argmax_configs(pkg, dev, name):
+    print(f"case lowrank_argmax {name}", flush=True)
+    x = pkg.synth.config_inputs(name)
+    xd = x.to(dev)
+    ids, score = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+    torch.cuda.synchronize()
+    rank = oracle.rank_proj(f(x.h), f(x.A), None, x.act)
+    assert_parity(ids, score, rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
+
+
+def test_lowrank_argmax_m512_rows(pkg, dev):
+    x = pkg.synth.config_inputs("qwen3_8b_m512")
+    xd = x.to(dev)
+    ids, score = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+    torch.cuda.synchronize()
+    rows = np.r_[0:24, 250:262, 488:512]           # a sample of the 512 rows (oracle cost)
+    rank = oracle.rank_proj(f(x.h[rows]), f(x.A), None, x.act)
+    assert_parity(ids[rows], score[rows], rank, f(x.B), f(x.base[rows]), f(x.prior), f(x.alpha[rows]),
+                  f(x.beta[rows]))
+
+
+# ------------------------------------------------------------------ golden fixtures
+
+@pytest.mark.parametrize("name", ["argmax_ragged_silu_f32.npz", "argmax_bf16_identity.npz",
+                                  "argmax_noprior_m20.npz"])
+def test_golden_argmax(pkg, dev, name):
+    z = np.load(os.path.join(GOLDEN, name))
+    act = str(z["act"])
+    base = torch.from_numpy(z["base"])
+    prior = torch.from_numpy(z["prior"])
+    if bool(z["base_bf16"]):
+        base, prior = base.to(torch.bfloat16), prior.to(torch.bfloat16)
+    prior_d = prior.to(dev) if bool(z["with_prior"]) else None
+    ids, score = pkg.lowrank_argmax(from_bits(z["h"], dev), from_bits(z["A"], dev), from_bits(z["B"], dev),
+                                    base.to(dev), prior_d, torch.from_numpy(z["alpha"]).to(dev),
+                                    torch.from_numpy(z["beta"]).to(dev), act=act)
+    torch.cuda.synchronize()
+    rank = oracle.bf16_bits_to_f32(z["rank"]).reshape(z["rank"].shape)
+    B = oracle.bf16_bits_to_f32(z["B"]).reshape(z["B"].shape)
+    assert_parity(ids, score, rank, B, f(base), f(prior) if prior_d is not None else None, z["alpha"], z["beta"],
+                  ref=(z["ids"], z["score"], z["second"]))
+
+
+@pytest.mark.parametrize("name", ["gru_b4_g32.npz", "gru_b17_g48_bias.npz"])
+def test_golden_gru(pkg, dev, name):
+    z = np.load(os.path.join(GOLDEN, name))
+    b_hh = from_bits(z["b_hh"], dev) if z["b_hh"].size else None
+    tok = torch.from_numpy(z["tokens"]).to(dev)
+    for h_key, out_key in (("h", "h_out"), (None, "h_out_zero")):
+        h = from_bits(z[h_key], dev) if h_key else None
+        out = pkg.gru_step(from_bits(z["table"], dev), tok, h, from_bits(z["W_hh"], dev), b_hh)
+        torch.cuda.synchronize()
+        ref = oracle.bf16_bits_to_f32(z[out_key]).reshape(z[out_key].shape)
+        ulps = bf16_ulps(f(out), ref)
+        assert ulps.max() <= 1 and (ulps > 0).mean() < 0.02, (name, out_key, ulps.max(), (ulps > 0).mean())
+
+
+# ------------------------------------------------------------------ GRU step
+
+@pytest.mark.parametrize("nb,G", [(1, 1024), (8, 1024), (33, 256), (64, 128)])
+def test_gru_step(pkg, dev, nb, G):
+    print(f"case gru_step nb={nb} G={G}", flush=True)
+    g = torch.Generator().manual_seed(nb * G)
+    rows = 300
+    table = torch.randn(rows, 3 * G, generator=g).to(torch.bfloat16)
+    w_hh = (torch.randn(3 * G, G, generator=g) * 0.02).to(torch.bfloat16)
+    b_hh = (torch.randn(3 * G, generator=g) * 0.1).to(torch.bfloat16)
+    h = torch.randn(nb, G, generator=g).to(torch.bfloat16)
+    tok_full = torch.randint(0, rows, (nb, 4), generator=g)
+    tok = tok_full[:, 2]                       # a strided column of token ids
+    out = pkg.gru_step(table.to(dev), tok_full.to(dev)[:, 2], h.to(dev), w_hh.to(dev), b_hh.to(dev))
+    torch.cuda.synchronize()
+    ref = oracle.gru_cell(f(table)[tok.numpy()], f(h), f(w_hh), f(b_hh))
+    ulps = bf16_ulps(f(out), ref)
+    assert ulps.max() <= 1 and (ulps > 0).mean() < 0.01
+
+
+# ------------------------------------------------------------------ rollout runner
+
+class _Head(torch.nn.Module):
+    """Duck-typed local head: the attributes DeLSGraphRunner reads."""
+
+    def __init__(self, V, E, G, r, act, rank_bias, seed, std=0.2):
+        super().__init__()
+        g = torch.Generator().manual_seed(seed)
+        self.embed_tokens = torch.nn.Embedding(V, E)
+        self.prefix_gru = torch.nn.GRU(E, G, num_layers=1, batch_first=True, bias=False)
+        self.rank_proj = torch.nn.Linear(G, r, bias=rank_bias)
+        self.low_rank_lm_head = torch.nn.Linear(r, V, bias=False)
+        self.rank_activation = act
+        with torch.no_grad():
+            self.embed_tokens.weight.copy_(torch.randn(V, E, generator=g))
+            self.prefix_gru.weight_ih_l0.copy_(torch.randn(3 * G, E, generator=g) * std)
+            self.prefix_gru.weight_hh_l0.copy_(torch.randn(3 * G, G, generator=g) * std)
+            self.rank_proj.weight.copy_(torch.randn(r, G, generator=g) * std)
+            if rank_bias:
+                self.rank_proj.bias.copy_(torch.randn(r, generator=g) * 0.1)
+            self.low_rank_lm_head.weight.copy_(torch.randn(V, r, generator=g) * std)
+        self.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("nb,steps,V,E,G,r,act,rank_bias,with_prior,std",
+                         [(1, 14, 5003, 32, 64, 64, "silu", False, True, 0.2),
+                          (3, 6, 2000, 16, 128, 96, "identity", True, True, 0.2),
+                          (8, 4, 151936, 64, 1024, 256, "silu", False, False, 0.02)])
+def test_graph_runner_rollout(pkg, dev, nb, steps, V, E, G, r, act, rank_bias, with_prior, std):
+    print(f"case runner nb={nb} steps={steps} V={V} G={G} r={r}", flush=True)
+    head = _Head(V, E, G, r, act, rank_bias, seed=nb + V, std=std).to(dev)
+    g = torch.Generator().manual_seed(11)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0) if with_prior else None
+    alphas = [0.1 + 0.05 * i for i in range(steps)]
+    betas = [0.3 if with_prior else 0.0] * steps
+    if with_prior:
+        betas[1] = 0.0
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V, alpha_values=alphas,
+                                 beta_values=betas, baseline_logits=prior, device=dev)
+    assert runner._can_triton_fuse
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    base = (torch.randn(nb, steps, V, generator=g) * 3).to(torch.bfloat16)
+    out = runner(prefix.to(dev), base.to(dev))
+    scores = runner.static_scores.clone()
+    torch.cuda.synchronize()
+    assert out.shape == (nb, steps) and out.dtype == torch.int64
+    # replay again and run the same kernels eagerly: identical ids (deterministic kernels)
+    out2 = runner(prefix.to(dev), base.to(dev))
+    runner.enqueue_eager()
+    torch.testing.assert_close(out2, out, rtol=0, atol=0)
+    torch.testing.assert_close(runner.static_out, out, rtol=0, atol=0)
+    # oracle, teacher-forced with the device's own ids so each step is checked on its own history
+    prior_np = f(prior.to(torch.bfloat16)) if with_prior else None
+    dev_ids = out.cpu().numpy()
+    rid, rsc, rsec = oracle.rollout(
+        prefix.numpy().reshape(-1), f(base), embed=f(head.embed_tokens.weight), W_ih=f(head.prefix_gru.weight_ih_l0),
+        W_hh=f(head.prefix_gru.weight_hh_l0), b_hh=None,
+        A=f(head.rank_proj.weight), rank_bias=f(head.rank_proj.bias) if rank_bias else None, act=act,
+        B=f(head.low_rank_lm_head.weight), prior=prior_np, alphas=alphas, betas=betas, forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(scores).reshape(-1), rid.reshape(-1), rsc.reshape(-1),
+                              rsec.reshape(-1))
+    # the device's bf16 GRU state may differ from the oracle's by an ulp: allow score drift of 2e-2
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["max_score_err"] < 2e-2, res
+    runner.close()
+
+
+def test_golden_rollout(pkg, dev):
+    z = np.load(os.path.join(GOLDEN, "rollout_b2_s6.npz"))
+    V, E = z["emb"].shape
+    G = z["W_hh"].shape[1]
+    r = z["A"].shape[0]
+    nb, steps = z["ids"].shape
+    head = _Head(V, E, G, r, str(z["act"]), False, seed=0).to(dev)
+    with torch.no_grad():
+        head.embed_tokens.weight.copy_(from_bits(z["emb"], dev))
+        head.prefix_gru.weight_ih_l0.copy_(from_bits(z["W_ih"], dev))
+        head.prefix_gru.weight_hh_l0.copy_(from_bits(z["W_hh"], dev))
+        head.rank_proj.weight.copy_(from_bits(z["A"], dev))
+        head.low_rank_lm_head.weight.copy_(from_bits(z["B"], dev))
+    prior = from_bits(z["prior"], dev)
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V,
+                                 alpha_values=z["alphas"].tolist(), beta_values=z["betas"].tolist(),
+                                 baseline_logits=prior, device=dev)
+    base = from_bits(z["base"], dev)
+    out = runner(torch.from_numpy(z["prefix"]).view(nb, 1).to(dev), base)
+    torch.cuda.synchronize()
+    res = oracle.check_parity(out.cpu().numpy().reshape(-1), f(runner.static_scores).reshape(-1),
+                              z["ids"].reshape(-1), z["scores"].reshape(-1), z["seconds"].reshape(-1))
+    assert res["id_mismatch_pinned"] == 0 and res["max_score_err"] < 2e-2, res
+    runner.close()
+
+
+# ------------------------------------------------------------------ error paths
+
+def test_errors_are_raised_not_faulted(pkg, dev):
+    B = torch.zeros(100, 64, dtype=torch.bfloat16, device=dev)
+    rank = torch.zeros(2, 64, dtype=torch.bfloat16, device=dev)
+    base = torch.zeros(2, 100, device=dev)
+    with pytest.raises(ValueError):
+        pkg.fused_argmax(rank, B, base[:, :50])
+    with pytest.raises(TypeError):
+        pkg.fused_argmax(rank.float(), B, base)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        pkg.fused_argmax(rank.cpu(), B, base)
+    # misaligned operand: caught by the C ABI
+    big = torch.zeros(2, 72, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(pkg._lib.DelsError, match="aligned"):
+        pkg.fused_argmax(big[:, 1:65], B, base)
+    with pytest.raises(pkg._lib.DelsError, match="not supported"):
+        pkg.fused_argmax(torch.zeros(2, 1024, dtype=torch.bfloat16, device=dev),
+                         torch.zeros(100, 1024, dtype=torch.bfloat16, device=dev), base)
