@@ -1,0 +1,299 @@
+"""Benchmark of the fused low-rank LM-head argmax (DeLS draft-token selection) on one MI355X.
+
+One step = one draft step of the hot path on one batch: the rank projection
+rank = bf16(h . A^T) and the fused combine + vocabulary argmax over B [V, r],
+base logits [M, V] and the log-prior [V], with all inputs resident in HBM.
+The default workload is the Qwen3-8B low-rank head at M=16 (d=4096, r=512,
+V=151936, fp32 base logits, per-position alpha/beta); ``--also-m512`` adds the
+batched M=512 shape (bf16 base and prior) as a second, informative record.
+
+Timing: ``--sets`` input sets (> 256 MB in total, so B cannot stay resident in
+the 256 MB MALL) are rotated step by step.  The K timed steps are one hipGraph
+of K consecutive draft steps (kernels back to back, no host launch overhead),
+bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
+The dominant kernel's average duration comes from a second graph of K fused
+argmax launches only (rank precomputed), timed the same way.
+
+CPU baseline: the oracle (a numpy port of the reference semantics) on a
+bounded number of full calls of the same workload, on this host's cores.
+
+Prints one JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+REPO_DIR = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO_DIR)
+
+METRIC = "argmax rows/s + % HBM/MFMA roofline, Qwen3-8B low-rank LM head, M=16 & 512"
+HBM_PEAK_GBS = 8000.0
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="qwen3_8b_m16", choices=["qwen3_8b_m16", "qwen3_4b_m16", "qwen3_8b_m512"])
+    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
+    ap.add_argument("--also-m512", action=argparse.BooleanOptionalAction, default=True)
+    ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--layout", default="packed", choices=["packed", "rowmajor"],
+                    help="weights in the MFMA-16 block layout (as the runner stores them) or row-major")
+    ap.add_argument("--traffic-file", default=os.path.join(REPO_DIR, "profiles", "traffic.json"))
+    return ap.parse_args()
+
+
+def workload_desc(name, x, layout):
+    s = x.shape
+    return {
+        "workload": name,
+        "M": s["M"], "d": s["d"], "r": s["r"], "V": s["V"],
+        "base_dtype": str(x.base.dtype).replace("torch.", ""),
+        "prior_dtype": str(x.prior.dtype).replace("torch.", ""),
+        "alpha_beta": "per-position U[0,0.6], period 16" if name != "qwen3_4b_m16" else "scalar 0.3",
+        "act": x.act,
+        "weights_layout": "MFMA-16 blocks" if layout == "packed" else "row-major",
+    }
+
+
+def kernel_bytes(M, d, r, V, base_bytes, prior_bytes):
+    """Algorithmic HBM bytes of the fused argmax kernel and of the whole step."""
+    argmax = 2 * r * V + base_bytes * M * V + prior_bytes * V + 2 * M * r + 12 * M
+    rank = 2 * r * d + 2 * M * d + 2 * M * r
+    return argmax, rank
+
+
+def make_sets(pkg, x_cpu, nsets, dev):
+    """Set 0: the seeded CPU inputs; sets 1..: the same distributions drawn on the GPU."""
+    import torch
+
+    x0 = x_cpu.to(dev)
+    sets = [x0]
+    g = torch.Generator(device=dev)
+    for i in range(1, nsets):
+        g.manual_seed(1000 + i)
+        s = x0.shape
+        h = torch.randn(s["M"], s["d"], generator=g, device=dev).to(torch.bfloat16)
+        A = (torch.randn(s["r"], s["d"], generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        B = (torch.randn(s["V"], s["r"], generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        base = (torch.randn(s["M"], s["V"], generator=g, device=dev) * 3).to(x0.base.dtype)
+        prior = x0.prior[torch.randperm(s["V"], generator=g, device=dev)].contiguous()
+        sets.append(pkg.synth.LowRankInputs(h, A, B, base, prior, x0.alpha, x0.beta, x0.act))
+    return sets
+
+
+def set_bytes(x):
+    return sum(t.numel() * t.element_size() for t in (x.h, x.A, x.B, x.base, x.prior))
+
+
+def time_graph(torch, record, steps, dev, reps=3):
+    """Capture `record(i)` for i < steps in one graph; best of `reps` timed replays (ms)."""
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        record(0)                        # sizes this stream's workspace outside the capture
+        torch.cuda.synchronize(dev)
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                record(i)
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    torch.cuda.synchronize(dev)
+    graph.replay()                       # warm replay
+    torch.cuda.synchronize(dev)
+    best = None
+    cur = torch.cuda.current_stream(dev)
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize(dev)
+        e0.record(cur)
+        graph.replay()
+        e1.record(cur)
+        torch.cuda.synchronize(dev)
+        ms = e0.elapsed_time(e1)
+        best = ms if best is None else min(best, ms)
+    return best, graph
+
+
+def bench_workload(pkg, name, args, dev, torch):
+    nsets = args.sets
+    x0 = pkg.synth.config_inputs(name)
+    per = set_bytes(x0)
+    if nsets <= 0:
+        nsets = max(3, -(-512 * 2**20 // per))
+    sets = make_sets(pkg, x0, nsets, dev)
+    s = x0.shape
+    M, d, r, V = s["M"], s["d"], s["r"], s["V"]
+    outs = [(torch.empty(M, dtype=torch.int64, device=dev), torch.empty(M, dtype=torch.float32, device=dev))
+            for _ in range(nsets)]
+    ranks = [torch.empty(M, r, dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
+    if args.layout == "packed":
+        weights = [(pkg.pack_operand(x.A), pkg.pack_operand(x.B)) for x in sets]
+    else:
+        weights = [(x.A, x.B) for x in sets]
+
+    def step(i):
+        x = sets[i % nsets]
+        o = outs[i % nsets]
+        A, B = weights[i % nsets]
+        pkg.lowrank_argmax(x.h, A, B, x.base, x.prior, x.alpha, x.beta, act=x.act, out_ids=o[0], out_score=o[1])
+
+    def argmax_only(i):
+        x = sets[i % nsets]
+        o = outs[i % nsets]
+        pkg.fused_argmax(ranks[i % nsets], weights[i % nsets][1], x.base, x.prior, x.alpha, x.beta, out_ids=o[0],
+                         out_score=o[1])
+
+    # eager warm-up (also sizes the shared workspace before capture)
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    eager = [(o[0].clone(), o[1].clone()) for o in outs]
+    for i in range(nsets):
+        pkg.rank_proj(sets[i].h, weights[i][0], None, sets[i].act, out=ranks[i])
+    torch.cuda.synchronize(dev)
+
+    ms_total, g_step = time_graph(torch, step, args.steps, dev)
+    # the graph replays must reproduce the eager results
+    for i in range(nsets):
+        if not (torch.equal(outs[i][0], eager[i][0]) and torch.equal(outs[i][1], eager[i][1])):
+            raise RuntimeError(f"graph replay differs from eager results on set {i}")
+    ms_kernel_total, g_arg = time_graph(torch, argmax_only, args.steps, dev)
+    del g_step, g_arg
+
+    ms_step = ms_total / args.steps
+    us_kernel = ms_kernel_total * 1e3 / args.steps
+    base_b = x0.base.element_size()
+    prior_b = x0.prior.element_size()
+    arg_bytes, rank_bytes = kernel_bytes(M, d, r, V, base_b, prior_b)
+    flops_step = 2.0 * M * r * (d + V)
+    rec = {
+        "M": M, "d": d, "r": r, "V": V,
+        "rows_per_s": M / (ms_step * 1e-3),
+        "us_per_step": ms_step * 1e3,
+        "us_fused_argmax": us_kernel,
+        "argmax_bytes": arg_bytes,
+        "step_bytes": arg_bytes + rank_bytes,
+        "argmax_GBs": arg_bytes / (us_kernel * 1e-6) / 1e9,
+        "step_GBs": (arg_bytes + rank_bytes) / (ms_step * 1e-3) / 1e9,
+        "step_TFLOPs": flops_step / (ms_step * 1e-3) / 1e12,
+        "sets": nsets,
+        "set_MB": per / 2**20,
+    }
+    rec["hbm_frac_step"] = rec["step_GBs"] / HBM_PEAK_GBS
+    rec["mfma_frac_step"] = rec["step_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS
+    return rec, x0
+
+
+def cpu_baseline(name, x0, seconds):
+    """The oracle on full calls of the workload, repeated for about `seconds`."""
+    import numpy as np
+
+    import oracle
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    f = lambda t: t.float().numpy()  # noqa: E731
+    h, A, B, base, prior, alpha, beta = (f(x0.h), f(x0.A), f(x0.B), f(x0.base), f(x0.prior), f(x0.alpha),
+                                         f(x0.beta))
+    M = h.shape[0]
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.lowrank_argmax(h, A, None, x0.act, B, base, prior, alpha, beta)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or calls >= 50:
+            break
+    return {
+        "value": M * calls / el,
+        "unit": "rows/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{calls} full calls of {name} (M={M}) through the numpy oracle (fp64 dot, fp32 combine), "
+                  f"{el:.1f} s on {platform.processor() or platform.machine()}",
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build targets one GPU: the fused argmax shards by rows or by "
+                                   "vocabulary without collectives on the hot path; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    pkg._lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    rec, x0 = bench_workload(pkg, args.workload, args, dev, torch)
+    traffic = None
+    if os.path.exists(args.traffic_file):
+        try:
+            with open(args.traffic_file) as fh:
+                traffic = json.load(fh).get(args.workload, {}).get("fused_argmax_hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    out = {
+        "metric": METRIC,
+        "value": rec["rows_per_s"],
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": rec["us_per_step"] / 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) h, N(0,0.02) A/B, N(0,3) base, permuted Zipf(1.1) log-prior; "
+                f"{rec['sets']} rotating sets of {rec['set_MB']:.0f} MB)",
+        "config": workload_desc(args.workload, x0, args.layout),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "fused_argmax_gemv_kernel",
+            "achieved": rec["argmax_GBs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": rec["argmax_GBs"] / HBM_PEAK_GBS,
+            "traffic": traffic,
+            "algorithmic_bytes": rec["argmax_bytes"],
+            "us_per_launch": rec["us_fused_argmax"],
+        },
+        "step": {k: rec[k] for k in ("us_per_step", "step_bytes", "step_GBs", "hbm_frac_step", "step_TFLOPs",
+                                     "mfma_frac_step")},
+    }
+    if args.also_m512 and args.workload != "qwen3_8b_m512":
+        try:
+            r512, _ = bench_workload(pkg, "qwen3_8b_m512", argparse.Namespace(**{**vars(args), "sets": 0,
+                                                                                   "steps": min(args.steps, 100)}),
+                                     dev, torch)
+            out["m512"] = {k: r512[k] for k in ("rows_per_s", "us_per_step", "us_fused_argmax", "argmax_GBs",
+                                                "step_GBs", "hbm_frac_step", "step_TFLOPs", "mfma_frac_step")}
+        except Exception as e:  # informative record only
+            out["m512"] = {"error": repr(e)}
+    if args.cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.workload, x0, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -6,11 +6,13 @@ Public surface (mirrors the reference's interface for this path):
   * ``parse_scalar_schedule``, ``load_unigram_log_prior``
   * ``fused_argmax``, ``lowrank_argmax``, ``rank_proj``, ``gru_step`` -- the
     per-step operators, each a thin wrapper over the C ABI in include/dels.h
+  * ``pack_operand`` -- repack a weight into the MFMA-16 block layout the
+    kernels stream at full HBM bandwidth
 """
 
 from .local_head import (DeLSLocalHead, load_unigram_log_prior, parse_scalar_schedule,
                          unigram_log_prior_from_counts)
-from .ops import fused_argmax, gru_step, lowrank_argmax, rank_proj
+from .ops import PackedWeight, fused_argmax, gru_step, lowrank_argmax, pack_operand, rank_proj
 from .runner import DeLSGraphRunner
 from . import synth
 
@@ -24,5 +26,7 @@ __all__ = [
     "lowrank_argmax",
     "rank_proj",
     "gru_step",
+    "pack_operand",
+    "PackedWeight",
     "synth",
 ]

@@ -19,6 +19,7 @@ LIB_PATH = os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
 DELS_OK = 0
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_IDENTITY, ACT_SILU = 0, 1
+LAYOUT_ROWMAJOR, LAYOUT_MFMA16 = 0, 1
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -38,6 +39,7 @@ class RolloutParams(ctypes.Structure):
         ("prior", _ptr), ("prior_dtype", _int),
         ("alpha", _fptr), ("beta", _fptr),
         ("batch", _i64), ("steps", _i64), ("G", _i64), ("r", _i64), ("V", _i64),
+        ("weights_layout", _int),
         ("prefix_ids", _ptr),
         ("base", _ptr), ("base_dtype", _int),
         ("out_ids", _ptr), ("out_scores", _ptr),
@@ -53,17 +55,21 @@ SIGNATURES = {
     "dels_strerror": (ctypes.c_char_p, [_int]),
     "dels_last_error": (ctypes.c_char_p, []),
     "dels_workspace_init": (_int, [_ptr, _sz, _ptr]),
+    "dels_packed_bytes": (_sz, [_i64, _i64]),
+    "dels_pack_operand": (_int, [_ptr, _i64, _i64, _i64, _ptr, _sz, _ptr]),
     "dels_rank_proj_ws_bytes": (_sz, [_i64, _i64, _i64]),
-    "dels_rank_proj": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_rank_proj": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _int, _i64, _i64, _i64, _ptr, _i64, _ptr, _sz,
+                              _ptr]),
     "dels_fused_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
-    "dels_fused_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _i64, _int, _ptr, _int, _fptr, _i64, _fptr, _i64,
+    "dels_fused_argmax": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _i64, _int, _ptr, _int, _fptr, _i64, _fptr, _i64,
                                  _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_lowrank_argmax_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
-    "dels_lowrank_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _int, _ptr, _i64, _ptr, _i64, _int, _ptr, _int,
+    "dels_lowrank_argmax": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _int, _ptr, _i64, _int, _ptr, _i64, _int, _ptr,
+                                   _int,
                                    _fptr, _i64, _fptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz,
                                    _ptr]),
     "dels_gru_step_ws_bytes": (_sz, [_i64, _i64]),
-    "dels_gru_step": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _ptr, _i64, _i64, _ptr, _i64, _ptr,
+    "dels_gru_step": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _int, _ptr, _i64, _i64, _ptr, _i64, _ptr,
                              _sz, _ptr]),
     "dels_rollout_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "dels_rollout_enqueue": (_int, [ctypes.POINTER(RolloutParams), _ptr]),

@@ -19,7 +19,8 @@ LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libdels_mi355x.so"
 LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 
-SOURCES = ["capi.hip", "skinny_gemm.hip", "fused_argmax.hip"]
+SOURCES = ["capi.hip", "skinny_gemm.hip", "fused_argmax.hip", "fused_argmax_f32.hip", "fused_argmax_bf16.hip",
+           "fused_argmax_f16.hip", "pack.hip"]
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (kept off on this target).
 HIP_FLAGS = [

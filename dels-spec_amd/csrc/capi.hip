@@ -30,8 +30,6 @@ static int hip_fail(hipError_t e, const char* what) {
     return fail(DELS_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
-
 int device_cu_count() {
     static int cache[64] = {0};
     int dev = 0;
@@ -71,25 +69,34 @@ static int check_bf16_matrix(const void* p, int64_t ld, int64_t cols, const char
     return DELS_OK;
 }
 
+// Checks of a bf16 weight operand in either layout.
+static int check_weight(const void* p, int64_t ld, int64_t cols, int layout, const char* name) {
+    if (layout == DELS_LAYOUT_ROWMAJOR) return check_bf16_matrix(p, ld, cols, name);
+    if (layout != DELS_LAYOUT_MFMA16) return fail(DELS_ERR_INVALID_ARGUMENT, "%s: unknown layout %d", name, layout);
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+    if (!aligned16(p)) return fail(DELS_ERR_ALIGNMENT, "packed %s must be 16-byte aligned", name);
+    return DELS_OK;
+}
+
 // ---- workspace layouts -------------------------------------------------------
 
+// Every layout starts with the shared control area [0, kCtrlBytes).
 struct LowrankLayout {
-    size_t argmax_off, rank_off, skinny_off, total;
+    size_t rank_off, part_off, total;
     SkinnyPlan plan;
 };
 
 static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) {
     LowrankLayout L{};
     L.plan = plan_skinny(M, d, r, false);
-    L.argmax_off = 0;
-    L.rank_off = align256(argmax_ws_bytes(M, r, V));
-    L.skinny_off = L.rank_off + align256((size_t)M * r * 2);
-    L.total = L.skinny_off + skinny_ws_bytes(L.plan);
+    L.rank_off = kCtrlBytes;
+    L.part_off = L.rank_off + align256((size_t)M * r * 2);
+    L.total = L.part_off + skinny_data_bytes(L.plan) + align256(argmax_data_bytes(M, r, V));
     return L;
 }
 
 struct RolloutLayout {
-    size_t argmax_off, rank_off, gru_off, total;
+    size_t part_off, total;   // rank projection and GRU steps run in turn and share the partials
     SkinnyPlan rank_plan, gru_plan;
 };
 
@@ -97,16 +104,15 @@ static RolloutLayout rollout_layout(int64_t batch, int64_t G, int64_t r, int64_t
     RolloutLayout L{};
     L.rank_plan = plan_skinny(batch, G, r, false);
     L.gru_plan = plan_skinny(batch, G, G, true);
-    L.argmax_off = 0;
-    L.rank_off = align256(argmax_ws_bytes(batch, r, V));
-    L.gru_off = L.rank_off + align256(skinny_ws_bytes(L.rank_plan));
-    L.total = L.gru_off + align256(skinny_ws_bytes(L.gru_plan));
+    L.part_off = kCtrlBytes;
+    L.total = L.part_off + std::max(skinny_data_bytes(L.rank_plan), skinny_data_bytes(L.gru_plan)) +
+              align256(argmax_data_bytes(batch, r, V));
     return L;
 }
 
 // ---- argument checks shared by several entry points ----------------------------
 
-static int check_argmax_args(const void* rank, int64_t ldrank, const void* B, int64_t ldb,
+static int check_argmax_args(const void* rank, int64_t ldrank, const void* B, int64_t ldb, int b_layout,
                              const void* base, int64_t ldbase, int base_dtype,
                              const void* prior, int prior_dtype,
                              const float* alpha, int64_t alpha_stride,
@@ -122,7 +128,7 @@ static int check_argmax_args(const void* rank, int64_t ldrank, const void* B, in
     if (M == 0) return DELS_OK;   // nothing to read or write
     int rc;
     if (check_rank && (rc = check_bf16_matrix(rank, ldrank, r, "rank")) != DELS_OK) return rc;
-    if ((rc = check_bf16_matrix(B, ldb, r, "B (low-rank LM head)")) != DELS_OK) return rc;
+    if ((rc = check_weight(B, ldb, r, b_layout, "B (low-rank LM head)")) != DELS_OK) return rc;
     if (!base) return fail(DELS_ERR_INVALID_ARGUMENT, "base logits pointer is NULL");
     if (!valid_dtype(base_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown base dtype %d", base_dtype);
     if (M > 1 && ldbase < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
@@ -144,8 +150,8 @@ static int check_ws(const void* ws, size_t ws_bytes, size_t need) {
 }
 
 static int check_gru_args(const void* gi_table, int64_t ld_gi, int64_t table_rows, const int64_t* tokens,
-                          const void* h_in, int64_t ldh_in, const void* w_hh, int64_t batch, int64_t G,
-                          const void* h_out, int64_t ldh_out) {
+                          const void* h_in, int64_t ldh_in, const void* w_hh, int w_layout, int64_t batch,
+                          int64_t G, const void* h_out, int64_t ldh_out) {
     if (batch < 0 || G <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad GRU shape batch=%lld G=%lld",
                                          (long long)batch, (long long)G);
     if (batch > 64) return fail(DELS_ERR_UNSUPPORTED, "GRU step supports batch <= 64 (got %lld)", (long long)batch);
@@ -157,7 +163,9 @@ static int check_gru_args(const void* gi_table, int64_t ld_gi, int64_t table_row
     if (!tokens) return fail(DELS_ERR_INVALID_ARGUMENT, "token ids pointer is NULL");
     int rc;
     if (h_in && (rc = check_bf16_matrix(h_in, ldh_in, G, "h_in")) != DELS_OK) return rc;
-    if ((rc = check_bf16_matrix(w_hh, G, G, "W_hh")) != DELS_OK) return rc;
+    if ((rc = check_weight(w_hh, G, G, w_layout, "W_hh")) != DELS_OK) return rc;
+    if (w_layout == DELS_LAYOUT_MFMA16 && G % 16 != 0)
+        return fail(DELS_ERR_UNSUPPORTED, "packed W_hh needs a hidden size divisible by 16");
     if (!h_out) return fail(DELS_ERR_INVALID_ARGUMENT, "h_out is NULL");
     if (batch > 1 && ldh_out < G) return fail(DELS_ERR_INVALID_ARGUMENT, "h_out leading dimension < G");
     if (h_in && h_in == h_out) return fail(DELS_ERR_INVALID_ARGUMENT, "h_in and h_out must not alias");
@@ -173,15 +181,17 @@ static int check_rollout(const dels_rollout* p) {
     if (p->act != DELS_ACT_IDENTITY && p->act != DELS_ACT_SILU)
         return fail(DELS_ERR_INVALID_ARGUMENT, "unknown rank activation %d", p->act);
     int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
-                            p->batch, p->G, p->h_b, p->G);
+                            p->weights_layout, p->batch, p->G, p->h_b, p->G);
     if (rc != DELS_OK) return rc;
     if ((rc = check_bf16_matrix(p->h_b, p->G, p->G, "h_b")) != DELS_OK) return rc;
-    if ((rc = check_bf16_matrix(p->rank_w, p->G, p->G, "rank_w")) != DELS_OK) return rc;
-    if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->base, p->steps * p->V, p->base_dtype, p->prior,
+    if ((rc = check_weight(p->rank_w, p->G, p->G, p->weights_layout, "rank_w")) != DELS_OK) return rc;
+    if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->weights_layout, p->base, p->steps * p->V, p->base_dtype, p->prior,
                                 p->prior_dtype, p->alpha, 0, p->beta, 0, p->batch, p->r, p->V, p->out_ids,
                                 p->steps, true)) != DELS_OK)
         return rc;
     const RolloutLayout L = rollout_layout(p->batch, p->G, p->r, p->V);
+    if (!skinny_supported(L.rank_plan) || !skinny_supported(L.gru_plan))
+        return fail(DELS_ERR_UNSUPPORTED, "rollout shape needs too many workgroup tiles");
     return check_ws(p->ws, p->ws_bytes, L.total);
 }
 
@@ -195,6 +205,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     g.ld_gi = p->ld_gi;
     g.table_rows = p->table_rows;
     g.w_hh = static_cast<const uint16_t*>(p->w_hh);
+    g.w_packed = p->weights_layout == DELS_LAYOUT_MFMA16;
     g.b_hh = static_cast<const uint16_t*>(p->b_hh);
     g.batch = B;
     g.G = G;
@@ -206,7 +217,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     g.ldh_in = G;
     g.h_out = static_cast<uint16_t*>(p->h_a);
     g.ldh_out = G;
-    hipError_t e = launch_gru_step(g, L.gru_plan, ws + L.gru_off, s);
+    hipError_t e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
     if (e != hipSuccess) return hip_fail(e, "GRU step launch");
 
     uint16_t* h_cur = static_cast<uint16_t*>(p->h_a);
@@ -216,15 +227,17 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         RankArgs ra{};
         ra.h = h_cur; ra.ldh = G;
         ra.A = static_cast<const uint16_t*>(p->rank_w); ra.lda = G;
+        ra.a_packed = p->weights_layout == DELS_LAYOUT_MFMA16;
         ra.bias = static_cast<const uint16_t*>(p->rank_b); ra.act = p->act;
         ra.M = B; ra.d = G; ra.r = r;
         ra.rank = static_cast<uint16_t*>(p->rank); ra.ldrank = r;
-        e = launch_rank_proj(ra, L.rank_plan, ws + L.rank_off, s);
+        e = launch_rank_proj(ra, L.rank_plan, ws, L.part_off, s);
         if (e != hipSuccess) return hip_fail(e, "rank projection launch");
 
         ArgmaxArgs aa{};
         aa.rank = static_cast<const uint16_t*>(p->rank); aa.ldrank = r;
         aa.B = static_cast<const uint16_t*>(p->lm_w); aa.ldb = r;
+        aa.b_packed = p->weights_layout == DELS_LAYOUT_MFMA16;
         aa.base = static_cast<const char*>(p->base) + (size_t)step * V * esz;
         aa.ldbase = p->steps * (int64_t)V;
         aa.base_dtype = p->base_dtype;
@@ -235,7 +248,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_ids = p->out_ids + step;
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
-        e = launch_fused_argmax(aa, ws + L.argmax_off, s);
+        e = launch_fused_argmax(aa, ws, s);
         if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
 
         if (step + 1 < p->steps) {
@@ -243,7 +256,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
             g.tok_stride = p->steps;
             g.h_in = h_cur;
             g.h_out = h_next;
-            e = launch_gru_step(g, L.gru_plan, ws + L.gru_off, s);
+            e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
             if (e != hipSuccess) return hip_fail(e, "GRU step launch");
             std::swap(h_cur, h_next);
         }
@@ -287,11 +300,32 @@ int dels_workspace_init(void* ws, size_t ws_bytes, void* stream) {
     return e == hipSuccess ? DELS_OK : hip_fail(e, "workspace fill launch");
 }
 
-size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r) {
-    return skinny_ws_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1), std::max<int64_t>(r, 1), false));
+size_t dels_packed_bytes(int64_t rows, int64_t cols) {
+    if (rows <= 0 || cols <= 0) return 0;
+    return packed_bytes(rows, cols);
 }
 
-int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, const void* bias, int act,
+int dels_pack_operand(const void* W, int64_t ldw, int64_t rows, int64_t cols, void* packed, size_t packed_bytes_,
+                      void* stream) {
+    if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
+    if (rows == 0 || cols == 0) return DELS_OK;
+    int rc = check_bf16_matrix(W, ldw, cols, "W (to pack)");
+    if (rc != DELS_OK) return rc;
+    if (!packed || !aligned16(packed)) return fail(DELS_ERR_ALIGNMENT, "packed output must be 16-byte aligned");
+    if (packed_bytes_ < packed_bytes(rows, cols))
+        return fail(DELS_ERR_INVALID_ARGUMENT, "packed output too small: %zu bytes given, %zu needed", packed_bytes_,
+                    packed_bytes(rows, cols));
+    hipError_t e = launch_pack_mfma16(static_cast<const uint16_t*>(W), ldw, rows, cols, static_cast<uint16_t*>(packed),
+                                      static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "pack launch");
+}
+
+size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r) {
+    return kCtrlBytes + skinny_data_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1),
+                                                      std::max<int64_t>(r, 1), false));
+}
+
+int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout, const void* bias, int act,
                    int64_t M, int64_t d, int64_t r, void* rank, int64_t ldrank, void* ws, size_t ws_bytes,
                    void* stream) {
     if (M < 0 || d <= 0 || r <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad rank projection shape");
@@ -302,36 +336,39 @@ int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, const
     if (M == 0) return DELS_OK;
     int rc;
     if ((rc = check_bf16_matrix(h, ldh, d, "h")) != DELS_OK) return rc;
-    if ((rc = check_bf16_matrix(A, lda, d, "A (rank projection)")) != DELS_OK) return rc;
+    if ((rc = check_weight(A, lda, d, a_layout, "A (rank projection)")) != DELS_OK) return rc;
     if (!rank) return fail(DELS_ERR_INVALID_ARGUMENT, "rank output is NULL");
     if (ldrank < r) return fail(DELS_ERR_INVALID_ARGUMENT, "rank leading dimension < r");
     const SkinnyPlan p = plan_skinny(M, d, r, false);
-    if ((rc = check_ws(ws, ws_bytes, skinny_ws_bytes(p))) != DELS_OK) return rc;
+    if (!skinny_supported(p)) return fail(DELS_ERR_UNSUPPORTED, "rank projection shape needs too many tiles");
+    if ((rc = check_ws(ws, ws_bytes, kCtrlBytes + skinny_data_bytes(p))) != DELS_OK) return rc;
     RankArgs ra{};
     ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
-    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda;
+    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda; ra.a_packed = a_layout == DELS_LAYOUT_MFMA16;
     ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
     ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
     ra.rank = static_cast<uint16_t*>(rank); ra.ldrank = ldrank;
-    hipError_t e = launch_rank_proj(ra, p, ws, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_rank_proj(ra, p, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "rank projection launch");
 }
 
-size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) { return argmax_ws_bytes(M, r, V); }
+size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) {
+    return kCtrlBytes + align256(argmax_data_bytes(M, r, V));
+}
 
-int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb, const void* base,
+int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb, int b_layout, const void* base,
                       int64_t ldbase, int base_dtype, const void* prior, int prior_dtype, const float* alpha,
                       int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t r,
                       int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
                       void* stream) {
-    int rc = check_argmax_args(rank, ldrank, B, ldb, base, ldbase, base_dtype, prior, prior_dtype, alpha,
+    int rc = check_argmax_args(rank, ldrank, B, ldb, b_layout, base, ldbase, base_dtype, prior, prior_dtype, alpha,
                                alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, true);
     if (rc != DELS_OK) return rc;
     if (M == 0) return DELS_OK;
-    if ((rc = check_ws(ws, ws_bytes, argmax_ws_bytes(M, r, V))) != DELS_OK) return rc;
+    if ((rc = check_ws(ws, ws_bytes, dels_fused_argmax_ws_bytes(M, r, V))) != DELS_OK) return rc;
     ArgmaxArgs a{};
     a.rank = static_cast<const uint16_t*>(rank); a.ldrank = ldrank;
-    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb;
+    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb; a.b_packed = b_layout == DELS_LAYOUT_MFMA16;
     a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
     a.prior = prior; a.prior_dtype = prior_dtype;
     a.alpha = alpha; a.alpha_stride = alpha_stride;
@@ -347,13 +384,13 @@ size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) 
                           std::max<int64_t>(V, 1)).total;
 }
 
-int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, const void* bias, int act,
-                        const void* B, int64_t ldb, const void* base, int64_t ldbase, int base_dtype,
+int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout, const void* bias,
+                        int act, const void* B, int64_t ldb, int b_layout, const void* base, int64_t ldbase, int base_dtype,
                         const void* prior, int prior_dtype, const float* alpha, int64_t alpha_stride,
                         const float* beta, int64_t beta_stride, int64_t M, int64_t d, int64_t r, int64_t V,
                         int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
                         void* stream) {
-    int rc = check_argmax_args(nullptr, r, B, ldb, base, ldbase, base_dtype, prior, prior_dtype, alpha,
+    int rc = check_argmax_args(nullptr, r, B, ldb, b_layout, base, ldbase, base_dtype, prior, prior_dtype, alpha,
                                alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, false);
     if (rc != DELS_OK) return rc;
     if (d <= 0 || d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8",
@@ -362,8 +399,9 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
         return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
     if (M == 0) return DELS_OK;
     if ((rc = check_bf16_matrix(h, ldh, d, "h")) != DELS_OK) return rc;
-    if ((rc = check_bf16_matrix(A, lda, d, "A (rank projection)")) != DELS_OK) return rc;
+    if ((rc = check_weight(A, lda, d, a_layout, "A (rank projection)")) != DELS_OK) return rc;
     const LowrankLayout L = lowrank_layout(M, d, r, V);
+    if (!skinny_supported(L.plan)) return fail(DELS_ERR_UNSUPPORTED, "rank projection shape needs too many tiles");
     if ((rc = check_ws(ws, ws_bytes, L.total)) != DELS_OK) return rc;
     char* w = static_cast<char*>(ws);
     hipStream_t s = static_cast<hipStream_t>(stream);
@@ -371,47 +409,52 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
 
     RankArgs ra{};
     ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
-    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda;
+    ra.A = static_cast<const uint16_t*>(A); ra.lda = lda; ra.a_packed = a_layout == DELS_LAYOUT_MFMA16;
     ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
     ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
     ra.rank = rank; ra.ldrank = r;
-    hipError_t e = launch_rank_proj(ra, L.plan, w + L.skinny_off, s);
+    hipError_t e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
     if (e != hipSuccess) return hip_fail(e, "rank projection launch");
 
     ArgmaxArgs a{};
     a.rank = rank; a.ldrank = r;
-    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb;
+    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb; a.b_packed = b_layout == DELS_LAYOUT_MFMA16;
     a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
     a.prior = prior; a.prior_dtype = prior_dtype;
     a.alpha = alpha; a.alpha_stride = alpha_stride;
     a.beta = beta; a.beta_stride = beta_stride;
     a.M = (int)M; a.r = (int)r; a.V = (int)V;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
-    e = launch_fused_argmax(a, w + L.argmax_off, s);
+    e = launch_fused_argmax(a, ws, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }
 
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {
-    return skinny_ws_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1), std::max<int64_t>(G, 1), true));
+    return kCtrlBytes + skinny_data_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1),
+                                                      std::max<int64_t>(G, 1), true));
 }
 
 int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const int64_t* tokens,
-                  int64_t tok_stride, const void* h_in, int64_t ldh_in, const void* w_hh, const void* b_hh,
+                  int64_t tok_stride, const void* h_in, int64_t ldh_in, const void* w_hh, int w_layout,
+                  const void* b_hh,
                   int64_t batch, int64_t G, void* h_out, int64_t ldh_out, void* ws, size_t ws_bytes,
                   void* stream) {
-    int rc = check_gru_args(gi_table, ld_gi, table_rows, tokens, h_in, ldh_in, w_hh, batch, G, h_out, ldh_out);
+    int rc = check_gru_args(gi_table, ld_gi, table_rows, tokens, h_in, ldh_in, w_hh, w_layout, batch, G, h_out,
+                            ldh_out);
     if (rc != DELS_OK) return rc;
     if (batch == 0) return DELS_OK;
     const SkinnyPlan p = plan_skinny(batch, G, G, true);
-    if ((rc = check_ws(ws, ws_bytes, skinny_ws_bytes(p))) != DELS_OK) return rc;
+    if (!skinny_supported(p)) return fail(DELS_ERR_UNSUPPORTED, "GRU shape needs too many tiles");
+    if ((rc = check_ws(ws, ws_bytes, kCtrlBytes + skinny_data_bytes(p))) != DELS_OK) return rc;
     GruArgs g{};
     g.gi_table = static_cast<const uint16_t*>(gi_table); g.ld_gi = ld_gi; g.table_rows = table_rows;
     g.tokens = tokens; g.tok_stride = tok_stride;
     g.h_in = static_cast<const uint16_t*>(h_in); g.ldh_in = ldh_in;
-    g.w_hh = static_cast<const uint16_t*>(w_hh); g.b_hh = static_cast<const uint16_t*>(b_hh);
+    g.w_hh = static_cast<const uint16_t*>(w_hh); g.w_packed = w_layout == DELS_LAYOUT_MFMA16;
+    g.b_hh = static_cast<const uint16_t*>(b_hh);
     g.batch = (int)batch; g.G = (int)G;
     g.h_out = static_cast<uint16_t*>(h_out); g.ldh_out = ldh_out;
-    hipError_t e = launch_gru_step(g, p, ws, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_gru_step(g, p, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "GRU step launch");
 }
 
@@ -451,9 +494,9 @@ int dels_graph_create(const dels_rollout* p, void** graph_out) {
     hipGraphExec_t exec = nullptr;
     if (rc == DELS_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
         rc = hip_fail(e, "hipGraphInstantiate");
-    hipStreamDestroy(cs);
+    (void)hipStreamDestroy(cs);
     if (rc != DELS_OK) {
-        if (graph) hipGraphDestroy(graph);
+        if (graph) (void)hipGraphDestroy(graph);
         return rc;
     }
     GraphHandle* hdl = new GraphHandle{graph, exec};

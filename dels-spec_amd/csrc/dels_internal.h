@@ -8,6 +8,21 @@
 
 namespace dels {
 
+// ---- workspace layout ---------------------------------------------------------
+// Every entry point uses the same control area at the start of the workspace:
+// cross-workgroup counters at [0, 32 KiB) and argmax keys at [32 KiB, 64 KiB).
+// Kernels return the control area to zero before they finish; data regions
+// (split-K partials, the rank buffer) start at kCtrlBytes and may hold anything
+// between calls.  Calls with different shapes or entry points can therefore
+// share one workspace.
+constexpr size_t kCtrlBytes = 65536;
+constexpr size_t kCountersOff = 0;
+constexpr int kMaxCounters = 8192;
+constexpr size_t kKeysOff = 32768;
+constexpr int kMaxKeyRows = 4096;
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 // ---- skinny GEMM: rank projection and fused GRU step -----------------------
 
 struct SkinnyPlan {
@@ -15,37 +30,40 @@ struct SkinnyPlan {
     int m_wg, n_wg;    // workgroup grid (row tiles, col tiles)
     int ksplit;        // workgroups sharing one output tile along K
     int ksteps;        // ceil(K / 32)
-    size_t counter_bytes, partial_bytes;
+    size_t partial_bytes;
 };
 
 // rows: M; cols: N (rank) or G (GRU, three gate tiles per column tile).
 SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru);
-size_t skinny_ws_bytes(const SkinnyPlan& p);
+// Bytes of the data region the plan needs (its counters live in the control area).
+size_t skinny_data_bytes(const SkinnyPlan& p);
+bool skinny_supported(const SkinnyPlan& p);
 
 struct RankArgs {
     const uint16_t* h; int64_t ldh;
-    const uint16_t* A; int64_t lda;
+    const uint16_t* A; int64_t lda; bool a_packed;
     const uint16_t* bias; int act;
     int M, d, r;
     uint16_t* rank; int64_t ldrank;
 };
-hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s);
+// `ws` is the workspace base (control area); partials go to ws + data_off.
+hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s);
 
 struct GruArgs {
     const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
     const int64_t* tokens; int64_t tok_stride;
     const uint16_t* h_in; int64_t ldh_in;
-    const uint16_t* w_hh; const uint16_t* b_hh;
+    const uint16_t* w_hh; bool w_packed; const uint16_t* b_hh;
     int batch, G;
     uint16_t* h_out; int64_t ldh_out;
 };
-hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s);
+hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s);
 
 // ---- fused combine + argmax -------------------------------------------------
 
 struct ArgmaxArgs {
     const uint16_t* rank; int64_t ldrank;
-    const uint16_t* B; int64_t ldb;
+    const uint16_t* B; int64_t ldb; bool b_packed;
     const void* base; int64_t ldbase; int base_dtype;
     const void* prior; int prior_dtype;
     const float* alpha; int64_t alpha_stride;
@@ -53,12 +71,22 @@ struct ArgmaxArgs {
     int M, r, V;
     int64_t* out_ids; float* out_score; int64_t ld_out;
 };
-size_t argmax_ws_bytes(int64_t M, int64_t r, int64_t V);
+// Data-region bytes the argmax needs beyond the control area (counter + keys).
+size_t argmax_data_bytes(int64_t M, int64_t r, int64_t V);
 bool argmax_supported(int64_t M, int64_t r, int64_t V);
 hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, hipStream_t s);
 
-// ---- workspace fill ---------------------------------------------------------
+// ---- workspace fill and operand packing ---------------------------------------
 hipError_t launch_fill_zero(void* ws, size_t bytes, hipStream_t s);
+
+// MFMA-16 block layout: 16-row x 32-column blocks of 1 KiB in wave64 lane order.
+inline int64_t packed_row_blocks(int64_t rows) { return (rows + 15) / 16; }
+inline int64_t packed_col_blocks(int64_t cols) { return (cols + 31) / 32; }
+inline size_t packed_bytes(int64_t rows, int64_t cols) {
+    return (size_t)packed_row_blocks(rows) * packed_col_blocks(cols) * 1024;
+}
+hipError_t launch_pack_mfma16(const uint16_t* W, int64_t ldw, int64_t rows, int64_t cols, uint16_t* P,
+                              hipStream_t s);
 
 // Device properties of the current device (cached per device id).
 int device_cu_count();

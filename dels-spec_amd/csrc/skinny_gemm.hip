@@ -24,7 +24,7 @@ enum : int { EPI_RANK = 0, EPI_GRU = 1 };
 
 struct SkinnyKArgs {
     const uint16_t* x; int64_t ldx;     // [M, K]; NULL means an all-zero X (GRU zero state)
-    const uint16_t* w; int64_t ldw;     // [wrows, K]
+    const uint16_t* w; int64_t ldw;     // [wrows, K] row-major, or MFMA-16 blocks (WP)
     int M, K, wrows;
     int ncols;                          // output columns (N for rank, G for GRU)
     int ksteps, ksplit;
@@ -99,10 +99,12 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyKArgs& a, const floa
     }
 }
 
-template <int WM, int WN, int EPI>
+// WP: W is in the MFMA-16 block layout (zero-padded, so no masking and every
+// operand load is one contiguous KiB per wave).
+template <int WM, int WN, int EPI, bool WP>
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
     constexpr int T = WM * WN;
-    __shared__ float red[4 * T * 256];
+    __shared__ float red[2 * T * 256];
     __shared__ int s_last;
 
     const int lane = threadIdx.x & 63;
@@ -136,9 +138,15 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
         bool wok[WN];
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
-            const int n = wcol<EPI>(c0, j, a.ncols) + lrow;
-            wok[j] = (n - (EPI == EPI_GRU ? j * a.ncols : 0)) < a.ncols && n < a.wrows;
-            wp[j] = a.w + (int64_t)(wok[j] ? n : 0) * a.ldw + kg * 8;
+            const int c = wcol<EPI>(c0, j, a.ncols);   // first W row of sub-tile j (a multiple of 16)
+            if constexpr (WP) {
+                wok[j] = true;
+                wp[j] = a.w + ((int64_t)(c >> 4) * a.ksteps) * 512 + lane * 8;
+            } else {
+                const int n = c + lrow;
+                wok[j] = (n - (EPI == EPI_GRU ? j * a.ncols : 0)) < a.ncols && n < a.wrows;
+                wp[j] = a.w + (int64_t)(wok[j] ? n : 0) * a.ldw + kg * 8;
+            }
         }
         for (int s = ks0 + wave; s < ks1; s += 4) {
             const int k = s * 32;
@@ -147,7 +155,12 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
 #pragma unroll
             for (int i = 0; i < WM; ++i) xv[i] = (kok && xok[i]) ? load_bf16x8(xp[i] + k) : zero_bf16x8();
 #pragma unroll
-            for (int j = 0; j < WN; ++j) wv[j] = (kok && wok[j]) ? load_bf16x8_nt(wp[j] + k) : zero_bf16x8();
+            for (int j = 0; j < WN; ++j) {
+                if constexpr (WP)
+                    wv[j] = load_bf16x8_nt(wp[j] + (int64_t)s * 512);
+                else
+                    wv[j] = (kok && wok[j]) ? load_bf16x8_nt(wp[j] + k) : zero_bf16x8();
+            }
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -156,19 +169,39 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
         }
     }
 
-    // Sum the four waves in a fixed order through LDS.
+    // Sum the four waves through LDS in a fixed order: (w0 + w2) + (w1 + w3).
+    if (wave >= 2) {
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+        for (int i = 0; i < WM; ++i)
 #pragma unroll
-        for (int j = 0; j < WN; ++j)
-            *reinterpret_cast<f32x4*>(&red[((wave * T) + i * WN + j) * 256 + lane * 4]) = acc[i][j];
+            for (int j = 0; j < WN; ++j)
+                *reinterpret_cast<f32x4*>(&red[(((wave - 2) * T) + i * WN + j) * 256 + lane * 4]) = acc[i][j];
+    }
     __syncthreads();
-    for (int e = threadIdx.x; e < T * 256; e += blockDim.x) {
-        float v = red[e];
-        v += red[T * 256 + e];
-        v += red[2 * T * 256 + e];
-        v += red[3 * T * 256 + e];
-        red[e] = v;
+    if (wave < 2) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                acc[i][j] += *reinterpret_cast<const f32x4*>(&red[((wave * T) + i * WN + j) * 256 + lane * 4]);
+    }
+    __syncthreads();
+    if (wave == 1) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j)
+                *reinterpret_cast<f32x4*>(&red[(i * WN + j) * 256 + lane * 4]) = acc[i][j];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                f32x4* p = reinterpret_cast<f32x4*>(&red[(i * WN + j) * 256 + lane * 4]);
+                *p = acc[i][j] + *p;
+            }
     }
     __syncthreads();
 
@@ -229,46 +262,46 @@ SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
     int ks = (int)std::max<int64_t>(1, 256 / std::max(tiles, 1));
     ks = std::min(ks, std::max(1, p.ksteps / 4));
     p.ksplit = ks;
-    p.counter_bytes = p.ksplit > 1 ? (size_t)tiles * sizeof(unsigned int) : 0;
     p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * tiles * p.wm * p.wn * 256 * sizeof(float) : 0;
     return p;
 }
 
-static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+size_t skinny_data_bytes(const SkinnyPlan& p) { return align256(p.partial_bytes); }
 
-size_t skinny_ws_bytes(const SkinnyPlan& p) {
-    return align256(p.counter_bytes) + align256(p.partial_bytes);
-}
+bool skinny_supported(const SkinnyPlan& p) { return (int64_t)p.m_wg * p.n_wg <= kMaxCounters; }
 
 template <int WM, int WN, int EPI>
-static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, hipStream_t s) {
+static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, bool packed, hipStream_t s) {
     dim3 grid(p.n_wg, p.m_wg, p.ksplit);
-    hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI>), grid, dim3(256), 0, s, ka);
+    if (packed)
+        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, true>), grid, dim3(256), 0, s, ka);
+    else
+        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, false>), grid, dim3(256), 0, s, ka);
     return hipGetLastError();
 }
 
-static void fill_ws(SkinnyKArgs& ka, const SkinnyPlan& p, void* ws) {
+static void fill_ws(SkinnyKArgs& ka, const SkinnyPlan& p, void* ws, size_t data_off) {
     char* w = static_cast<char*>(ws);
-    ka.counters = p.counter_bytes ? reinterpret_cast<unsigned int*>(w) : nullptr;
-    ka.partial = p.partial_bytes ? reinterpret_cast<float*>(w + align256(p.counter_bytes)) : nullptr;
+    ka.counters = reinterpret_cast<unsigned int*>(w + kCountersOff);
+    ka.partial = p.ksplit > 1 ? reinterpret_cast<float*>(w + data_off) : nullptr;
     ka.ksteps = p.ksteps;
     ka.ksplit = p.ksplit;
 }
 
-hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s) {
+hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s) {
     SkinnyKArgs ka{};
     ka.x = a.h; ka.ldx = a.ldh;
     ka.w = a.A; ka.ldw = a.lda;
     ka.M = a.M; ka.K = a.d; ka.wrows = a.r; ka.ncols = a.r;
     ka.bias = a.bias; ka.act = a.act;
     ka.out = a.rank; ka.ldout = a.ldrank;
-    fill_ws(ka, p, ws);
-    if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, s);
-    if (p.wm == 2) return launch_skinny<2, 2, EPI_RANK>(ka, p, s);
-    return launch_skinny<4, 4, EPI_RANK>(ka, p, s);
+    fill_ws(ka, p, ws, data_off);
+    if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, a.a_packed, s);
+    if (p.wm == 2) return launch_skinny<2, 2, EPI_RANK>(ka, p, a.a_packed, s);
+    return launch_skinny<4, 4, EPI_RANK>(ka, p, a.a_packed, s);
 }
 
-hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, hipStream_t s) {
+hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s) {
     SkinnyKArgs ka{};
     ka.x = a.h_in; ka.ldx = a.ldh_in;
     ka.w = a.w_hh; ka.ldw = a.G;
@@ -280,10 +313,10 @@ hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, hipS
     // A zero state needs no K loop: every workgroup runs the epilogue alone.
     SkinnyPlan q = p;
     if (a.h_in == nullptr) q.ksplit = 1;
-    fill_ws(ka, q, ws);
-    if (q.wm == 1) return launch_skinny<1, 3, EPI_GRU>(ka, q, s);
-    if (q.wm == 2) return launch_skinny<2, 3, EPI_GRU>(ka, q, s);
-    return launch_skinny<4, 3, EPI_GRU>(ka, q, s);
+    fill_ws(ka, q, ws, data_off);
+    if (q.wm == 1) return launch_skinny<1, 3, EPI_GRU>(ka, q, a.w_packed, s);
+    if (q.wm == 2) return launch_skinny<2, 3, EPI_GRU>(ka, q, a.w_packed, s);
+    return launch_skinny<4, 3, EPI_GRU>(ka, q, a.w_packed, s);
 }
 
 }  // namespace dels

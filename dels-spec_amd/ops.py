@@ -17,7 +17,8 @@ Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
 from __future__ import annotations
 
 import threading
-from typing import Iterable, Optional, Sequence, Union
+from dataclasses import dataclass
+from typing import Optional, Sequence, Union
 
 import torch
 
@@ -53,6 +54,56 @@ def _require_bf16_matrix(t: torch.Tensor, name: str, rows: Optional[int] = None,
         raise ValueError(f"{name} has {t.shape[1]} columns, expected {cols}")
     if t.shape[1] > 1 and t.stride(1) != 1:
         raise ValueError(f"{name} must have unit column stride")
+
+
+@dataclass
+class PackedWeight:
+    """A bf16 [rows, cols] weight stored in the MFMA-16 block layout.
+
+    16-row x 32-column blocks of 1 KiB in wave64 lane order (include/dels.h,
+    DELS_LAYOUT_MFMA16): every MFMA operand load of the kernels then reads one
+    contiguous KiB.  Produced by ``pack_operand``.
+    """
+
+    data: torch.Tensor
+    rows: int
+    cols: int
+
+    @property
+    def shape(self) -> tuple[int, int]:
+        return (self.rows, self.cols)
+
+    @property
+    def device(self) -> torch.device:
+        return self.data.device
+
+
+Weight = Union[torch.Tensor, PackedWeight]
+
+
+def pack_operand(W: torch.Tensor) -> PackedWeight:
+    """Repack a bf16 [rows, cols] GPU matrix into the MFMA-16 block layout."""
+    _require_bf16_matrix(W, "W")
+    rows, cols = W.shape
+    lib = _lib.load()
+    nbytes = max(int(lib.dels_packed_bytes(rows, cols)), 16)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=W.device)
+    _lib.check(lib.dels_pack_operand(W.data_ptr(), W.stride(0), rows, cols, buf.data_ptr(), buf.numel(),
+                                     _stream_ptr(W.device)), "dels_pack_operand")
+    return PackedWeight(buf, int(rows), int(cols))
+
+
+def _weight(w: Weight, name: str, cols: Optional[int] = None, rows: Optional[int] = None):
+    """(pointer, leading dimension, layout code, rows, cols) of a weight operand."""
+    if isinstance(w, PackedWeight):
+        _require_cuda(w.data, name)
+        if cols is not None and w.cols != cols:
+            raise ValueError(f"{name} has {w.cols} columns, expected {cols}")
+        if rows is not None and w.rows != rows:
+            raise ValueError(f"{name} has {w.rows} rows, expected {rows}")
+        return w.data.data_ptr(), 0, _lib.LAYOUT_MFMA16, w.rows, w.cols
+    _require_bf16_matrix(w, name, rows=rows, cols=cols)
+    return w.data_ptr(), w.stride(0), _lib.LAYOUT_ROWMAJOR, int(w.shape[0]), int(w.shape[1])
 
 
 class _Workspaces:
@@ -160,22 +211,20 @@ def _outputs(out_ids, out_score, M, dev):
     return out_ids, out_score, ld
 
 
-def rank_proj(h: torch.Tensor, rank_weight: torch.Tensor, rank_bias: Optional[torch.Tensor] = None,
+def rank_proj(h: torch.Tensor, rank_weight: Weight, rank_bias: Optional[torch.Tensor] = None,
               act: str = "identity", *, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``rank = act(F.linear(h, rank_weight, rank_bias))`` in bf16 (code/kernel/dels.py:437-443)."""
+    """``rank = act(F.linear(h, rank_weight, rank_bias))`` in bf16 (code/kernel/dels.py:437-443).
+
+    ``rank_weight`` is A [r, d] bf16, row-major or packed (``pack_operand``).
+    """
     if act not in _ACTS:
         raise ValueError(f"Unsupported DeLS rank_activation={act!r}.")
     if h.dim() == 1:
         h = h.unsqueeze(0)
     M, d = h.shape
     _require_bf16_matrix(h, "h", cols=d)
-    _require_bf16_matrix(rank_weight, "rank_weight", cols=d)
-    r = rank_weight.shape[0]
-    if rank_bias is not None:
-        _require_cuda(rank_bias, "rank_bias")
-        if rank_bias.dtype != torch.bfloat16 or rank_bias.numel() != r:
-            raise ValueError("rank_bias must be a bfloat16 vector of length r")
-        rank_bias = rank_bias.contiguous()
+    a_ptr, lda, a_lay, r, _ = _weight(rank_weight, "rank_weight", cols=d)
+    rank_bias = _bias(rank_bias, r)
     if out is None:
         out = torch.empty(M, r, dtype=torch.bfloat16, device=h.device)
     else:
@@ -183,30 +232,38 @@ def rank_proj(h: torch.Tensor, rank_weight: torch.Tensor, rank_bias: Optional[to
     lib = _lib.load()
     nbytes = lib.dels_rank_proj_ws_bytes(M, d, r)
     ws = workspace(h.device, nbytes)
-    _lib.check(lib.dels_rank_proj(h.data_ptr(), h.stride(0), rank_weight.data_ptr(), rank_weight.stride(0),
+    _lib.check(lib.dels_rank_proj(h.data_ptr(), h.stride(0), a_ptr, lda, a_lay,
                                   rank_bias.data_ptr() if rank_bias is not None else None, _ACTS[act],
                                   M, d, r, out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(),
                                   _stream_ptr(h.device)), "dels_rank_proj")
     return out
 
 
-def fused_argmax(rank: torch.Tensor, lm_head_weight: torch.Tensor, base_logits: torch.Tensor,
+def _bias(rank_bias: Optional[torch.Tensor], r: int) -> Optional[torch.Tensor]:
+    if rank_bias is None:
+        return None
+    _require_cuda(rank_bias, "rank_bias")
+    if rank_bias.dtype != torch.bfloat16 or rank_bias.numel() != r:
+        raise ValueError("rank_bias must be a bfloat16 vector of length r")
+    return rank_bias.contiguous()
+
+
+def fused_argmax(rank: torch.Tensor, lm_head_weight: Weight, base_logits: torch.Tensor,
                  baseline_logits: Optional[torch.Tensor] = None, alpha: Scalars = 1.0, beta: Scalars = 0.0,
                  *, out_ids: Optional[torch.Tensor] = None,
                  out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Per-row argmax of ``rank.B^T * alpha + base - beta * prior`` (code/kernel/dels.py:15-138).
 
-    ``rank`` [M, r] bf16; ``lm_head_weight`` B [V, r] bf16; ``base_logits`` an
-    [M, V] view (any row stride) in fp32/bf16/fp16; ``baseline_logits`` the
-    prior [V] (or None); ``alpha``/``beta`` scalars, length-M sequences or
-    device tensors.  Returns ``(ids int64[M], score fp32[M])``.
+    ``rank`` [M, r] bf16; ``lm_head_weight`` B [V, r] bf16 (row-major or
+    packed); ``base_logits`` an [M, V] view (any row stride) in fp32/bf16/fp16;
+    ``baseline_logits`` the prior [V] (or None); ``alpha``/``beta`` scalars,
+    length-M sequences or device tensors.  Returns ``(ids int64[M], score fp32[M])``.
     """
     if rank.dim() == 1:
         rank = rank.unsqueeze(0)
     M, r = rank.shape
     _require_bf16_matrix(rank, "rank", cols=r)
-    _require_bf16_matrix(lm_head_weight, "lm_head_weight", cols=r)
-    V = lm_head_weight.shape[0]
+    b_ptr, ldb, b_lay, V, _ = _weight(lm_head_weight, "lm_head_weight", cols=r)
     base = _base_view(base_logits, M, V)
     prior = _prior_view(baseline_logits, V)
     dev = rank.device
@@ -216,7 +273,7 @@ def fused_argmax(rank: torch.Tensor, lm_head_weight: torch.Tensor, base_logits: 
     lib = _lib.load()
     ws = workspace(dev, lib.dels_fused_argmax_ws_bytes(M, r, V))
     _lib.check(lib.dels_fused_argmax(
-        rank.data_ptr(), rank.stride(0), lm_head_weight.data_ptr(), lm_head_weight.stride(0),
+        rank.data_ptr(), rank.stride(0), b_ptr, ldb, b_lay,
         base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
         prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
         a.data_ptr(), a_s, b.data_ptr(), b_s, M, r, V,
@@ -225,15 +282,16 @@ def fused_argmax(rank: torch.Tensor, lm_head_weight: torch.Tensor, base_logits: 
     return out_ids, out_score
 
 
-def lowrank_argmax(h: torch.Tensor, rank_weight: torch.Tensor, lm_head_weight: torch.Tensor,
+def lowrank_argmax(h: torch.Tensor, rank_weight: Weight, lm_head_weight: Weight,
                    base_logits: torch.Tensor, baseline_logits: Optional[torch.Tensor] = None,
                    alpha: Scalars = 1.0, beta: Scalars = 0.0, act: str = "identity",
                    rank_bias: Optional[torch.Tensor] = None, *, out_ids: Optional[torch.Tensor] = None,
                    out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """One DeLS draft step: rank projection of ``h`` then the fused argmax.
 
-    ``h`` [M, d] bf16, ``rank_weight`` A [r, d] bf16, ``lm_head_weight`` B [V, r]
-    bf16 (code/kernel/dels.py:437-446).  Returns ``(ids int64[M], score fp32[M])``.
+    ``h`` [M, d] bf16, ``rank_weight`` A [r, d] and ``lm_head_weight`` B [V, r]
+    bf16, each row-major or packed (code/kernel/dels.py:437-446).  Returns
+    ``(ids int64[M], score fp32[M])``.
     """
     if act not in _ACTS:
         raise ValueError(f"Unsupported DeLS rank_activation={act!r}.")
@@ -241,17 +299,11 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: torch.Tensor, lm_head_weight: t
         h = h.unsqueeze(0)
     M, d = h.shape
     _require_bf16_matrix(h, "h", cols=d)
-    _require_bf16_matrix(rank_weight, "rank_weight", cols=d)
-    r = rank_weight.shape[0]
-    _require_bf16_matrix(lm_head_weight, "lm_head_weight", cols=r)
-    V = lm_head_weight.shape[0]
+    a_ptr, lda, a_lay, r, _ = _weight(rank_weight, "rank_weight", cols=d)
+    b_ptr, ldb, b_lay, V, _ = _weight(lm_head_weight, "lm_head_weight", cols=r)
     base = _base_view(base_logits, M, V)
     prior = _prior_view(baseline_logits, V)
-    if rank_bias is not None:
-        _require_cuda(rank_bias, "rank_bias")
-        if rank_bias.dtype != torch.bfloat16 or rank_bias.numel() != r:
-            raise ValueError("rank_bias must be a bfloat16 vector of length r")
-        rank_bias = rank_bias.contiguous()
+    rank_bias = _bias(rank_bias, r)
     dev = h.device
     a, a_s = _rows_param(alpha, M, dev, "alpha")
     b, b_s = _rows_param(beta, M, dev, "beta")
@@ -259,9 +311,9 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: torch.Tensor, lm_head_weight: t
     lib = _lib.load()
     ws = workspace(dev, lib.dels_lowrank_argmax_ws_bytes(M, d, r, V))
     _lib.check(lib.dels_lowrank_argmax(
-        h.data_ptr(), h.stride(0), rank_weight.data_ptr(), rank_weight.stride(0),
+        h.data_ptr(), h.stride(0), a_ptr, lda, a_lay,
         rank_bias.data_ptr() if rank_bias is not None else None, _ACTS[act],
-        lm_head_weight.data_ptr(), lm_head_weight.stride(0),
+        b_ptr, ldb, b_lay,
         base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
         prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
         a.data_ptr(), a_s, b.data_ptr(), b_s, M, d, r, V,
@@ -271,13 +323,13 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: torch.Tensor, lm_head_weight: t
 
 
 def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.Tensor],
-             w_hh: torch.Tensor, b_hh: Optional[torch.Tensor] = None, *,
+             w_hh: Weight, b_hh: Optional[torch.Tensor] = None, *,
              out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``h_out = GRUCell(gi_table[tokens], h_in)`` with bf16 state (code/kernel/dels.py:359-373).
 
     ``gi_table`` [rows, 3G] bf16 is ``F.linear(E, W_ih, b_ih)``; ``tokens`` [B]
     int64 (a strided view is fine); ``h_in`` [B, G] bf16 or None for zeros;
-    ``w_hh`` [3G, G] bf16; ``b_hh`` [3G] bf16 or None.
+    ``w_hh`` [3G, G] bf16 (row-major contiguous or packed); ``b_hh`` [3G] bf16 or None.
     """
     _require_cuda(tokens, "tokens")
     if tokens.dtype != torch.int64:
@@ -285,8 +337,8 @@ def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.
     tokens = tokens.reshape(-1) if tokens.dim() != 1 else tokens
     nb = tokens.numel()
     G = w_hh.shape[1]
-    _require_bf16_matrix(w_hh, "w_hh", rows=3 * G, cols=G)
-    if not w_hh.is_contiguous():
+    w_ptr, ldw, w_lay, _, _ = _weight(w_hh, "w_hh", rows=3 * G, cols=G)
+    if w_lay == _lib.LAYOUT_ROWMAJOR and ldw != G:
         raise ValueError("w_hh must be contiguous")
     _require_bf16_matrix(gi_table, "gi_table", cols=3 * G)
     if h_in is not None:
@@ -295,7 +347,7 @@ def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.
         if b_hh.dtype != torch.bfloat16 or b_hh.numel() != 3 * G:
             raise ValueError("b_hh must be a bfloat16 vector of length 3G")
         b_hh = b_hh.contiguous()
-    dev = w_hh.device
+    dev = tokens.device
     if out is None:
         out = torch.empty(nb, G, dtype=torch.bfloat16, device=dev)
     else:
@@ -305,6 +357,6 @@ def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.
     _lib.check(lib.dels_gru_step(
         gi_table.data_ptr(), gi_table.stride(0), gi_table.shape[0], tokens.data_ptr(), tokens.stride(0),
         h_in.data_ptr() if h_in is not None else None, h_in.stride(0) if h_in is not None else G,
-        w_hh.data_ptr(), b_hh.data_ptr() if b_hh is not None else None, nb, G,
+        w_ptr, w_lay, b_hh.data_ptr() if b_hh is not None else None, nb, G,
         out.data_ptr(), out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_gru_step")
     return out

@@ -19,7 +19,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .ops import _DTYPES, new_workspace
+from .ops import _DTYPES, new_workspace, pack_operand
 
 _ACT_CODES = {"identity": _lib.ACT_IDENTITY, "silu": _lib.ACT_SILU}
 
@@ -96,6 +96,12 @@ class DeLSGraphRunner:
                 raise ValueError(
                     "DeLS local-head vocab size does not match the runner: "
                     f"local_head={self.lm_head_weight.shape[0]}, vocab={self.vocab_size}.")
+            # Weights the rollout streams every step, repacked once into the MFMA-16 block layout.
+            self._packed = self.gru_hidden_dim % 16 == 0
+            if self._packed:
+                self._w_hh_p = pack_operand(self.gru_w_hh)
+                self._rank_w_p = pack_operand(self.rank_weight)
+                self._lm_w_p = pack_operand(self.lm_head_weight)
 
             B, G, r, V, S = self.batch_size, self.gru_hidden_dim, self.rank_dim, self.vocab_size, self.steps
             self.static_prefix_ids = torch.zeros(B, 1, dtype=torch.long, device=device)
@@ -116,17 +122,18 @@ class DeLSGraphRunner:
         p.gi_table = self._gru_input_proj_table.data_ptr()
         p.ld_gi = self._gru_input_proj_table.stride(0)
         p.table_rows = self._gru_input_proj_table.shape[0]
-        p.w_hh = self.gru_w_hh.data_ptr()
+        p.w_hh = self._w_hh_p.data.data_ptr() if self._packed else self.gru_w_hh.data_ptr()
         p.b_hh = self.gru_b_hh.data_ptr() if self.gru_b_hh is not None else None
-        p.rank_w = self.rank_weight.data_ptr()
+        p.rank_w = self._rank_w_p.data.data_ptr() if self._packed else self.rank_weight.data_ptr()
         p.rank_b = self.rank_bias.data_ptr() if self.rank_bias is not None else None
         p.act = self._act
-        p.lm_w = self.lm_head_weight.data_ptr()
+        p.lm_w = self._lm_w_p.data.data_ptr() if self._packed else self.lm_head_weight.data_ptr()
         p.prior = prior.data_ptr() if prior is not None else None
         p.prior_dtype = _DTYPES[dtype]
         p.alpha = self._alpha.data_ptr()
         p.beta = self._beta.data_ptr()
         p.batch, p.steps, p.G, p.r, p.V = B, S, G, r, V
+        p.weights_layout = _lib.LAYOUT_MFMA16 if self._packed else _lib.LAYOUT_ROWMAJOR
         p.prefix_ids = self.static_prefix_ids.data_ptr()
         p.base = self.static_base_logits.data_ptr()
         p.base_dtype = _DTYPES[dtype]

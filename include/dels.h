@@ -57,12 +57,35 @@ extern "C" {
 #define DELS_ACT_IDENTITY 0
 #define DELS_ACT_SILU 1
 
+/*
+ * Weight layouts.  DELS_LAYOUT_ROWMAJOR: [rows, cols] row-major with a leading
+ * dimension.  DELS_LAYOUT_MFMA16: the "MFMA-16 block" layout written by
+ * dels_pack_operand -- the matrix is cut into 16-row x 32-column blocks (rows
+ * padded to 16, columns to 32, with zeros), blocks stored row-block-major, and
+ * each 1 KiB block in wave64 lane order (lane l holds the 8 elements of row
+ * l%16 at columns 8*(l/16)..+7 of the block), so every 16-byte-per-lane load of
+ * an MFMA operand reads one contiguous KiB of HBM.  Leading dimensions are
+ * ignored for packed operands.
+ */
+#define DELS_LAYOUT_ROWMAJOR 0
+#define DELS_LAYOUT_MFMA16 1
+
 int dels_abi_version(void);
 const char* dels_strerror(int status);
 const char* dels_last_error(void);
 
 /* Zero-fill a workspace on `stream` with a fill kernel (capture-safe). */
 int dels_workspace_init(void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * Repack a bf16 [rows, cols] row-major weight into the MFMA-16 block layout
+ * (no counterpart in the reference, whose runner keeps .contiguous() copies of
+ * the same weights, code/kernel/dels.py:260-276).  `packed` must hold
+ * dels_packed_bytes(rows, cols) bytes and be 16-byte aligned.
+ */
+size_t dels_packed_bytes(int64_t rows, int64_t cols);
+int dels_pack_operand(const void* W, int64_t ldw, int64_t rows, int64_t cols,
+                      void* packed, size_t packed_bytes, void* stream);
 
 /*
  * Rank projection rank = bf16(act(bf16(h . A^T + bias)))  [M, r] bf16.
@@ -72,7 +95,7 @@ int dels_workspace_init(void* ws, size_t ws_bytes, void* stream);
  *   h [M, d] bf16 (ldh), A [r, d] bf16 (lda), bias [r] bf16 or NULL.
  */
 size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r);
-int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda,
+int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout,
                    const void* bias, int act, int64_t M, int64_t d, int64_t r,
                    void* rank, int64_t ldrank, void* ws, size_t ws_bytes, void* stream);
 
@@ -80,7 +103,7 @@ int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda,
  * Fused low-rank LM-head combine + vocabulary argmax, given rank.
  * Replaces _fused_low_rank_argmax_kernel + _reduce_argmax_kernel as launched
  * by DeLSGraphRunner._argmax_step_triton (code/kernel/dels.py:15-138, 375-423).
- *   rank  [M, r] bf16 (ldrank)          B     [V, r] bf16 (ldb)
+ *   rank  [M, r] bf16 (ldrank)          B     [V, r] bf16 (ldb, b_layout)
  *   base  [M, V] base_dtype (ldbase)    prior [V] prior_dtype, or NULL
  *   alpha/beta: fp32 device arrays read at alpha[m*alpha_stride] (stride 0
  *   broadcasts one value).  The prior term is applied to row m only when
@@ -90,7 +113,7 @@ int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda,
  * returns id 0 with score -inf.
  */
 size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V);
-int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb,
+int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb, int b_layout,
                       const void* base, int64_t ldbase, int base_dtype,
                       const void* prior, int prior_dtype,
                       const float* alpha, int64_t alpha_stride,
@@ -105,9 +128,9 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
  * lives in the workspace.
  */
 size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V);
-int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda,
+int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout,
                         const void* bias, int act,
-                        const void* B, int64_t ldb,
+                        const void* B, int64_t ldb, int b_layout,
                         const void* base, int64_t ldbase, int base_dtype,
                         const void* prior, int prior_dtype,
                         const float* alpha, int64_t alpha_stride,
@@ -123,14 +146,14 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda,
  *   gi_table [table_rows, 3G] bf16 (ld_gi) = F.linear(E, W_ih, b_ih);
  *   tokens[b*tok_stride] int64 (clamped to [0, table_rows) before use);
  *   h_in [batch, G] bf16 (ldh_in) or NULL for a zero state;
- *   w_hh [3G, G] bf16, b_hh [3G] bf16 or NULL; h_out [batch, G] bf16.
+ *   w_hh [3G, G] bf16 in w_layout, b_hh [3G] bf16 or NULL; h_out [batch, G] bf16.
  * Gate order (r, z, n) as torch.nn.GRU; gh = bf16(h . W_hh^T + b_hh).
  */
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G);
 int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows,
                   const int64_t* tokens, int64_t tok_stride,
                   const void* h_in, int64_t ldh_in,
-                  const void* w_hh, const void* b_hh,
+                  const void* w_hh, int w_layout, const void* b_hh,
                   int64_t batch, int64_t G,
                   void* h_out, int64_t ldh_out,
                   void* ws, size_t ws_bytes, void* stream);
@@ -157,6 +180,7 @@ typedef struct dels_rollout {
     const float* alpha;     /* [steps] fp32 */
     const float* beta;      /* [steps] fp32 */
     int64_t batch, steps, G, r, V;
+    int weights_layout;     /* DELS_LAYOUT_* of w_hh, rank_w and lm_w */
     const int64_t* prefix_ids; /* [batch] int64 */
     const void* base;       /* [batch, steps, V] */
     int base_dtype;

@@ -67,37 +67,38 @@ def test_workspace_sizes(pkg):
     w = lib.dels_lowrank_argmax_ws_bytes(16, 4096, 512, 151936)
     assert w >= lib.dels_fused_argmax_ws_bytes(16, 512, 151936) + 16 * 512 * 2
     assert w % 256 == 0
-    assert lib.dels_rollout_ws_bytes(8, 1024, 512, 151936) > lib.dels_gru_step_ws_bytes(8, 1024)
+    assert lib.dels_rollout_ws_bytes(8, 1024, 512, 151936) >= lib.dels_gru_step_ws_bytes(8, 1024)
+    assert lib.dels_fused_argmax_ws_bytes(1, 8, 1) == 65536   # the shared control area
     assert lib.dels_rank_proj_ws_bytes(1, 64, 64) >= 0
 
 
 def test_argument_errors_return_codes(pkg):
     lib = pkg._lib.load()
     # NULL operands
-    rc = lib.dels_fused_argmax(None, 512, None, 512, None, 100, 0, None, 0, None, 0, None, 0, 16, 512, 100,
+    rc = lib.dels_fused_argmax(None, 512, None, 512, 0, None, 100, 0, None, 0, None, 0, None, 0, 16, 512, 100,
                                None, None, 1, None, 0, None)
     assert rc == -1 and b"rank is NULL" in lib.dels_last_error()
     # unsupported rank dimension
-    rc = lib.dels_fused_argmax(None, 0, None, 0, None, 0, 0, None, 0, None, 0, None, 0, 4, 1024, 100,
+    rc = lib.dels_fused_argmax(None, 0, None, 0, 0, None, 0, 0, None, 0, None, 0, None, 0, 4, 1024, 100,
                                None, None, 1, None, 0, None)
     assert rc == -2
     # misaligned operand (a fake, never-dereferenced address)
-    rc = lib.dels_fused_argmax(0x1002, 64, 0x2000, 64, 0x3000, 100, 0, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
+    rc = lib.dels_fused_argmax(0x1002, 64, 0x2000, 64, 0, 0x3000, 100, 0, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
                                100, 0x5000, None, 1, 0x6000, 4096, None)
     assert rc == -3
     # workspace too small
-    rc = lib.dels_fused_argmax(0x1000, 64, 0x2000, 64, 0x3000, 100, 0, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
+    rc = lib.dels_fused_argmax(0x1000, 64, 0x2000, 64, 0, 0x3000, 100, 0, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
                                100, 0x5000, None, 1, 0x6000, 16, None)
     assert rc == -4 and b"too small" in lib.dels_last_error()
     # bad base dtype
-    rc = lib.dels_fused_argmax(0x1000, 64, 0x2000, 64, 0x3000, 100, 7, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
+    rc = lib.dels_fused_argmax(0x1000, 64, 0x2000, 64, 0, 0x3000, 100, 7, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
                                100, 0x5000, None, 1, 0x6000, 4096, None)
     assert rc == -1
     # GRU: aliasing in/out, batch too large
-    rc = lib.dels_gru_step(0x1000, 96, 10, 0x2000, 1, 0x3000, 32, 0x4000, None, 2, 32, 0x3000, 32, 0x5000,
+    rc = lib.dels_gru_step(0x1000, 96, 10, 0x2000, 1, 0x3000, 32, 0x4000, 0, None, 2, 32, 0x3000, 32, 0x5000,
                            1 << 20, None)
     assert rc == -1 and b"alias" in lib.dels_last_error()
-    rc = lib.dels_gru_step(0x1000, 96, 10, 0x2000, 1, 0x3000, 32, 0x4000, None, 65, 32, 0x6000, 32, 0x5000,
+    rc = lib.dels_gru_step(0x1000, 96, 10, 0x2000, 1, 0x3000, 32, 0x4000, 0, None, 65, 32, 0x6000, 32, 0x5000,
                            1 << 20, None)
     assert rc == -2
     # rollout: NULL params, steps <= 0
@@ -110,6 +111,12 @@ def test_argument_errors_return_codes(pkg):
     assert lib.dels_graph_create(ctypes.byref(p), ctypes.byref(h)) == -1 and not h.value
     assert lib.dels_graph_launch(None, None) == -1
     assert lib.dels_graph_destroy(None) == 0
+    # unknown weight layout; packing into a too-small buffer
+    rc = lib.dels_fused_argmax(0x1000, 64, 0x2000, 64, 7, 0x3000, 100, 0, None, 0, 0x4000, 0, 0x4000, 0, 2, 64,
+                               100, 0x5000, None, 1, 0x6000, 1 << 16, None)
+    assert rc == -1 and b"layout" in lib.dels_last_error()
+    assert lib.dels_packed_bytes(17, 40) == 2 * 2 * 1024
+    assert lib.dels_pack_operand(0x1000, 40, 17, 40, 0x8000, 1024, None) == -1
 
 
 def test_python_errors_before_the_gpu(pkg):
