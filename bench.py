@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--also-m512", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 512 MiB buffer 8 times (scale reference for HBM byte counters)")
     ap.add_argument("--layout", default="packed", choices=["packed", "rowmajor"],
                     help="weights in the MFMA-16 block layout (as the runner stores them) or row-major")
     ap.add_argument("--traffic-file", default=os.path.join(REPO_DIR, "profiles", "traffic.json"))
@@ -139,6 +141,7 @@ def bench_workload(pkg, name, args, dev, torch):
             for _ in range(nsets)]
     ranks = [torch.empty(M, r, dtype=torch.bfloat16, device=dev) for _ in range(nsets)]
     if args.layout == "packed":
+        # as the runner stores them: both weights in the MFMA-16 block layout
         weights = [(pkg.pack_operand(x.A), pkg.pack_operand(x.B)) for x in sets]
     else:
         weights = [(x.A, x.B) for x in sets]
@@ -239,10 +242,18 @@ def main():
 
     import __graft_entry__
 
-    pkg = __graft_entry__.load_package()
-    pkg._lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.ones(512 * 2**20 // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize(dev)
+        print(json.dumps({"copy_calibration_bytes_per_copy": src.numel() * 4, "copies": 8}))
+        return
+    pkg = __graft_entry__.load_package()
+    pkg._lib.load()
 
     rec, x0 = bench_workload(pkg, args.workload, args, dev, torch)
     traffic = None

@@ -22,6 +22,8 @@ namespace dels {
 
 enum : int { EPI_RANK = 0, EPI_GRU = 1 };
 
+constexpr int kMaxKSplit = 16;   // workgroups per output tile along K (loads unrolled to this)
+
 struct SkinnyKArgs {
     const uint16_t* x; int64_t ldx;     // [M, K]; NULL means an all-zero X (GRU zero state)
     const uint16_t* w; int64_t ldw;     // [wrows, K] row-major, or MFMA-16 blocks (WP)
@@ -210,28 +212,40 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
         return;
     }
 
-    // Split K: publish the partial tile, the last workgroup reduces.
+    // Split K: publish the partial tile, the last workgroup reduces.  No cache
+    // fences: the partials are written and read with device-scope (coherent)
+    // atomic stores/loads, every store is waited for before the one counter
+    // read-modify-write, and the summation runs in split order, so the result
+    // does not depend on which workgroup arrives last.
     const int tile_id = blockIdx.y * gridDim.x + blockIdx.x;
     const int ntile = gridDim.x * gridDim.y;
     float* mine = a.partial + ((int64_t)z * ntile + tile_id) * (T * 256);
-    for (int e = threadIdx.x; e < T * 256; e += blockDim.x) mine[e] = red[e];
-    __threadfence();
+    for (int e = threadIdx.x; e < T * 256; e += blockDim.x)
+        __hip_atomic_store(mine + e, red[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);   // the stores above have reached device coherence
     __syncthreads();
     if (threadIdx.x == 0) {
-        const unsigned prev = atomicAdd(&a.counters[tile_id], 1u);
+        const unsigned prev = __hip_atomic_fetch_add(&a.counters[tile_id], 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == (unsigned)(a.ksplit - 1));
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     for (int e = threadIdx.x; e < T * 256; e += blockDim.x) {
+        // all split loads in flight at once, then the sum in split order
+        float p[kMaxKSplit];
+#pragma unroll
+        for (int zz = 0; zz < kMaxKSplit; ++zz)
+            p[zz] = zz < a.ksplit ? __hip_atomic_load(a.partial + ((int64_t)zz * ntile + tile_id) * (T * 256) + e,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : 0.f;
         float v = 0.f;
-        for (int zz = 0; zz < a.ksplit; ++zz)
-            v += __hip_atomic_load(a.partial + ((int64_t)zz * ntile + tile_id) * (T * 256) + e,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int zz = 0; zz < kMaxKSplit; ++zz) v += p[zz];
         red[e] = v;
     }
-    if (threadIdx.x == 0) atomic_store_u32(&a.counters[tile_id], 0u);
+    if (threadIdx.x == 0)
+        __hip_atomic_exchange(&a.counters[tile_id], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     skinny_epilogue<WM, WN, EPI>(a, red, m0, c0);
 }
@@ -261,7 +275,7 @@ SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
     // Aim for about 256 workgroups with at least one K step per wave.
     int ks = (int)std::max<int64_t>(1, 256 / std::max(tiles, 1));
     ks = std::min(ks, std::max(1, p.ksteps / 4));
-    p.ksplit = ks;
+    p.ksplit = std::min(ks, kMaxKSplit);
     p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * tiles * p.wm * p.wn * 256 * sizeof(float) : 0;
     return p;
 }

@@ -208,19 +208,21 @@ def test_packed_equals_rowmajor(pkg, dev, M, r, V, bdt):
     x = pkg.synth.lowrank_inputs(M, 1024, r, V, base_dtype=bdt, prior_dtype=bdt, seed=M + r, act="silu")
     xd = x.to(dev)
     Ap, Bp = pkg.pack_operand(xd.A), pkg.pack_operand(xd.B)
-    row = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta, act="silu")
-    row = (row[0].clone(), row[1].clone())
-    pk = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act="silu")
-    torch.testing.assert_close(pk[0], row[0], rtol=0, atol=0)
-    torch.testing.assert_close(pk[1], row[1], rtol=0, atol=0)
+    # same rank, B row-major vs packed: the same kernel family and K order -> identical
     rank_row = pkg.rank_proj(xd.h, xd.A, None, "silu").clone()
+    fa_row = pkg.fused_argmax(rank_row, xd.B, xd.base, xd.prior, xd.alpha, xd.beta)
+    fa_row = (fa_row[0].clone(), fa_row[1].clone())
+    fa_pk = pkg.fused_argmax(rank_row, Bp, xd.base, xd.prior, xd.alpha, xd.beta)
+    torch.testing.assert_close(fa_pk[0], fa_row[0], rtol=0, atol=0)
+    torch.testing.assert_close(fa_pk[1], fa_row[1], rtol=0, atol=0)
+    # packed A may run a different rank-projection kernel: equal up to accumulation order
     rank_pk = pkg.rank_proj(xd.h, Ap, None, "silu")
-    torch.testing.assert_close(rank_pk, rank_row, rtol=0, atol=0)
-    fa = pkg.fused_argmax(rank_pk, Bp, xd.base, xd.prior, xd.alpha, xd.beta)
-    torch.testing.assert_close(fa[0], row[0], rtol=0, atol=0)
+    assert (bf16_ulps(f(rank_pk), f(rank_row)) > 0).mean() < 2e-3
+    pk = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act="silu")
     torch.cuda.synchronize()
     rank = oracle.rank_proj(f(x.h), f(x.A), None, "silu")
     assert_parity(pk[0], pk[1], rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
+    assert_parity(fa_row[0], fa_row[1], f(rank_row), f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
 
 
 def test_packed_gru_equals_rowmajor(pkg, dev):
