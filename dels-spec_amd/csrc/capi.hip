@@ -82,7 +82,7 @@ static int check_weight(const void* p, int64_t ld, int64_t cols, int layout, con
 
 // Every layout starts with the shared control area [0, kCtrlBytes).
 struct LowrankLayout {
-    size_t rank_off, part_off, total;
+    size_t rank_off, part_off, argmax_off, total;
     SkinnyPlan plan;
 };
 
@@ -91,12 +91,13 @@ static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) 
     L.plan = plan_skinny(M, d, r, false);
     L.rank_off = kCtrlBytes;
     L.part_off = L.rank_off + align256((size_t)M * r * 2);
-    L.total = L.part_off + skinny_data_bytes(L.plan) + align256(argmax_data_bytes(M, r, V));
+    L.argmax_off = L.part_off + skinny_data_bytes(L.plan);
+    L.total = L.argmax_off + align256(argmax_data_bytes(M, r, V));
     return L;
 }
 
 struct RolloutLayout {
-    size_t part_off, total;   // rank projection and GRU steps run in turn and share the partials
+    size_t part_off, argmax_off, total;   // rank projection and GRU steps run in turn and share the partials
     SkinnyPlan rank_plan, gru_plan;
 };
 
@@ -105,8 +106,8 @@ static RolloutLayout rollout_layout(int64_t batch, int64_t G, int64_t r, int64_t
     L.rank_plan = plan_skinny(batch, G, r, false);
     L.gru_plan = plan_skinny(batch, G, G, true);
     L.part_off = kCtrlBytes;
-    L.total = L.part_off + std::max(skinny_data_bytes(L.rank_plan), skinny_data_bytes(L.gru_plan)) +
-              align256(argmax_data_bytes(batch, r, V));
+    L.argmax_off = L.part_off + std::max(skinny_data_bytes(L.rank_plan), skinny_data_bytes(L.gru_plan));
+    L.total = L.argmax_off + align256(argmax_data_bytes(batch, r, V));
     return L;
 }
 
@@ -248,7 +249,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_ids = p->out_ids + step;
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
-        e = launch_fused_argmax(aa, ws, s);
+        e = launch_fused_argmax(aa, ws, L.argmax_off, s);
         if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
 
         if (step + 1 < p->steps) {
@@ -375,7 +376,7 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
     a.beta = beta; a.beta_stride = beta_stride;
     a.M = (int)M; a.r = (int)r; a.V = (int)V;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
-    hipError_t e = launch_fused_argmax(a, ws, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_fused_argmax(a, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }
 
@@ -425,7 +426,7 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     a.beta = beta; a.beta_stride = beta_stride;
     a.M = (int)M; a.r = (int)r; a.V = (int)V;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
-    e = launch_fused_argmax(a, ws, s);
+    e = launch_fused_argmax(a, ws, L.argmax_off, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }
 

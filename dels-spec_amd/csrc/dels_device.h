@@ -13,6 +13,10 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 struct bf16_t { uint16_t bits; };   // storage tag for bf16 base/prior
 struct f16_t { uint16_t bits; };    // storage tag for fp16 base/prior
+struct no_prior_t {};                // "no prior term" tag
+
+template <typename T> struct is_no_prior { static constexpr bool value = false; };
+template <> struct is_no_prior<no_prior_t> { static constexpr bool value = true; };
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 

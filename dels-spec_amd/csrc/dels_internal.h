@@ -71,10 +71,12 @@ struct ArgmaxArgs {
     int M, r, V;
     int64_t* out_ids; float* out_score; int64_t ld_out;
 };
-// Data-region bytes the argmax needs beyond the control area (counter + keys).
+// Data-region bytes the argmax needs beyond the control area (counter + keys):
+// the per-chunk partials of the tiled kernel.
 size_t argmax_data_bytes(int64_t M, int64_t r, int64_t V);
 bool argmax_supported(int64_t M, int64_t r, int64_t V);
-hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, hipStream_t s);
+// `ws` is the workspace base (control area); partials go to ws + data_off.
+hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
 // ---- workspace fill and operand packing ---------------------------------------
 hipError_t launch_fill_zero(void* ws, size_t bytes, hipStream_t s);

@@ -1,16 +1,99 @@
 // Host side of the fused combine + argmax: workspace layout and dispatch to
-// the per-dtype instantiations of the GEMV kernel (fused_argmax_gemv.h).
+// the per-dtype instantiations of the GEMV kernel (fused_argmax_gemv.h, few
+// rows) and of the MFMA-tiled kernel (fused_argmax_tiled.h, many rows).
 #include <algorithm>
 
 #include "fused_argmax_gemv.h"
+#include "fused_argmax_tiled.h"
 
 namespace dels {
 
-size_t argmax_data_bytes(int64_t /*M*/, int64_t /*r*/, int64_t /*V*/) { return 0; }
+namespace {
+
+// Rows from which the tiled kernel takes over from the GEMV kernel.
+constexpr int kTiledMinRows = 64;
+// CUs the tiled grid is planned for (MI355X).  A fixed figure keeps the
+// partials size, and so every *_ws_bytes() result, independent of the device.
+constexpr int kPlanCUs = 256;
+
+int base_elem_bytes(int dtype) { return dtype == 0 ? 4 : 2; }
+
+// Partials of the tiled kernel: one key per (vocabulary chunk, row).
+size_t tiled_part_bytes(int64_t M, int64_t V) {
+    if (M < kTiledMinRows) return 0;
+    int gx = 1, gy = 1;
+    tiled_grid((int)std::min<int64_t>(M, kMaxKeyRows), (int)V, kPlanCUs, &gx, &gy);
+    return (size_t)gx * (size_t)M * 8;
+}
+
+// The tiled kernel reads B in the packed layout with r a multiple of 32 (up to
+// 512), and moves base/prior rows with 16-byte direct-to-LDS loads.
+bool tiled_eligible(const ArgmaxArgs& a) {
+    if (a.M < kTiledMinRows || !a.b_packed) return false;
+    if (a.r % 32 != 0 || !(a.r == 128 || a.r == 256 || a.r == 512)) return false;
+    const int eb = base_elem_bytes(a.base_dtype);
+    const int vq = 16 / eb;   // elements per 16-byte base load
+    if (a.V % vq != 0 || a.ldbase % vq != 0 || (reinterpret_cast<uintptr_t>(a.base) & 15) != 0) return false;
+    if (a.prior != nullptr) {
+        const int pb = base_elem_bytes(a.prior_dtype);
+        if ((reinterpret_cast<uintptr_t>(a.prior) & 3) != 0 || (pb == 2 && (a.V & 1) != 0)) return false;
+    }
+    return (reinterpret_cast<uintptr_t>(a.rank) & 15) == 0 && a.ldrank % 8 == 0;
+}
+
+// Unsigned max of the per-chunk keys of each row, decoded into (id, score).
+__global__ __launch_bounds__(256) void argmax_partials_reduce_kernel(const unsigned long long* __restrict__ part,
+                                                                     int chunks, int M, int V, int64_t* out_ids,
+                                                                     float* out_score, int64_t ld_out) {
+    const int m = blockIdx.x * 256 + threadIdx.x;
+    if (m >= M) return;
+    unsigned long long k = 0;
+    for (int x = 0; x < chunks; ++x) {
+        const unsigned long long p = part[(int64_t)x * M + m];
+        k = p > k ? p : k;
+    }
+    uint32_t idx = ~(uint32_t)(k & 0xffffffffull);
+    float val = f32_from_order_key((uint32_t)(k >> 32));
+    if (k == 0ull || idx >= (uint32_t)V) {
+        idx = 0;
+        val = -__builtin_inff();
+    }
+    out_ids[(int64_t)m * ld_out] = (int64_t)idx;
+    if (out_score) out_score[(int64_t)m * ld_out] = val;
+}
+
+}  // namespace
+
+size_t argmax_data_bytes(int64_t M, int64_t /*r*/, int64_t V) { return tiled_part_bytes(M, V); }
 
 bool argmax_supported(int64_t M, int64_t r, int64_t /*V*/) { return r >= 8 && r <= 512 && M <= kMaxKeyRows; }
 
-hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, hipStream_t s) {
+hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s) {
+    // prior kind: 0 none, 1 fp32, 2 bf16, 3 fp16
+    const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
+    char* w = static_cast<char*>(ws);
+    if (tiled_eligible(a)) {
+        int gx = 1, gy = 1;
+        tiled_grid(a.M, a.V, kPlanCUs, &gx, &gy);
+        TiledKArgs ka{};
+        ka.rank = a.rank; ka.ldrank = a.ldrank;
+        ka.B = a.B;
+        ka.base = a.base; ka.ldbase = a.ldbase;
+        ka.prior = a.prior;
+        ka.alpha = a.alpha; ka.alpha_stride = a.alpha_stride;
+        ka.beta = a.beta; ka.beta_stride = a.beta_stride;
+        ka.M = a.M; ka.V = a.V; ka.ntiles = (a.V + 15) / 16;
+        ka.part = reinterpret_cast<unsigned long long*>(w + data_off);
+        const int ks = a.r / 32;
+        hipError_t e;
+        if (a.base_dtype == 1) e = launch_tiled_bf16(ka, ks, pk, gx, gy, s);
+        else if (a.base_dtype == 2) e = launch_tiled_f16(ka, ks, pk, gx, gy, s);
+        else e = launch_tiled_f32(ka, ks, pk, gx, gy, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 255) / 256), dim3(256), 0, s, ka.part, gx,
+                           a.M, a.V, a.out_ids, a.out_score, a.ld_out);
+        return hipGetLastError();
+    }
     ArgmaxKArgs ka{};
     ka.rank = a.rank; ka.ldrank = a.ldrank;
     ka.B = a.B; ka.ldb = a.ldb;
@@ -21,13 +104,10 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, hipStream_t s) {
     ka.M = a.M; ka.r = a.r; ka.V = a.V;
     ka.ksteps = (a.r + 31) / 32;
     ka.out_ids = a.out_ids; ka.out_score = a.out_score; ka.ld_out = a.ld_out;
-    char* w = static_cast<char*>(ws);
     ka.counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
     ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
     // one 128-byte line per row while the rows fit the key area, else packed
     ka.key_stride = (int64_t)a.M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
-    // prior kind: 0 none, 1 fp32, 2 bf16, 3 fp16
-    const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     if (a.base_dtype == 1) return launch_gemv_bf16(ka, a.b_packed, pk, s);
     if (a.base_dtype == 2) return launch_gemv_f16(ka, a.b_packed, pk, s);
     return launch_gemv_f32(ka, a.b_packed, pk, s);

@@ -58,11 +58,6 @@ enum : int {
     B_ROWMAJOR = 2,       // [V, r] row-major: clamped row/column, masked data
 };
 
-struct no_prior_t {};
-
-template <typename T> struct is_no_prior { static constexpr bool value = false; };
-template <> struct is_no_prior<no_prior_t> { static constexpr bool value = true; };
-
 __device__ __forceinline__ bf16x8 masked_bf16x8(u32x4 v, uint32_t mask) {
     v.x &= mask; v.y &= mask; v.z &= mask; v.w &= mask;
     return __builtin_bit_cast(bf16x8, v);

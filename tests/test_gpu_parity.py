@@ -36,9 +36,12 @@ def assert_parity(ids, score, rank_np, B_np, base_np, prior_np, alpha, beta, ref
     rid, rsc, rsec = ref
     pick = oracle.score_at(rank_np, B_np, base_np, prior_np, alpha, beta, np.clip(ids, 0, B_np.shape[0] - 1))
     res = oracle.check_parity(ids, score, rid, rsc, rsec, pick)
-    assert res["id_mismatch_pinned"] == 0, res
-    assert res["score_bad"] == 0, res
-    assert res["unpinned_far_pick"] == 0, res
+    bad = sorted(set(res["bad_rows"]) | set(res["score_bad_rows"]))[:8]
+    detail = [(int(m), int(ids[m]), int(rid[m]), float(score[m]), float(rsc[m]), float(pick[m]), float(rsec[m]))
+              for m in bad]   # (row, dev id, ref id, dev score, ref score, ref score at dev id, ref runner-up)
+    assert res["id_mismatch_pinned"] == 0, (res, detail)
+    assert res["score_bad"] == 0, (res, detail)
+    assert res["unpinned_far_pick"] == 0, (res, detail)
     return res
 
 
@@ -78,6 +81,105 @@ def test_fused_argmax_random(pkg, dev, M, r, V, bdt, pdt, per_row):
     torch.cuda.synchronize()
     assert_parity(ids, score, f(rank), f(x.B), f(x.base), None if prior is None else f(prior),
                   f(x.alpha), f(x.beta))
+
+
+# Many rows with B packed: the MFMA-tiled kernel (256-row groups, vocabulary
+# chunks, per-chunk partials).  Ragged row groups (M % 256), a ragged last
+# vocabulary tile (V % 16 = 8), every base dtype, every prior kind and r in
+# {128, 256, 512}.
+TILED_CASES = [
+    # M, r, V, base dtype, prior dtype (None: no prior), per-row alpha/beta
+    (64, 128, 4096, torch.float32, torch.float32, True),
+    (100, 256, 20008, torch.bfloat16, torch.bfloat16, True),
+    (256, 512, 30000, torch.float16, None, True),
+    (300, 512, 50008, torch.bfloat16, torch.float32, True),
+    (512, 512, 151936, torch.bfloat16, torch.bfloat16, True),
+    (512, 256, 151936, torch.float32, torch.float16, False),
+]
+
+
+@pytest.mark.parametrize("M,r,V,bdt,pdt,per_row", TILED_CASES)
+def test_fused_argmax_tiled_random(pkg, dev, M, r, V, bdt, pdt, per_row):
+    print(f"case fused_argmax tiled M={M} r={r} V={V} base={bdt} prior={pdt}", flush=True)
+    x = pkg.synth.lowrank_inputs(M, 64, r, V, base_dtype=bdt, prior_dtype=pdt or torch.float32,
+                                 per_position=per_row, seed=M * 5 + r)
+    rank = (torch.randn(M, r, generator=torch.Generator().manual_seed(M + V)) * 2).to(torch.bfloat16)
+    prior = x.prior if pdt is not None else None
+    Bp = pkg.pack_operand(x.B.to(dev))
+    ids, score = pkg.fused_argmax(rank.to(dev), Bp, x.base.to(dev),
+                                  None if prior is None else prior.to(dev), x.alpha.to(dev), x.beta.to(dev))
+    torch.cuda.synchronize()
+    assert_parity(ids, score, f(rank), f(x.B), f(x.base), None if prior is None else f(prior),
+                  f(x.alpha), f(x.beta))
+    # same inputs, row-major B: the GEMV kernel must agree on every pinned row
+    ids2, score2 = pkg.fused_argmax(rank.to(dev), x.B.to(dev), x.base.to(dev),
+                                    None if prior is None else prior.to(dev), x.alpha.to(dev), x.beta.to(dev))
+    torch.cuda.synchronize()
+    assert_parity(ids2, score2, f(rank), f(x.B), f(x.base), None if prior is None else f(prior),
+                  f(x.alpha), f(x.beta))
+
+
+def test_fused_argmax_tiled_repeat_is_bitwise_stable(pkg, dev):
+    """Back-to-back calls of the tiled kernel return bit-identical ids and
+    scores (a guard for the cross-wave hand-off of the LDS stage buffers)."""
+    M, r, V = 512, 256, 151936
+    x = pkg.synth.lowrank_inputs(M, 64, r, V, base_dtype=torch.float32, prior_dtype=torch.float16,
+                                 per_position=False, seed=11)
+    rank = (torch.randn(M, r, generator=torch.Generator().manual_seed(12)) * 2).to(torch.bfloat16).to(dev)
+    Bp = pkg.pack_operand(x.B.to(dev))
+    base, prior, al, be = x.base.to(dev), x.prior.to(dev), x.alpha.to(dev), x.beta.to(dev)
+    first = None
+    for _ in range(12):
+        ids, score = pkg.fused_argmax(rank, Bp, base, prior, al, be)
+        torch.cuda.synchronize()
+        if first is None:
+            first = (ids.clone(), score.clone())
+        else:
+            assert torch.equal(ids, first[0]) and torch.equal(score, first[1])
+    assert_parity(first[0], first[1], f(rank), f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
+
+
+def test_fused_argmax_tiled_ties_inf_strided(pkg, dev):
+    """Tiled kernel edge cases: ties across vocabulary chunks and row groups go
+    to the lowest index, an all -inf row gives id 0, a row with beta = 0 skips
+    an infinite prior, and a strided base view (ldbase > V) is read correctly."""
+    M, r, V, ld = 320, 128, 12000, 12008
+    g = torch.Generator().manual_seed(3)
+    rank = torch.zeros(M, r, dtype=torch.bfloat16)
+    B = (torch.randn(V, r, generator=g) * 0.02).to(torch.bfloat16)
+    big = torch.randn(M, ld, generator=g).float()
+    base_full = big.clone()
+    base = base_full[:, :V]                   # strided view: ldbase = 12008
+    alpha = torch.ones(M)
+    beta = torch.zeros(M)
+    prior = torch.zeros(V)
+    # rank = 0: scores are base - beta * prior exactly
+    base[0, 11990] = 50.0
+    base[0, 17] = 50.0                        # tie across chunks: 17 wins
+    base[1, 5000] = 40.0
+    base[1, 5001] = 40.0                      # tie inside a tile
+    base[2, :] = -float("inf")                # all -inf: id 0
+    base[300, 7] = 60.0                       # second row group
+    base[300, 11999] = 60.0
+    prior[123] = float("inf")                 # only rows with beta != 0 see it
+    beta[5] = 1.0
+    base[5, 123] = 1e6                        # row 5: beta = 1 drives index 123 to -inf
+    base[6, 123] = 1e6                        # row 6: beta = 0 keeps it
+    Bp = pkg.pack_operand(B.to(dev))
+    based = base_full.to(dev)[:, :V]
+    assert based.stride(0) == ld
+    ids, score = pkg.fused_argmax(rank.to(dev), Bp, based, prior.to(dev), alpha.to(dev), beta.to(dev))
+    torch.cuda.synchronize()
+    ids = ids.cpu().numpy()
+    score = score.cpu().numpy()
+    assert ids[0] == 17 and score[0] == 50.0
+    assert ids[1] == 5000 and score[1] == 40.0
+    assert ids[2] == 0 and score[2] == -np.inf
+    assert ids[300] == 7 and score[300] == 60.0
+    assert ids[5] != 123 and ids[6] == 123
+    ref = oracle.fused_argmax(f(rank), f(B), f(base), f(prior), f(alpha), f(beta))
+    rows = np.r_[3:5, 7:300, 301:M]
+    assert np.array_equal(ids[rows], ref[0][rows])
 
 
 def test_fused_argmax_strided_base_and_outputs(pkg, dev):
