@@ -34,6 +34,8 @@ bool tiled_eligible(const ArgmaxArgs& a) {
     const int eb = base_elem_bytes(a.base_dtype);
     const int vq = 16 / eb;   // elements per 16-byte base load
     if (a.V % vq != 0 || a.ldbase % vq != 0 || (reinterpret_cast<uintptr_t>(a.base) & 15) != 0) return false;
+    // per-lane 32-bit byte offsets into base
+    if ((int64_t)a.M * a.ldbase * eb >= ((int64_t)1 << 31)) return false;
     if (a.prior != nullptr) {
         const int pb = base_elem_bytes(a.prior_dtype);
         if ((reinterpret_cast<uintptr_t>(a.prior) & 3) != 0 || (pb == 2 && (a.V & 1) != 0)) return false;
@@ -42,16 +44,27 @@ bool tiled_eligible(const ArgmaxArgs& a) {
 }
 
 // Unsigned max of the per-chunk keys of each row, decoded into (id, score).
+// One wave per row: the lanes load the chunks' keys in parallel (so the loads'
+// latencies overlap) and reduce with cross-lane shuffles.
 __global__ __launch_bounds__(256) void argmax_partials_reduce_kernel(const unsigned long long* __restrict__ part,
                                                                      int chunks, int M, int V, int64_t* out_ids,
                                                                      float* out_score, int64_t ld_out) {
-    const int m = blockIdx.x * 256 + threadIdx.x;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
     if (m >= M) return;
     unsigned long long k = 0;
-    for (int x = 0; x < chunks; ++x) {
+    for (int x = lane; x < chunks; x += 64) {
         const unsigned long long p = part[(int64_t)x * M + m];
         k = p > k ? p : k;
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)k, off, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), off, 64);
+        const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+        k = o > k ? o : k;
+    }
+    if (lane != 0) return;
     uint32_t idx = ~(uint32_t)(k & 0xffffffffull);
     float val = f32_from_order_key((uint32_t)(k >> 32));
     if (k == 0ull || idx >= (uint32_t)V) {
@@ -82,7 +95,9 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
         ka.prior = a.prior;
         ka.alpha = a.alpha; ka.alpha_stride = a.alpha_stride;
         ka.beta = a.beta; ka.beta_stride = a.beta_stride;
-        ka.M = a.M; ka.V = a.V; ka.ntiles = (a.V + 15) / 16;
+        ka.M = a.M; ka.V = a.V;
+        ka.nblk16 = (a.V + 15) / 16;
+        ka.ntiles = (a.V + tiled::kTileCols - 1) / tiled::kTileCols;
         ka.part = reinterpret_cast<unsigned long long*>(w + data_off);
         const int ks = a.r / 32;
         hipError_t e;
@@ -90,7 +105,7 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
         else if (a.base_dtype == 2) e = launch_tiled_f16(ka, ks, pk, gx, gy, s);
         else e = launch_tiled_f32(ka, ks, pk, gx, gy, s);
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 255) / 256), dim3(256), 0, s, ka.part, gx,
+        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, ka.part, gx,
                            a.M, a.V, a.out_ids, a.out_score, a.ld_out);
         return hipGetLastError();
     }

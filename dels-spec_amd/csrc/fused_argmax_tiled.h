@@ -3,26 +3,36 @@
 //
 // Semantics as the GEMV kernel (code/kernel/dels.py:42-138):
 //     s[m, v] = fp32(rank_m . B[v]) * alpha_m + base[m, v] - beta_m * prior[v]
-// and per row the lowest v attaining max_v s[m, v].
+// and per row the lowest v attaining max_v s[m, v]; here the two products are
+// fused multiply-adds (one rounding each, as a compiled Triton kernel does).
 //
 // Here the contraction rank[M, r] x B[V, r]^T is a real dense GEMM, computed
-// transposed: each v_mfma_f32_16x16x32_bf16 takes a 16-vocabulary x 32-K slab of
-// B (straight from the MFMA-16 block layout) as its A operand and a 32-K x
-// 16-row slab of rank as its B operand, so lane l ends up holding four
-// consecutive vocabulary columns 4*(l/16)+q of row l%16.  That puts one row per
-// lane: the running argmax stays in the lane over the whole vocabulary chunk
-// and the base logits it needs are four consecutive elements of one row.
+// transposed with v_mfma_f32_32x32x16_bf16 (on gfx950 the 32x32 bf16 MFMA
+// issues at close to twice the rate of the 16x16x32 one): the A operand is a
+// 32-vocabulary x 16-K slab of B, the B operand a 16-K x 32-row slab of rank,
+// so lane l ends up with row l%32 and the sixteen vocabulary columns
+// 8*g + 4*(l/32) + q (g, q < 4) of the tile.  One row per lane: the running
+// argmax stays in the lane over the whole vocabulary chunk, visiting its
+// candidates in increasing index order (so a strict ">" keeps the lowest index
+// of a tie), and the base logits it needs are four runs of four consecutive
+// elements of one row.
 //
-// Workgroup: 8 waves, 2 waves per SIMD.  Wave w keeps the rank operand of its
-// 32 rows (two 16-row tiles) in VGPRs for the whole kernel; a workgroup covers
-// 256 rows and a contiguous chunk of the vocabulary.  The chunk is streamed in
-// stages of TV 16-column tiles: B's stage is one contiguous run of the packed
-// layout and is copied HBM -> LDS with direct-to-LDS loads
-// (global_load_lds_dwordx4, no VGPR staging), together with each wave's
-// base-logit tile (laid out so the epilogue reads it lane-contiguously) and the
-// prior slice.  Stages are double-buffered in LDS with one barrier per stage,
-// so the next stage's loads stay in flight across the contraction and
-// epilogue of the current one.
+// Workgroup: 8 waves, 2 per SIMD.  Wave w keeps the rank operand of its 32
+// rows in VGPRs for the whole kernel (r/16 K steps x 16 bytes per lane); a
+// workgroup covers 256 rows and a contiguous chunk of 32-column vocabulary
+// tiles, one tile per pipeline stage.  A stage's B tile is two consecutive
+// 16-row block rows of the MFMA-16 layout -- one contiguous run of HBM -- and
+// is copied HBM -> LDS with direct-to-LDS loads (global_load_lds_dwordx4, no
+// VGPR staging) that gather it into K-step-major MFMA-32 operand order,
+// together with each wave's base-logit tile (laid out so that the epilogue
+// reads it lane-contiguously) and the prior slice.
+// NBUF stage buffers (as many as fit in 160 KiB of LDS, up to 4) keep NBUF-1
+// stages of loads in flight; each wave waits for its own loads of the stage
+// with an explicit vmcnt count (every wave issues the same number of loads
+// per stage) and a barrier then publishes the stage to all waves.  The
+// buffers are distinct LDS objects named statically in an NBUF-way unrolled
+// loop, so the compiler can tell the reads of one buffer from the loads in
+// flight into the others and adds no waits of its own.
 //
 // Workgroups sharing a vocabulary chunk (the row groups) have linear ids that
 // differ by a multiple of 8, so they run on the same XCD and the second read of
@@ -46,12 +56,14 @@ namespace dels {
 
 struct TiledKArgs {
     const uint16_t* rank; int64_t ldrank;
-    const uint16_t* B;          // MFMA-16 blocks, ksteps = r / 32 exactly
+    const uint16_t* B;          // MFMA-16 blocks, r a multiple of 32
     const void* base; int64_t ldbase;
     const void* prior;          // nullptr when there is no prior
     const float* alpha; int64_t alpha_stride;
     const float* beta; int64_t beta_stride;
-    int M, V, ntiles;           // ntiles = ceil(V / 16)
+    int M, V;
+    int nblk16;                 // ceil(V / 16): 16-row block rows of the packed B
+    int ntiles;                 // ceil(V / 32): 32-column vocabulary tiles
     unsigned long long* part;   // [gridDim.x, M]
 };
 
@@ -59,43 +71,79 @@ namespace tiled {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kRowTiles = 2;                      // 16-row tiles per wave
-constexpr int kRowsPerWG = kWaves * kRowTiles * 16;
-constexpr int kTV = 2;                            // 16-column vocabulary tiles per stage
-constexpr int kStageCols = kTV * 16;
-
-// LDS bytes of the parts of one stage buffer.
-template <int KSTEPS, typename BaseT>
-constexpr int b_bytes() { return kTV * KSTEPS * 1024; }
-template <typename BaseT>
-constexpr int base_bytes_per_wave() { return kRowTiles * 16 * kStageCols * (int)sizeof(BaseT); }
+constexpr int kRowsPerWave = 32;
+constexpr int kRowsPerWG = kWaves * kRowsPerWave;
+constexpr int kTileCols = 32;
+constexpr int kLdsBytes = 160 * 1024;
 constexpr int kPriorBytesPerWave = 256;
 
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-
-__device__ __forceinline__ void dma16(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 16, 0, 0);
-}
-__device__ __forceinline__ void dma4(const void* g, void* lds) {
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds, 4, 0, 0);
-}
-
-// Workgroup barrier for the stage buffers.  Before it, each wave waits for all
-// of its own memory operations, in particular its direct-to-LDS loads: those
-// count in vmcnt, and the LDS-only release fence does not wait for them on
-// every path (the loop back edge), so the wait is explicit.  Other waves read
-// the B tiles this wave loaded as soon as they pass the barrier.  The fences
-// keep the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_waitcnt(0);   // vmcnt(0) expcnt(0) lgkmcnt(0)
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
+// Stage buffer parts: B tile (two 16-row block rows of KS 1 KiB blocks), each
+// wave's base tile (32 rows x 32 columns) and each wave's prior slice.
+template <int KS>
+constexpr int b_bytes() { return 2 * KS * 1024; }
 template <typename BaseT>
-__device__ __forceinline__ void base4_from_lds(const char* p, float (&o)[4]) {
-    if constexpr (sizeof(BaseT) == 4) {
+constexpr int base_bytes_per_wave() { return kRowsPerWave * kTileCols * (int)sizeof(BaseT); }
+template <int KS, typename BaseT>
+constexpr int stage_bytes() {
+    return b_bytes<KS>() + kWaves * base_bytes_per_wave<BaseT>() + kWaves * kPriorBytesPerWave;
+}
+template <int KS, typename BaseT>
+constexpr int num_buffers() {
+    constexpr int n = kLdsBytes / stage_bytes<KS, BaseT>();
+    return n > 4 ? 4 : n;
+}
+// Direct-to-LDS load instructions one wave issues per stage.
+template <int KS, typename BaseT, bool PRIOR>
+constexpr int loads_per_stage() {
+    return (2 * KS) / kWaves + (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0);
+}
+
+// Direct-to-LDS loads: lane l's 16 (or 4) bytes from `g` land at LDS address
+// M0 + 16*l (4*l); `lds` must be wave-uniform.  Written as asm so that the
+// compiler does not track them: its own tracking cannot tell the stage buffers
+// apart and would make every LDS read wait for all loads in flight.  The waits
+// they need are the explicit vmcnt counts of stage_barrier().
+__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+}
+// Address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset.
+// The base is read from the first lane so that it is an SGPR pair whatever the
+// compiler can prove about its uniformity.
+__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+// An LDS-DMA instruction needs one wait state after the SALU write of M0 that
+// precedes it; the compiler cannot see that inside asm, so the s_nop is part
+// of the statement.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
+}
+
+// Wait until at most N of this wave's vector-memory operations are
+// outstanding and all of its LDS operations are done (gfx9 s_waitcnt
+// encoding: vmcnt split over bits 3:0 and 15:14, expcnt 6:4 left at 7,
+// lgkmcnt 11:8 = 0), then the workgroup barrier.  The empty asm statements
+// with a memory clobber keep the compiler from moving memory accesses across.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <typename T>
+__device__ __forceinline__ void cvt4(const char* p, float (&o)[4]) {
+    if constexpr (sizeof(T) == 4) {
         const f32x4 v = *reinterpret_cast<const f32x4*>(p);
         o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
     } else {
@@ -103,7 +151,7 @@ __device__ __forceinline__ void base4_from_lds(const char* p, float (&o)[4]) {
         const uint32_t w[2] = {v.x, v.y};
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            if constexpr (std::is_same<BaseT, bf16_t>::value) {
+            if constexpr (std::is_same<T, bf16_t>::value) {
                 o[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
                 o[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
             } else {
@@ -120,206 +168,239 @@ __device__ __forceinline__ void base4_from_lds(const char* p, float (&o)[4]) {
 
 }  // namespace tiled
 
-template <int KSTEPS, typename BaseT, typename PriorT>
+template <int KS, typename BaseT, typename PriorT>
 __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(TiledKArgs a) {
 #pragma clang fp contract(off)
     using namespace tiled;
-    constexpr int kB = b_bytes<KSTEPS, BaseT>();
+    constexpr int kSteps = 2 * KS;                       // 16-deep K steps
+    constexpr int kB = b_bytes<KS>();
     constexpr int kBaseW = base_bytes_per_wave<BaseT>();
     constexpr bool kPrior = !is_no_prior<PriorT>::value;
-    // One stage buffer: B tiles, every wave's base tile, every wave's prior slice.
+    constexpr int NBUF = num_buffers<KS, BaseT>();
+    constexpr int P = NBUF - 1;                          // stages in flight
+    constexpr int E = loads_per_stage<KS, BaseT, kPrior>();
+    static_assert(NBUF >= 2, "stage does not fit twice in LDS");
+    static_assert((2 * KS) % kWaves == 0, "B blocks per stage must split over the waves");
+
     struct __attribute__((aligned(1024))) Stage {
         char b[kB];
         char base[kWaves][kBaseW];
         char prior[kWaves][kPriorBytesPerWave];
     };
-    // Two distinct LDS objects rather than one array indexed by parity: the
-    // compiler can then tell that reads of one buffer do not depend on the
-    // direct-to-LDS loads in flight into the other, and inserts no wait for them.
+    struct NoStage {};
     __shared__ Stage lds0, lds1;
+    __shared__ std::conditional_t<(NBUF > 2), Stage, NoStage> lds2;
+    __shared__ std::conditional_t<(NBUF > 3), Stage, NoStage> lds3;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int col = lane & 15;      // row (within a 16-row tile) of this lane
-    const int kg = lane >> 4;       // K group of the operands / vocabulary quad of the results
-    const int mw = blockIdx.y * kRowsPerWG + wave * (kRowTiles * 16);   // first row of this wave
+    const int rl = lane & 31;       // row of this lane within the wave's 32
+    const int h = lane >> 5;        // K half of the operands / vocabulary quad of the results
+    const int mw = blockIdx.y * kRowsPerWG + wave * kRowsPerWave;   // first row of this wave
     const bool wave_active = mw < a.M;
 
-    // Vocabulary chunk of this workgroup: tiles [t0, t1).
-    const int t0 = (int)(((int64_t)blockIdx.x * a.ntiles) / gridDim.x);
-    const int t1 = (int)(((int64_t)(blockIdx.x + 1) * a.ntiles) / gridDim.x);
-    const int nst = (t1 - t0 + kTV - 1) / kTV;
-    const int vend = min(a.V, t1 * 16);
+    // Vocabulary chunk of this workgroup: 32-column tiles [T0, T0 + nst), one per
+    // stage.  (A round-robin assignment of tiles measured slower: the base rows
+    // are then read in pieces no workgroup continues.)
+    const int T0 = (int)(((int64_t)blockIdx.x * a.ntiles) / gridDim.x);
+    const int nst = (int)(((int64_t)(blockIdx.x + 1) * a.ntiles) / gridDim.x) - T0;
+    auto tile_of = [&](int st) { return T0 + st; };
 
     // Rank operand of the wave's rows, resident for the whole kernel.
-    bf16x8 ra[kRowTiles][KSTEPS];
-    float al[kRowTiles], be[kRowTiles], best[kRowTiles];
-    int bidx[kRowTiles];
-    bool use_prior[kRowTiles];
+    const int mrow = min(mw + rl, a.M - 1);
+    bf16x8 ra[kSteps];
+    {
+        const uint16_t* rp = a.rank + (int64_t)mrow * a.ldrank + h * 8;
 #pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt) {
-        const int m = min(mw + rt * 16 + col, a.M - 1);
-        const uint16_t* rp = a.rank + (int64_t)m * a.ldrank + kg * 8;
-#pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) ra[rt][s] = load_bf16x8(rp + s * 32);
-        al[rt] = a.alpha[(int64_t)m * a.alpha_stride];
-        be[rt] = a.beta[(int64_t)m * a.beta_stride];
-        use_prior[rt] = kPrior && be[rt] != 0.f;
-        best[rt] = -__builtin_inff();
-        bidx[rt] = INT_MAX;
+        for (int s = 0; s < kSteps; ++s) ra[s] = load_bf16x8(rp + s * 16);
     }
+    const float al = a.alpha[(int64_t)mrow * a.alpha_stride];
+    const float be = a.beta[(int64_t)mrow * a.beta_stride];
+    const bool use_prior = kPrior && be != 0.f;
+    float best = -__builtin_inff();
+    int bidx = INT_MAX;
 
     const char* Bg = reinterpret_cast<const char*>(a.B);
     const char* baseg = static_cast<const char*>(a.base);
     const char* priorg = static_cast<const char*>(a.prior);
+    // byte offset of this lane's base row (the host keeps M * ldbase * size below 2^31)
+    const uint32_t row_off = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
 
-    // Issue the direct-to-LDS loads of stage `st` into buffer S.  Addresses past
-    // the chunk are clamped to valid memory (their results are masked in the
-    // epilogue).
-    auto issue_stage = [&](Stage& S, int st) {
-        const int tb = t0 + st * kTV;
-        // B: kTV * KSTEPS blocks of 1 KiB, contiguous in the packed layout.
-        constexpr int nb = kTV * KSTEPS / kWaves;
-#pragma unroll
-        for (int j = 0; j < nb; ++j) {
-            const int blk = wave * nb + j;                  // block within the stage
-            const int t = min(tb + blk / KSTEPS, t1 - 1);   // clamped tile
-            const int64_t goff = ((int64_t)t * KSTEPS + blk % KSTEPS) * 1024 + lane * 16;
-            dma16(Bg + goff, S.b + blk * 1024);
-        }
-        // Base logits of the wave's rows: lane L of each 1 KiB load is row L%16,
-        // 16-byte chunk L/16 of the stage's columns.
-        const int vs = tb * 16;
-#pragma unroll
-        for (int rt = 0; rt < kRowTiles; ++rt) {
-            const int m = min(mw + rt * 16 + col, a.M - 1);
-            const char* rowp = baseg + (int64_t)m * a.ldbase * (int64_t)sizeof(BaseT);
+    // Direct-to-LDS loads of stage `st` into buffer S: exactly E instructions
+    // per wave.  Addresses past the data are clamped to valid memory; their
+    // results are masked in the epilogue.
+    // The B tile is stored K-step-major: LDS block s (1 KiB) holds the A
+    // operand of 16-deep step s in lane order, gathered by the loads from the
+    // two 16-row block rows of the packed layout (lane L: row L%32 of the tile,
+    // K 16s + 8*(L/32) .. +7), so every operand read is one contiguous,
+    // bank-conflict-free KiB.
+    // Per-lane part of the B gather offset: row l%16 of block row (l/16)%2, K group l/32.
+    const uint32_t b_lane = ((lane & 15) + 16 * h) * 16;
+    const uint32_t b_hi = ((lane >> 4) & 1) ? (uint32_t)KS * 1024 : 0u;
+    // Load `piece` (0 <= piece < E) of stage `st` into buffer S: pieces 0..nb-1
+    // are B blocks, then the base-logit loads, then the prior slice.  `piece` is
+    // a constant wherever this is called (unrolled loops), so the chain of
+    // tests folds away.
+    constexpr int nb = kSteps / kWaves;
+    constexpr int nbase = sizeof(BaseT) == 4 ? 4 : 2;
+    auto issue_piece = [&](Stage& S, int st, int piece) {
+        const int T = tile_of(st);
+        const int vs = T * kTileCols;
+        if (piece < nb) {
+            // block rows 2T and 2T+1 (the second clamped to the last one, masked later)
+            const int rb0 = min(2 * T, a.nblk16 - 1);
+            const bool two = 2 * T + 1 < a.nblk16;
+            const char* bt = Bg + (int64_t)rb0 * KS * 1024;
+            const int step = wave * nb + piece;                  // K step of this load
+            dma16(bt, b_lane + (two ? b_hi : 0u) + (step >> 1) * 1024 + (step & 1) * 512, S.b + step * 1024);
+        } else if (piece < nb + nbase) {
+            const int g = piece - nb;
             if constexpr (sizeof(BaseT) == 4) {
-#pragma unroll
-                for (int t = 0; t < kTV; ++t) {
-                    const int v = min(vs + t * 16 + kg * 4, a.V - 4);
-                    dma16(rowp + (int64_t)v * 4, S.base[wave] + (rt * kTV + t) * 1024);
-                }
+                // load g: lane L -> row L%32, 4-column chunk 2g + L/32
+                const int v = min(vs + 4 * (2 * g + h), a.V - 4);
+                dma16(baseg, row_off + (uint32_t)v * 4u, S.base[wave] + g * 1024);
             } else {
-                const int v = min(vs + kg * 8, a.V - 8);
-                dma16(rowp + (int64_t)v * 2, S.base[wave] + rt * 1024);
+                // load g: lane L -> row L%32, 8-column chunk 2g + L/32
+                const int v = min(vs + 8 * (2 * g + h), a.V - 8);
+                dma16(baseg, row_off + (uint32_t)v * 2u, S.base[wave] + g * 1024);
             }
-        }
-        // Prior slice of the stage's columns (one dword per lane).
-        if constexpr (kPrior) {
+        } else if constexpr (kPrior) {
             if constexpr (sizeof(PriorT) == 4) {
                 const int v = min(vs + (lane & 31), a.V - 1);
-                dma4(priorg + (int64_t)v * 4, S.prior[wave]);
+                dma4(priorg, (uint32_t)v * 4u, S.prior[wave]);
             } else {
                 const int v = min(vs + 2 * (lane & 15), a.V - 2);
-                dma4(priorg + (int64_t)v * 2, S.prior[wave]);
+                dma4(priorg, (uint32_t)v * 2u, S.prior[wave]);
             }
         }
+    };
+    auto issue_stage = [&](Stage& S, int st) {
+#pragma unroll
+        for (int piece = 0; piece < E; ++piece) issue_piece(S, st, piece);
     };
 
-    // Epilogue operands of one stage, read from LDS into registers before the
-    // next stage's loads are issued (so no read of this stage can be made to
-    // wait for them).
-    struct EpiRegs {
-        float base[kTV][kRowTiles][4];
-        float prior[kTV][4];
-    };
-    auto read_epilogue = [&](const Stage& S, EpiRegs& e) {
-        const char* Lb = S.base[wave];
-        const char* Lp = S.prior[wave];
-#pragma unroll
-        for (int t = 0; t < kTV; ++t) {
-            if constexpr (kPrior) {
-                if constexpr (sizeof(PriorT) == 4) {
-                    const f32x4 p = *reinterpret_cast<const f32x4*>(Lp + (t * 16 + kg * 4) * 4);
-                    e.prior[t][0] = p[0]; e.prior[t][1] = p[1]; e.prior[t][2] = p[2]; e.prior[t][3] = p[3];
-                } else {
-                    base4_from_lds<PriorT>(Lp + (t * 16 + kg * 4) * 2, e.prior[t]);
-                }
-            } else {
-                e.prior[t][0] = e.prior[t][1] = e.prior[t][2] = e.prior[t][3] = 0.f;
-            }
-#pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
-                if constexpr (sizeof(BaseT) == 4)
-                    base4_from_lds<BaseT>(Lb + (rt * kTV + t) * 1024 + lane * 16, e.base[t][rt]);
-                else
-                    base4_from_lds<BaseT>(Lb + rt * 1024 + (col + 16 * (2 * t + (kg >> 1))) * 16 + (kg & 1) * 8,
-                                          e.base[t][rt]);
-            }
-        }
+    // Epilogue operands of one stage: base[g][q] and prior[g][q] of column
+    // 8g + 4h + q.  (No load in flight targets this buffer until the next
+    // barrier, so they are read from LDS right where they are used.)
+    auto read_epilogue = [&](const Stage& S, int g, float (&b4)[4], float (&p4)[4]) {
+        if constexpr (sizeof(BaseT) == 4)
+            cvt4<BaseT>(S.base[wave] + g * 1024 + lane * 16, b4);
+        else
+            cvt4<BaseT>(S.base[wave] + (g >> 1) * 1024 + (rl + 32 * (g & 1)) * 16 + h * 8, b4);
+        if constexpr (kPrior)
+            cvt4<PriorT>(S.prior[wave] + (8 * g + 4 * h) * (int)sizeof(PriorT), p4);
+        else
+            p4[0] = p4[1] = p4[2] = p4[3] = 0.f;
     };
 
-    auto consume_stage = [&](const Stage& S, const EpiRegs& e, int st) {
-        f32x4 acc[kTV][kRowTiles];
+    // Contraction of one stage (one accumulation chain, operands read two steps
+    // ahead) and the fused combine + running argmax.  The running index is kept
+    // as a wave-uniform candidate slot st*16 + c (c = 4g + q), decoded at the end.
+    // `next` / `nst_next`: the buffer and stage whose loads are spread over this
+    // contraction (one piece every kSteps/E steps), so that they pass through
+    // the address unit while the matrix cores work (nst_next < 0: none).
+    auto consume_stage = [&](const Stage& S, int st, Stage& next, int st_next) {
+        f32x16 acc;
 #pragma unroll
-        for (int t = 0; t < kTV; ++t)
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        const char* ap = S.b + lane * 16;
+        auto opnd = [&](int s) { return *reinterpret_cast<const bf16x8*>(ap + s * 1024); };
+        const bool issue = st_next >= 0;
+        // The scheduling barriers pin the order read(s+2), mma(s): the read
+        // latency hides behind two contractions instead of stalling each one.
+        bf16x8 a0 = opnd(0), a1 = opnd(1);
 #pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < kSteps; ++s) {
+            const bf16x8 nx = s + 2 < kSteps ? opnd(s + 2) : a1;
+            __builtin_amdgcn_sched_barrier(0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, ra[s], acc, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-#pragma unroll
-            for (int t = 0; t < kTV; ++t) {
-                const bf16x8 bv = *reinterpret_cast<const bf16x8*>(S.b + (t * KSTEPS + s) * 1024 + lane * 16);
-#pragma unroll
-                for (int rt = 0; rt < kRowTiles; ++rt)
-                    acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bv, ra[rt][s], acc[t][rt], 0, 0, 0);
-            }
+            for (int piece = 0; piece < E; ++piece)
+                if (s == piece * kSteps / E && issue) issue_piece(next, st_next, piece);
+            a0 = a1;
+            a1 = nx;
         }
-        const int vs = (t0 + st * kTV) * 16;
+        const int vs = tile_of(st) * kTileCols;
+        auto epilogue = [&](auto masked) {
 #pragma unroll
-        for (int t = 0; t < kTV; ++t) {
-#pragma unroll
-            for (int rt = 0; rt < kRowTiles; ++rt) {
+            for (int g = 0; g < 4; ++g) {
+                float b4[4], p4[4];
+                read_epilogue(S, g, b4, p4);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int v = vs + t * 16 + kg * 4 + q;
-                    float sc = acc[t][rt][q] * al[rt];
-                    sc = sc + e.base[t][rt][q];
-                    const float scp = sc - be[rt] * e.prior[t][q];
-                    sc = use_prior[rt] ? scp : sc;
-                    // branch-free: (in chunk) and (larger, or equal at a lower index)
-                    const bool take = (v < vend) & ((sc > best[rt]) | ((sc == best[rt]) & (v < bidx[rt])));
-                    best[rt] = take ? sc : best[rt];
-                    bidx[rt] = take ? v : bidx[rt];
+                    float sc = __builtin_fmaf(acc[4 * g + q], al, b4[q]);
+                    const float scp = __builtin_fmaf(-be, p4[q], sc);
+                    sc = use_prior ? scp : sc;
+                    if constexpr (decltype(masked)::value)
+                        sc = vs + 8 * g + 4 * h + q < a.V ? sc : -__builtin_inff();
+                    // candidates arrive in increasing index order: strict ">" keeps the lowest index
+                    const bool take = sc > best;
+                    best = take ? sc : best;
+                    bidx = take ? st * 16 + 4 * g + q : bidx;
+                }
+            }
+        };
+        if (vs + kTileCols > a.V)   // only the last tile of the vocabulary is partial
+            epilogue(std::true_type{});
+        else
+            epilogue(std::false_type{});
+    };
+
+    // Pipeline: stages 0..P-1 are issued up front; at stage st each wave waits
+    // for its own loads of st (the younger stages may stay in flight), the
+    // barrier publishes st, the freed buffer of st-1 takes stage st+P, and st
+    // is contracted.
+    auto buf = [&](int i) -> Stage& {
+        if constexpr (NBUF > 3) { if (i == 3) return lds3; }
+        if constexpr (NBUF > 2) { if (i == 2) return lds2; }
+        return i == 1 ? lds1 : lds0;
+    };
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+        if (i < nst) issue_stage(buf(i), i);
+    for (int st0 = 0; st0 < nst; st0 += NBUF) {
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) {
+            const int st = st0 + u;
+            if (st < nst) {
+                const int younger = min(P - 1, nst - 1 - st);
+                if constexpr (P >= 3) {
+                    if (younger >= 2) stage_barrier<2 * E>();
+                    else if (younger == 1) stage_barrier<E>();
+                    else stage_barrier<0>();
+                } else if constexpr (P == 2) {
+                    if (younger >= 1) stage_barrier<E>();
+                    else stage_barrier<0>();
+                } else {
+                    stage_barrier<0>();
+                }
+                const int st_next = st + P < nst ? st + P : -1;
+                if (wave_active) {
+                    consume_stage(buf(u), st, buf((u + P) % NBUF), st_next);
+                } else if (st_next >= 0) {
+                    issue_stage(buf((u + P) % NBUF), st_next);
                 }
             }
         }
-    };
-
-    // Double-buffered pipeline, one barrier per stage: past the barrier, stage st
-    // has landed for every wave and the other buffer (read during stage st-1) is
-    // free, so stage st+1 is issued into it and streams in while stage st is
-    // contracted.  Unrolled by two so each half names its buffers statically.
-    if (nst > 0) issue_stage(lds0, 0);
-    for (int st = 0; st < nst; st += 2) {
-        EpiRegs e;
-        lds_barrier();
-        read_epilogue(lds0, e);
-        if (st + 1 < nst) issue_stage(lds1, st + 1);
-        if (wave_active) consume_stage(lds0, e, st);
-        if (st + 1 >= nst) break;
-        lds_barrier();
-        read_epilogue(lds1, e);
-        if (st + 2 < nst) issue_stage(lds0, st + 2);
-        if (wave_active) consume_stage(lds1, e, st + 1);
     }
 
-    // Reduce the four vocabulary quads of each row (lanes l, l^16, l^32, l^48).
-#pragma unroll
-    for (int rt = 0; rt < kRowTiles; ++rt) {
-#pragma unroll
-        for (int off = 16; off < 64; off <<= 1) {
-            const float ov = __shfl_xor(best[rt], off, 64);
-            const int oi = __shfl_xor(bidx[rt], off, 64);
-            if (argmax_better(ov, oi, best[rt], bidx[rt])) {
-                best[rt] = ov;
-                bidx[rt] = oi;
-            }
+    // Decode the candidate slot into the vocabulary index, then merge the two
+    // vocabulary quads of each row (lanes l and l^32).
+    {
+        if (bidx != INT_MAX) {
+            const int st = bidx >> 4, c = bidx & 15;
+            bidx = tile_of(st) * kTileCols + 8 * (c >> 2) + 4 * h + (c & 3);
         }
-        const int m = mw + rt * 16 + col;
-        if (kg == 0 && m < a.M) {
-            const unsigned long long key = bidx[rt] == INT_MAX ? 0ull : pack_argmax(best[rt], (uint32_t)bidx[rt]);
+        const float ov = __shfl_xor(best, 32, 64);
+        const int oi = __shfl_xor(bidx, 32, 64);
+        if (argmax_better(ov, oi, best, bidx)) {
+            best = ov;
+            bidx = oi;
+        }
+        const int m = mw + rl;
+        if (h == 0 && m < a.M) {
+            const unsigned long long key = bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx);
             a.part[(int64_t)blockIdx.x * a.M + m] = key;
         }
     }
@@ -329,17 +410,17 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
 // about one workgroup per CU, chunk count a multiple of 8 (XCD pairing).
 inline void tiled_grid(int M, int V, int cus, int* gx, int* gy) {
     const int groups = (M + tiled::kRowsPerWG - 1) / tiled::kRowsPerWG;
-    const int ntiles = (V + 15) / 16;
+    const int ntiles = (V + tiled::kTileCols - 1) / tiled::kTileCols;
     int x = std::max(1, cus / groups);
     if (x >= 8) x -= x % 8;
-    x = std::max(1, std::min(x, (ntiles + tiled::kTV - 1) / tiled::kTV));
+    x = std::max(1, std::min(x, ntiles));
     *gx = x;
     *gy = groups;
 }
 
-template <int KSTEPS, typename BaseT, typename PriorT>
+template <int KS, typename BaseT, typename PriorT>
 hipError_t launch_tiled_inst(const TiledKArgs& ka, int gx, int gy, hipStream_t s) {
-    hipLaunchKernelGGL((fused_argmax_tiled_kernel<KSTEPS, BaseT, PriorT>), dim3(gx, gy, 1), dim3(tiled::kThreads), 0,
+    hipLaunchKernelGGL((fused_argmax_tiled_kernel<KS, BaseT, PriorT>), dim3(gx, gy, 1), dim3(tiled::kThreads), 0,
                        s, ka);
     return hipGetLastError();
 }
