@@ -52,7 +52,71 @@ def parse_args():
     ap.add_argument("--layout", default="packed", choices=["packed", "rowmajor"],
                     help="weights in the MFMA-16 block layout (as the runner stores them) or row-major")
     ap.add_argument("--traffic-file", default=os.path.join(REPO_DIR, "profiles", "traffic.json"))
+    ap.add_argument("--traffic-from", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "COPY_FETCH_CSV", "COPY_WRITE_CSV"),
+                    help="turn rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE counter CSVs of a bench run and of a "
+                         "--copy-calibration run into per-launch HBM bytes (written to --traffic-file); no GPU use")
     return ap.parse_args()
+
+
+# Kernels of the fused argmax per workload (the tiled path adds its partials reduce).
+ARGMAX_KERNELS = {"qwen3_8b_m16": ("fused_argmax_gemv_kernel",),
+                  "qwen3_4b_m16": ("fused_argmax_gemv_kernel",),
+                  "qwen3_8b_m512": ("fused_argmax_tiled_kernel", "argmax_partials_reduce_kernel")}
+
+
+def _counter_means(path):
+    """Mean counter value (KiB per dispatch) per (kernel substring match, counter) from a rocprofv3 CSV."""
+    import csv
+    import statistics
+    per = {}
+    with open(path) as fh:
+        for row in csv.DictReader(fh):
+            per.setdefault((row["Kernel_Name"], row["Counter_Name"]), []).append(float(row["Counter_Value"]))
+    return {k: (statistics.mean(v), len(v)) for k, v in per.items()}
+
+
+def traffic_from(args):
+    """HBM bytes per launch of the argmax kernels from FETCH_SIZE / WRITE_SIZE counters.
+
+    Each counter is scaled by the ratio of the bytes a plain copy kernel moves
+    (512 MiB read, 512 MiB written per dispatch) to what the same counter reads
+    for that copy.  The bench run holds the M=16 (GEMV) and M=512 (tiled)
+    launches; the two are told apart by kernel name.
+    """
+    fetch, write, cfetch, cwrite = (_counter_means(p) for p in args.traffic_from)
+    copy_bytes = 512 * 2**20
+
+    def copy_scale(means, counter):
+        vals = [m for (k, c), (m, n) in means.items() if c == counter and "copy" in k.lower()]
+        if not vals:
+            raise SystemExit(f"no copy kernel with {counter} in the calibration CSV")
+        return copy_bytes / (max(vals) * 1024.0)
+
+    fs, ws = copy_scale(cfetch, "FETCH_SIZE"), copy_scale(cwrite, "WRITE_SIZE")
+
+    def kib(means, counter, names):
+        total = 0.0
+        for name in names:
+            vals = [(m, n) for (k, c), (m, n) in means.items() if c == counter and name in k]
+            if not vals:
+                return None
+            total += max(vals, key=lambda t: t[1])[0]
+        return total
+
+    out = {"fetch_scale": fs, "write_scale": ws,
+           "method": "rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch, mean over dispatches), "
+                     "each scaled by copy_bytes / counter of a 512 MiB device copy"}
+    # the default bench run covers these two workloads (the M=16 record and the M=512 one)
+    for wl in ("qwen3_8b_m16", "qwen3_8b_m512"):
+        names = ARGMAX_KERNELS[wl]
+        f, w = kib(fetch, "FETCH_SIZE", names), kib(write, "WRITE_SIZE", names)
+        if f is None or w is None:
+            continue
+        out[wl] = {"kernels": list(names), "fetch_kib": f, "write_kib": w,
+                   "fused_argmax_hbm_bytes_per_launch": f * 1024.0 * fs + w * 1024.0 * ws}
+    with open(args.traffic_file, "w") as fh:
+        json.dump(out, fh, indent=1)
+    print(json.dumps(out))
 
 
 def workload_desc(name, x, layout):
@@ -237,6 +301,9 @@ def cpu_baseline(name, x0, seconds):
 
 def main():
     args = parse_args()
+    if args.traffic_from:
+        traffic_from(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: the fused argmax shards by rows or by "
                                    "vocabulary without collectives on the hot path; run with --gpus 1"}))
@@ -259,13 +326,14 @@ def main():
     pkg._lib.load()
 
     rec, x0 = bench_workload(pkg, args.workload, args, dev, torch)
-    traffic = None
+    traffic_all = {}
     if os.path.exists(args.traffic_file):
         try:
             with open(args.traffic_file) as fh:
-                traffic = json.load(fh).get(args.workload, {}).get("fused_argmax_hbm_bytes_per_launch")
-        except Exception:
-            traffic = None
+                traffic_all = json.load(fh)
+        except (OSError, ValueError):
+            traffic_all = {}
+    traffic = traffic_all.get(args.workload, {}).get("fused_argmax_hbm_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": rec["rows_per_s"],
@@ -283,7 +351,7 @@ def main():
         "config": workload_desc(args.workload, x0, args.layout),
         "roofline": {
             "bound": "hbm",
-            "kernel": "fused_argmax_gemv_kernel",
+            "kernel": " + ".join(ARGMAX_KERNELS[args.workload]),
             "achieved": rec["argmax_GBs"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -303,6 +371,9 @@ def main():
             out["m512"] = {k: r512[k] for k in ("rows_per_s", "us_per_step", "us_fused_argmax", "argmax_GBs",
                                                 "argmax_hbm_frac", "argmax_TFLOPs", "argmax_mfma_frac",
                                                 "step_GBs", "hbm_frac_step", "step_TFLOPs", "mfma_frac_step")}
+            out["m512"]["argmax_traffic"] = traffic_all.get("qwen3_8b_m512", {}).get(
+                "fused_argmax_hbm_bytes_per_launch")
+            out["m512"]["argmax_algorithmic_bytes"] = r512["argmax_bytes"]
         except Exception as e:  # informative record only
             out["m512"] = {"error": repr(e)}
     if args.cpu_baseline:
