@@ -82,7 +82,7 @@ static int check_weight(const void* p, int64_t ld, int64_t cols, int layout, con
 
 // Every layout starts with the shared control area [0, kCtrlBytes).
 struct LowrankLayout {
-    size_t rank_off, part_off, argmax_off, total;
+    size_t rank_off, part_off, argmax_off, decode_off, total;
     SkinnyPlan plan;
 };
 
@@ -92,7 +92,8 @@ static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) 
     L.rank_off = kCtrlBytes;
     L.part_off = L.rank_off + align256((size_t)M * r * 2);
     L.argmax_off = L.part_off + skinny_data_bytes(L.plan);
-    L.total = L.argmax_off + align256(argmax_data_bytes(M, r, V));
+    L.decode_off = L.argmax_off + align256(argmax_data_bytes(M, r, V));
+    L.total = L.decode_off + decode_data_bytes(M, d, r);
     return L;
 }
 
@@ -380,6 +381,8 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }
 
+int dels_debug_set_decode_spin_limit(int limit) { return set_decode_spin_limit(limit); }
+
 size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) {
     return lowrank_layout(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1), std::max<int64_t>(r, 1),
                           std::max<int64_t>(V, 1)).total;
@@ -414,9 +417,6 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
     ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
     ra.rank = rank; ra.ldrank = r;
-    hipError_t e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
-    if (e != hipSuccess) return hip_fail(e, "rank projection launch");
-
     ArgmaxArgs a{};
     a.rank = rank; a.ldrank = r;
     a.B = static_cast<const uint16_t*>(B); a.ldb = ldb; a.b_packed = b_layout == DELS_LAYOUT_MFMA16;
@@ -426,6 +426,14 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     a.beta = beta; a.beta_stride = beta_stride;
     a.M = (int)M; a.r = (int)r; a.V = (int)V;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
+    hipError_t e;
+    if (decode_eligible(M, d, r, ra.a_packed, a.b_packed)) {
+        // few rows, packed weights: rank projection and argmax in one launch
+        e = launch_lowrank_decode(ra, a, ws, L.decode_off, s);
+        return e == hipSuccess ? DELS_OK : hip_fail(e, "fused decode step launch");
+    }
+    e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
+    if (e != hipSuccess) return hip_fail(e, "rank projection launch");
     e = launch_fused_argmax(a, ws, L.argmax_off, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }

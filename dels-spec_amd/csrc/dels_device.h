@@ -53,6 +53,12 @@ __device__ __forceinline__ bf16x8 load_bf16x8_nt(const uint16_t* p) {
 }
 __device__ __forceinline__ bf16x8 zero_bf16x8() { return __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u}); }
 
+// Eight bf16 values kept (mask ~0) or zeroed (mask 0) without a branch.
+__device__ __forceinline__ bf16x8 masked_bf16x8(u32x4 v, uint32_t mask) {
+    v.x &= mask; v.y &= mask; v.z &= mask; v.w &= mask;
+    return __builtin_bit_cast(bf16x8, v);
+}
+
 // Order-preserving map float -> uint32 (a < b  <=>  key(a) < key(b) for non-NaN).
 // -0.0 is folded onto +0.0 so that equal scores compare equal.
 __device__ __forceinline__ uint32_t f32_order_key(float f) {

@@ -78,6 +78,19 @@ bool argmax_supported(int64_t M, int64_t r, int64_t V);
 // `ws` is the workspace base (control area); partials go to ws + data_off.
 hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
+// ---- fused decode step: rank projection + argmax in one launch (M <= 16) --------
+
+// Both weights packed, r/32 in {2, 4, 8, 16}, d a multiple of 32 and at most
+// 32 K blocks per split of the rank projection.
+bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed);
+// Data-region bytes of the decode step (rank partials and the shared bf16 rank).
+size_t decode_data_bytes(int64_t M, int64_t d, int64_t r);
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, size_t data_off,
+                                 hipStream_t s);
+// Polls of the rank-ready count before a workgroup computes the rank itself
+// (test hook; returns the previous value).
+int set_decode_spin_limit(int limit);
+
 // ---- workspace fill and operand packing ---------------------------------------
 hipError_t launch_fill_zero(void* ws, size_t bytes, hipStream_t s);
 

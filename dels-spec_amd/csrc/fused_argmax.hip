@@ -5,6 +5,7 @@
 
 #include "fused_argmax_gemv.h"
 #include "fused_argmax_tiled.h"
+#include "lowrank_decode.h"
 
 namespace dels {
 
@@ -126,6 +127,79 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
     if (a.base_dtype == 1) return launch_gemv_bf16(ka, a.b_packed, pk, s);
     if (a.base_dtype == 2) return launch_gemv_f16(ka, a.b_packed, pk, s);
     return launch_gemv_f32(ka, a.b_packed, pk, s);
+}
+
+// ---- fused decode step ------------------------------------------------------
+
+namespace {
+int g_decode_spin_limit = 1 << 14;
+
+struct DecodePlan {
+    int nct, nz, kpz, ksa;
+};
+
+DecodePlan decode_plan(int64_t d, int64_t r) {
+    DecodePlan p{};
+    p.nct = (int)(r / 16);
+    p.nz = kDecodeWGs / std::max(p.nct, 1);
+    p.ksa = (int)(d / 32);
+    p.kpz = (p.ksa + p.nz - 1) / std::max(p.nz, 1);
+    return p;
+}
+}  // namespace
+
+int set_decode_spin_limit(int limit) {
+    const int prev = g_decode_spin_limit;
+    g_decode_spin_limit = std::max(0, limit);
+    return prev;
+}
+
+bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed) {
+    if (M < 1 || M > 16 || !a_packed || !b_packed) return false;
+    if (!(r == 64 || r == 128 || r == 256 || r == 512)) return false;
+    if (d < 32 || d % 32 != 0) return false;
+    const DecodePlan p = decode_plan(d, r);
+    return kDecodeWGs % p.nct == 0 && (p.kpz + 3) / 4 <= kDecodeMaxJ;
+}
+
+size_t decode_data_bytes(int64_t M, int64_t d, int64_t r) {
+    if (M > 16 || r % 16 != 0 || d % 32 != 0) return 0;
+    const DecodePlan p = decode_plan(d, r);
+    return align256((size_t)p.nct * p.nz * 256 * sizeof(float)) + align256((size_t)16 * r * 2);
+}
+
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, size_t data_off,
+                                 hipStream_t s) {
+    const DecodePlan p = decode_plan(ra.d, ra.r);
+    char* w = static_cast<char*>(ws);
+    DecodeKArgs k{};
+    ArgmaxKArgs& ka = k.am;
+    ka.rank = nullptr; ka.ldrank = 0;
+    ka.B = a.B; ka.ldb = a.ldb;
+    ka.base = a.base; ka.ldbase = a.ldbase;
+    ka.prior = a.prior;
+    ka.alpha = a.alpha; ka.alpha_stride = a.alpha_stride;
+    ka.beta = a.beta; ka.beta_stride = a.beta_stride;
+    ka.M = a.M; ka.r = a.r; ka.V = a.V;
+    ka.ksteps = a.r / 32;
+    ka.out_ids = a.out_ids; ka.out_score = a.out_score; ka.ld_out = a.ld_out;
+    unsigned int* counters = reinterpret_cast<unsigned int*>(w + kCountersOff);
+    ka.counter = counters;                         // argmax arrivals
+    ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
+    ka.key_stride = 16;                            // M <= 16: one 128-byte line per row
+    k.done = counters + 1;                         // published rank tiles
+    k.tile_cnt = counters + 64;                    // per-tile split arrivals (nct <= 32)
+    k.h = ra.h; k.ldh = ra.ldh;
+    k.A = ra.A;
+    k.bias = ra.bias; k.act = ra.act;
+    k.ksa = p.ksa; k.nct = p.nct; k.nz = p.nz; k.kpz = p.kpz;
+    k.partial = reinterpret_cast<float*>(w + data_off);
+    k.rank_buf = reinterpret_cast<uint16_t*>(w + data_off + align256((size_t)p.nct * p.nz * 256 * sizeof(float)));
+    k.spin_limit = g_decode_spin_limit;
+    const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
+    if (a.base_dtype == 1) return launch_decode_bf16(k, ka.ksteps, pk, s);
+    if (a.base_dtype == 2) return launch_decode_f16(k, ka.ksteps, pk, s);
+    return launch_decode_f32(k, ka.ksteps, pk, s);
 }
 
 }  // namespace dels

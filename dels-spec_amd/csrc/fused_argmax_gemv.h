@@ -58,11 +58,6 @@ enum : int {
     B_ROWMAJOR = 2,       // [V, r] row-major: clamped row/column, masked data
 };
 
-__device__ __forceinline__ bf16x8 masked_bf16x8(u32x4 v, uint32_t mask) {
-    v.x &= mask; v.y &= mask; v.z &= mask; v.w &= mask;
-    return __builtin_bit_cast(bf16x8, v);
-}
-
 // Operands of one 16-row vocabulary tile held by a lane: the B MFMA operand for
 // every K step, and the four base logits and the prior of its column.
 template <int KSTEPS>

@@ -1,0 +1,11 @@
+// Instantiations of the fused decode-step kernel (rank projection + argmax,
+// M <= 16) for bf16_t base logits; one translation unit per base dtype.
+#include "lowrank_decode.h"
+
+namespace dels {
+
+hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s) {
+    return launch_decode_for_base<bf16_t>(ka, ksteps, prior_kind, s);
+}
+
+}  // namespace dels

@@ -150,24 +150,61 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
                 wp[j] = a.w + (int64_t)(wok[j] ? n : 0) * a.ldw + kg * 8;
             }
         }
-        for (int s = ks0 + wave; s < ks1; s += 4) {
+        // Wave w takes K steps ks0 + w + 4*it.  Operands are prefetched D
+        // iterations ahead in a register ring; every load is unconditional
+        // (clamped address; the data is masked when used), so the loop body is
+        // branch-free and each wait covers only the slot about to be used.
+        // Iterations past the wave's range contribute exact zeros.
+        constexpr int D = (WM + WN) <= 2 ? 8 : ((WM + WN) <= 4 ? 4 : 3);
+        const int n_iter = (ks1 - ks0 + 3) / 4;
+        const int s_fallback = min(ks0, a.ksteps - 1);
+        // Raw operand loads of iteration `it` (masks are applied at use, so no
+        // instruction needs the data before its MFMA).
+        auto load_iter = [&](int it, u32x4 (&xv)[WM], u32x4 (&wv)[WN]) {
+            const int s_raw = ks0 + wave + 4 * it;
+            const bool sok = s_raw < ks1;
+            const int s = sok ? s_raw : s_fallback;
             const int k = s * 32;
-            const bool kok = (k + kg * 8) < a.K;
-            bf16x8 xv[WM], wv[WN];
+            const bool kok = sok && (k + kg * 8) < a.K;
 #pragma unroll
-            for (int i = 0; i < WM; ++i) xv[i] = (kok && xok[i]) ? load_bf16x8(xp[i] + k) : zero_bf16x8();
+            for (int i = 0; i < WM; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xp[i] + (kok ? k : 0));
 #pragma unroll
             for (int j = 0; j < WN; ++j) {
                 if constexpr (WP)
-                    wv[j] = load_bf16x8_nt(wp[j] + (int64_t)s * 512);
+                    wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[j] + (int64_t)s * 512));
                 else
-                    wv[j] = (kok && wok[j]) ? load_bf16x8_nt(wp[j] + k) : zero_bf16x8();
+                    wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[j] + (kok ? k : 0)));
+            }
+        };
+        auto mma_iter = [&](int it, const u32x4 (&xv)[WM], const u32x4 (&wv)[WN]) {
+            const int s_raw = ks0 + wave + 4 * it;
+            const bool sok = s_raw < ks1;
+            const bool kok = sok && (s_raw * 32 + kg * 8) < a.K;
+            bf16x8 xo[WM], wo[WN];
+#pragma unroll
+            for (int i = 0; i < WM; ++i) xo[i] = masked_bf16x8(xv[i], (kok && xok[i]) ? 0xffffffffu : 0u);
+#pragma unroll
+            for (int j = 0; j < WN; ++j) {
+                if constexpr (WP)
+                    wo[j] = masked_bf16x8(wv[j], sok ? 0xffffffffu : 0u);
+                else
+                    wo[j] = masked_bf16x8(wv[j], (kok && wok[j]) ? 0xffffffffu : 0u);
             }
 #pragma unroll
             for (int i = 0; i < WM; ++i)
 #pragma unroll
                 for (int j = 0; j < WN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xv[i], wv[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xo[i], wo[j], acc[i][j], 0, 0, 0);
+        };
+        u32x4 rx[D][WM], rw[D][WN];
+#pragma unroll
+        for (int u = 0; u < D; ++u) load_iter(u, rx[u], rw[u]);
+        for (int it0 = 0; it0 < n_iter; it0 += D) {
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                mma_iter(it0 + u, rx[u], rw[u]);
+                load_iter(it0 + u + D, rx[u], rw[u]);
+            }
         }
     }
 
@@ -263,10 +300,10 @@ SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
         p.wm = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
     } else if (rows <= 16) {
         p.wm = 1; p.wn = 1;
-    } else if (rows <= 32) {
-        p.wm = 2; p.wn = 2;
     } else {
-        p.wm = 4; p.wn = 4;
+        // 32 x 32 output tiles: at M=512 the 64 x 64 tiles leave only 64
+        // workgroups before split-K and measured 29 us against 16 us here.
+        p.wm = 2; p.wn = 2;
     }
     p.m_wg = (int)cdiv(rows, 16 * p.wm);
     p.n_wg = (int)cdiv(cols, gru ? 16 : 16 * p.wn);
@@ -311,8 +348,7 @@ hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, si
     ka.out = a.rank; ka.ldout = a.ldrank;
     fill_ws(ka, p, ws, data_off);
     if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, a.a_packed, s);
-    if (p.wm == 2) return launch_skinny<2, 2, EPI_RANK>(ka, p, a.a_packed, s);
-    return launch_skinny<4, 4, EPI_RANK>(ka, p, a.a_packed, s);
+    return launch_skinny<2, 2, EPI_RANK>(ka, p, a.a_packed, s);
 }
 
 hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s) {

@@ -140,6 +140,16 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
                         void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * Test hook (no counterpart in the reference).  With M <= 16 rows and both
+ * weights in the MFMA-16 layout, dels_lowrank_argmax runs the rank projection
+ * and the argmax in one launch whose workgroups wait (bounded) for each other's
+ * rank tiles; a workgroup that polls `limit` times without seeing them computes
+ * the rank itself.  Sets that poll limit for later launches (0 forces the local
+ * computation) and returns the previous one.  Not thread-safe.
+ */
+int dels_debug_set_decode_spin_limit(int limit);
+
+/*
  * One GRU local-head step h_out = GRUCell(gi_table[tokens], h_in).
  * Replaces DeLSGraphRunner._gru_cell / _fused_gru_cell_kernel plus the
  * input-table gather (code/kernel/dels.py:140-211, 359-373, 432, 461).

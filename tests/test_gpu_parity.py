@@ -384,6 +384,72 @@ def test_lowrank_argmax_configs(pkg, dev, name):
     assert_parity(ids, score, rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
 
 
+# Few rows with both weights packed: the one-launch decode step (split rank
+# projection over all workgroups, then the argmax stream).  Every r it takes,
+# d that does and does not divide evenly over the K splits, 1..16 rows, bias,
+# silu, every base dtype and prior kind.
+DECODE_CASES = [
+    # M, d, r, act, bias, base dtype, prior dtype (None: no prior), V
+    (16, 4096, 512, "identity", False, torch.float32, torch.float32, 151936),
+    (16, 2560, 256, "silu", True, torch.bfloat16, torch.bfloat16, 151936),
+    (5, 1024, 128, "silu", False, torch.float16, None, 20011),
+    (1, 352, 64, "identity", True, torch.float32, torch.float16, 5003),
+    (9, 4096, 512, "silu", True, torch.bfloat16, torch.float32, 30000),
+]
+
+
+@pytest.mark.parametrize("M,d,r,act,bias,bdt,pdt,V", DECODE_CASES)
+def test_lowrank_decode_step(pkg, dev, M, d, r, act, bias, bdt, pdt, V):
+    print(f"case decode M={M} d={d} r={r} {act} bias={bias} base={bdt} prior={pdt} V={V}", flush=True)
+    x = pkg.synth.lowrank_inputs(M, d, r, V, base_dtype=bdt, prior_dtype=pdt or torch.float32, per_position=True,
+                                 seed=M + d + r)
+    g = torch.Generator().manual_seed(d)
+    rb = (torch.randn(r, generator=g) * 0.5).to(torch.bfloat16) if bias else None
+    xd = x.to(dev)
+    Ap, Bp = pkg.pack_operand(xd.A), pkg.pack_operand(xd.B)
+    prior = xd.prior if pdt is not None else None
+    ids, score = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, prior, xd.alpha, xd.beta, act=act,
+                                    rank_bias=None if rb is None else rb.to(dev))
+    torch.cuda.synchronize()
+    rank = oracle.rank_proj(f(x.h), f(x.A), None if rb is None else f(rb), act)
+    assert_parity(ids, score, rank, f(x.B), f(x.base), None if prior is None else f(x.prior), f(x.alpha),
+                  f(x.beta))
+
+
+def test_lowrank_decode_repeat_and_local_rank_fallback(pkg, dev):
+    """Back-to-back decode steps are bit-identical (the cross-workgroup hand-off
+    of rank tiles and counters resets itself), and with the rank-ready poll
+    limit forced to zero -- every workgroup computes the rank itself, as when the
+    grid is not co-resident -- the results still meet the parity rule."""
+    M, d, r, V = 16, 4096, 512, 151936
+    x = pkg.synth.config_inputs("qwen3_8b_m16")
+    xd = x.to(dev)
+    Ap, Bp = pkg.pack_operand(xd.A), pkg.pack_operand(xd.B)
+    first = None
+    for _ in range(10):
+        ids, score = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+        torch.cuda.synchronize()
+        if first is None:
+            first = (ids.clone(), score.clone())
+        else:
+            assert torch.equal(ids, first[0]) and torch.equal(score, first[1])
+    rank = oracle.rank_proj(f(x.h), f(x.A), None, x.act)
+    ref = oracle.fused_argmax(rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
+    assert_parity(first[0], first[1], rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta), ref=ref)
+    lib = pkg._lib.load()
+    prev = lib.dels_debug_set_decode_spin_limit(0)
+    try:
+        ids2, score2 = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+        torch.cuda.synchronize()
+    finally:
+        lib.dels_debug_set_decode_spin_limit(prev)
+    assert_parity(ids2, score2, rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta), ref=ref)
+    # and the normal path again, on the workspace the fallback call used
+    ids3, score3 = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+    torch.cuda.synchronize()
+    assert torch.equal(ids3, first[0]) and torch.equal(score3, first[1])
+
+
 def test_lowrank_argmax_m512_rows(pkg, dev):
     x = pkg.synth.config_inputs("qwen3_8b_m512")
     xd = x.to(dev)
