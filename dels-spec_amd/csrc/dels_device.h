@@ -83,6 +83,36 @@ __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) 
     return (v > bv) || (v == bv && i < bi);
 }
 
+// Direct-to-LDS loads: lane l's 16 (or 4) bytes from `g` land at LDS address
+// M0 + 16*l (4*l); `lds` must be wave-uniform.  Written as asm so that the
+// compiler does not track them: its own tracking cannot tell the stage buffers
+// apart and would make every LDS read wait for all loads in flight.  The waits
+// they need are the explicit vmcnt counts of stage_barrier().
+__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+}
+// Address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset.
+// The base is read from the first lane so that it is an SGPR pair whatever the
+// compiler can prove about its uniformity.
+__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+}
+// The compiler's hazard recognizer does not look inside asm, so the statement
+// carries its own wait states: a VMEM instruction needs 5 after a VALU write of
+// an SGPR it reads (the base pair comes from v_readfirstlane, often just before)
+// and an LDS-DMA instruction 1 after the SALU write of M0.  s_nop 4 gives 5.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds) {
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1"
+                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
+}
+__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds) {
+    asm volatile("s_nop 4\n\tglobal_load_lds_dword %0, %1"
+                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }

@@ -98,35 +98,6 @@ constexpr int loads_per_stage() {
     return (2 * KS) / kWaves + (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0);
 }
 
-// Direct-to-LDS loads: lane l's 16 (or 4) bytes from `g` land at LDS address
-// M0 + 16*l (4*l); `lds` must be wave-uniform.  Written as asm so that the
-// compiler does not track them: its own tracking cannot tell the stage buffers
-// apart and would make every LDS read wait for all loads in flight.  The waits
-// they need are the explicit vmcnt counts of stage_barrier().
-__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
-    return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
-}
-// Address = wave-uniform 64-bit base (SGPRs) + per-lane 32-bit byte offset.
-// The base is read from the first lane so that it is an SGPR pair whatever the
-// compiler can prove about its uniformity.
-__device__ __forceinline__ const void* sgpr_ptr(const void* p) {
-    const uint64_t v = (uint64_t)(uintptr_t)p;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return (const void*)(uintptr_t)(((uint64_t)hi << 32) | lo);
-}
-// An LDS-DMA instruction needs one wait state after the SALU write of M0 that
-// precedes it; the compiler cannot see that inside asm, so the s_nop is part
-// of the statement.
-__device__ __forceinline__ void dma16(const void* base, uint32_t off, void* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
-}
-__device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds) {
-    asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1"
-                 : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
-}
-
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding and all of its LDS operations are done (gfx9 s_waitcnt
 // encoding: vmcnt split over bits 3:0 and 15:14, expcnt 6:4 left at 7,
