@@ -11,8 +11,11 @@ Timing: ``--sets`` input sets (> 256 MB in total, so B cannot stay resident in
 the 256 MB MALL) are rotated step by step.  The K timed steps are one hipGraph
 of K consecutive draft steps (kernels back to back, no host launch overhead),
 bracketed by torch.cuda.synchronize() and HIP events on the launch stream.
-The dominant kernel's average duration comes from a second graph of K fused
-argmax launches only (rank precomputed), timed the same way.
+With packed weights at M <= 16 a step is one launch of the decode kernel
+(rank projection and fused argmax in one kernel), so the step graph times that
+kernel directly; at M=512 the dominant kernel, the fused argmax, is timed by a
+second graph of K argmax launches only (rank precomputed), the same way.  The
+argmax-only graph is reported at M=16 too, as a secondary figure.
 
 CPU baseline: the oracle (a numpy port of the reference semantics) on a
 bounded number of full calls of the same workload, on this host's cores.
@@ -58,10 +61,19 @@ def parse_args():
     return ap.parse_args()
 
 
-# Kernels of the fused argmax per workload (the tiled path adds its partials reduce).
-ARGMAX_KERNELS = {"qwen3_8b_m16": ("fused_argmax_gemv_kernel",),
-                  "qwen3_4b_m16": ("fused_argmax_gemv_kernel",),
-                  "qwen3_8b_m512": ("fused_argmax_tiled_kernel", "argmax_partials_reduce_kernel")}
+# The dominant kernel(s) of one step per workload, with packed weights.  At
+# M <= 16 the whole step (rank projection + fused argmax) is one launch of the
+# decode kernel; at M=512 the step runs the rank projection GEMM, then the tiled
+# argmax and its partials reduce, which dominate.
+ROOFLINE_KERNELS = {"qwen3_8b_m16": ("lowrank_decode_kernel",),
+                    "qwen3_4b_m16": ("lowrank_decode_kernel",),
+                    "qwen3_8b_m512": ("fused_argmax_tiled_kernel", "argmax_partials_reduce_kernel")}
+# With row-major weights the M=16 step is the rank projection and the GEMV argmax.
+ROWMAJOR_M16_KERNELS = ("fused_argmax_gemv_kernel",)
+
+
+def step_is_one_launch(workload, layout):
+    return layout == "packed" and workload in ("qwen3_8b_m16", "qwen3_4b_m16")
 
 
 def _counter_means(path):
@@ -108,12 +120,12 @@ def traffic_from(args):
                      "each scaled by copy_bytes / counter of a 512 MiB device copy"}
     # the default bench run covers these two workloads (the M=16 record and the M=512 one)
     for wl in ("qwen3_8b_m16", "qwen3_8b_m512"):
-        names = ARGMAX_KERNELS[wl]
+        names = ROOFLINE_KERNELS[wl]
         f, w = kib(fetch, "FETCH_SIZE", names), kib(write, "WRITE_SIZE", names)
         if f is None or w is None:
             continue
         out[wl] = {"kernels": list(names), "fetch_kib": f, "write_kib": w,
-                   "fused_argmax_hbm_bytes_per_launch": f * 1024.0 * fs + w * 1024.0 * ws}
+                   "hbm_bytes_per_launch": f * 1024.0 * fs + w * 1024.0 * ws}
     with open(args.traffic_file, "w") as fh:
         json.dump(out, fh, indent=1)
     print(json.dumps(out))
@@ -333,7 +345,19 @@ def main():
                 traffic_all = json.load(fh)
         except (OSError, ValueError):
             traffic_all = {}
-    traffic = traffic_all.get(args.workload, {}).get("fused_argmax_hbm_bytes_per_launch")
+    traffic = traffic_all.get(args.workload, {}).get("hbm_bytes_per_launch")
+    one_launch = step_is_one_launch(args.workload, args.layout)
+    if one_launch:
+        # the step is the decode kernel: its bytes are the whole step's
+        kernels = ROOFLINE_KERNELS[args.workload]
+        roof_bytes, roof_us = rec["step_bytes"], rec["us_per_step"]
+    else:
+        kernels = ROOFLINE_KERNELS[args.workload] if args.layout == "packed" or args.workload == "qwen3_8b_m512" \
+            else ROWMAJOR_M16_KERNELS
+        roof_bytes, roof_us = rec["argmax_bytes"], rec["us_fused_argmax"]
+        if args.layout != "packed":
+            traffic = None       # the committed counters are of the packed run
+    roof_gbs = roof_bytes / (roof_us * 1e-6) / 1e9
     out = {
         "metric": METRIC,
         "value": rec["rows_per_s"],
@@ -351,17 +375,21 @@ def main():
         "config": workload_desc(args.workload, x0, args.layout),
         "roofline": {
             "bound": "hbm",
-            "kernel": " + ".join(ARGMAX_KERNELS[args.workload]),
-            "achieved": rec["argmax_GBs"],
+            "kernel": " + ".join(kernels),
+            "achieved": roof_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": rec["argmax_GBs"] / HBM_PEAK_GBS,
+            "frac": roof_gbs / HBM_PEAK_GBS,
             "traffic": traffic,
-            "algorithmic_bytes": rec["argmax_bytes"],
-            "us_per_launch": rec["us_fused_argmax"],
+            "algorithmic_bytes": roof_bytes,
+            "us_per_launch": roof_us,
         },
         "step": {k: rec[k] for k in ("us_per_step", "step_bytes", "step_GBs", "hbm_frac_step", "step_TFLOPs",
                                      "mfma_frac_step")},
+        "fused_argmax_only": {"kernel": " + ".join(ROWMAJOR_M16_KERNELS if args.workload != "qwen3_8b_m512"
+                                                   else ROOFLINE_KERNELS[args.workload]),
+                              "us_per_launch": rec["us_fused_argmax"], "algorithmic_bytes": rec["argmax_bytes"],
+                              "GBs": rec["argmax_GBs"], "hbm_frac": rec["argmax_hbm_frac"]},
     }
     if args.also_m512 and args.workload != "qwen3_8b_m512":
         try:
@@ -371,8 +399,7 @@ def main():
             out["m512"] = {k: r512[k] for k in ("rows_per_s", "us_per_step", "us_fused_argmax", "argmax_GBs",
                                                 "argmax_hbm_frac", "argmax_TFLOPs", "argmax_mfma_frac",
                                                 "step_GBs", "hbm_frac_step", "step_TFLOPs", "mfma_frac_step")}
-            out["m512"]["argmax_traffic"] = traffic_all.get("qwen3_8b_m512", {}).get(
-                "fused_argmax_hbm_bytes_per_launch")
+            out["m512"]["argmax_traffic"] = traffic_all.get("qwen3_8b_m512", {}).get("hbm_bytes_per_launch")
             out["m512"]["argmax_algorithmic_bytes"] = r512["argmax_bytes"]
         except Exception as e:  # informative record only
             out["m512"] = {"error": repr(e)}

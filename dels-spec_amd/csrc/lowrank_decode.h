@@ -110,7 +110,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     __shared__ int s_idx[4][16];
     __shared__ int s_last;
     __shared__ int s_ready;
-    __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * KSTEPS * 32];   // local rank (fallback)
+    __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * KSTEPS * 32];   // the rank, [16][r] bf16
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -208,20 +208,22 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     }
     __syncthreads();
 
-    bf16x8 ra[KSTEPS];
+    // The rank lands in LDS (s_rank, 16 rows x r bf16) either way, then every
+    // wave takes its MFMA operands from there.
     if (s_ready) {
-        const bool mok = col < a.M;
-        const uint16_t* rp = d.rank_buf + (int64_t)col * r + kg * 8;
+        // Published by the tile reducers: read once per workgroup, a 64-byte
+        // share per thread, with device-coherent loads.
+        constexpr int kPer = r / 64;   // 8-byte words per thread
+        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(d.rank_buf);
+        unsigned long long* dst = reinterpret_cast<unsigned long long*>(s_rank);
+        unsigned long long w[kPer];
 #pragma unroll
-        for (int s = 0; s < KSTEPS; ++s) {
-            const unsigned long long* q = reinterpret_cast<const unsigned long long*>(rp + s * 32);
-            const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const u32x4 v = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-            ra[s] = masked_bf16x8(v, mok ? ~0u : 0u);
-        }
+        for (int i = 0; i < kPer; ++i)
+            w[i] = __hip_atomic_load(src + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = w[i];
     } else {
-        // Fallback: the whole rank in this workgroup, tile by tile, into LDS.
+        // Fallback: the whole rank in this workgroup, tile by tile.
         for (int cc = 0; cc < d.nct; ++cc) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
             for (int kb0 = 0; kb0 < d.ksa; kb0 += 4 * kDecodeMaxJ)
@@ -231,8 +233,12 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
                 const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
                 s_rank[m * r + cc * 16 + n] = decode_rank_epilogue(d, decode_tile_at(red, m, n), cc * 16 + n);
             }
-            __syncthreads();
+            __syncthreads();   // red is rewritten by the next tile's sum
         }
+    }
+    __syncthreads();
+    bf16x8 ra[KSTEPS];
+    {
         const bool mok = col < a.M;
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s)
