@@ -98,7 +98,7 @@ static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) 
 }
 
 struct RolloutLayout {
-    size_t part_off, argmax_off, total;   // rank projection and GRU steps run in turn and share the partials
+    size_t part_off, argmax_off, decode_off, total;   // the steps' kernels run in turn and share the partials
     SkinnyPlan rank_plan, gru_plan;
 };
 
@@ -108,7 +108,8 @@ static RolloutLayout rollout_layout(int64_t batch, int64_t G, int64_t r, int64_t
     L.gru_plan = plan_skinny(batch, G, G, true);
     L.part_off = kCtrlBytes;
     L.argmax_off = L.part_off + std::max(skinny_data_bytes(L.rank_plan), skinny_data_bytes(L.gru_plan));
-    L.total = L.argmax_off + align256(argmax_data_bytes(batch, r, V));
+    L.decode_off = L.argmax_off + align256(argmax_data_bytes(batch, r, V));
+    L.total = L.decode_off + decode_data_bytes(batch, G, r);
     return L;
 }
 
@@ -233,8 +234,6 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         ra.bias = static_cast<const uint16_t*>(p->rank_b); ra.act = p->act;
         ra.M = B; ra.d = G; ra.r = r;
         ra.rank = static_cast<uint16_t*>(p->rank); ra.ldrank = r;
-        e = launch_rank_proj(ra, L.rank_plan, ws, L.part_off, s);
-        if (e != hipSuccess) return hip_fail(e, "rank projection launch");
 
         ArgmaxArgs aa{};
         aa.rank = static_cast<const uint16_t*>(p->rank); aa.ldrank = r;
@@ -250,8 +249,17 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_ids = p->out_ids + step;
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
-        e = launch_fused_argmax(aa, ws, L.argmax_off, s);
-        if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
+
+        if (decode_eligible(B, G, r, ra.a_packed, aa.b_packed)) {
+            // rank projection and argmax in one launch
+            e = launch_lowrank_decode(ra, aa, ws, L.decode_off, s);
+            if (e != hipSuccess) return hip_fail(e, "fused decode step launch");
+        } else {
+            e = launch_rank_proj(ra, L.rank_plan, ws, L.part_off, s);
+            if (e != hipSuccess) return hip_fail(e, "rank projection launch");
+            e = launch_fused_argmax(aa, ws, L.argmax_off, s);
+            if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
+        }
 
         if (step + 1 < p->steps) {
             g.tokens = p->out_ids + step;

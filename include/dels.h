@@ -198,7 +198,8 @@ typedef struct dels_rollout {
     float* out_scores;      /* [batch, steps] fp32 or NULL */
     void* h_a;              /* [batch, G] bf16 state buffers (ping-pong) */
     void* h_b;
-    void* rank;             /* [batch, r] bf16 */
+    void* rank;             /* [batch, r] bf16 scratch for the rank (unused when the
+                               step runs as one fused launch: packed weights, batch <= 16) */
     void* ws;
     size_t ws_bytes;
 } dels_rollout;
