@@ -8,11 +8,15 @@ Public surface (mirrors the reference's interface for this path):
     per-step operators, each a thin wrapper over the C ABI in include/dels.h
   * ``pack_operand`` -- repack a weight into the MFMA-16 block layout the
     kernels stream at full HBM bandwidth
+  * ``quantize_pack_fp8``, ``fused_argmax_fp8``, ``lowrank_argmax_fp8`` -- the
+    fp8 (e4m3 weights, per-channel scales) variant of the same step
 """
 
 from .local_head import (DeLSLocalHead, load_unigram_log_prior, parse_scalar_schedule,
                          unigram_log_prior_from_counts)
-from .ops import PackedWeight, fused_argmax, gru_step, lowrank_argmax, pack_operand, rank_proj
+from .ops import (Fp8Weight, PackedWeight, fused_argmax, fused_argmax_fp8, gru_step, lowrank_argmax,
+                  lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows, quantize_pack_fp8,
+                  rank_proj)
 from .runner import DeLSGraphRunner
 from . import synth
 
@@ -28,5 +32,11 @@ __all__ = [
     "gru_step",
     "pack_operand",
     "PackedWeight",
+    "Fp8Weight",
+    "quantize_e4m3_rows",
+    "pack_operand_fp8",
+    "quantize_pack_fp8",
+    "fused_argmax_fp8",
+    "lowrank_argmax_fp8",
     "synth",
 ]

@@ -20,6 +20,7 @@ DELS_OK = 0
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_IDENTITY, ACT_SILU = 0, 1
 LAYOUT_ROWMAJOR, LAYOUT_MFMA16 = 0, 1
+LAYOUT_FP8_K128, LAYOUT_FP8_K32 = 2, 3
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -77,6 +78,15 @@ SIGNATURES = {
     "dels_graph_create": (_int, [ctypes.POINTER(RolloutParams), ctypes.POINTER(_ptr)]),
     "dels_graph_launch": (_int, [_ptr, _ptr]),
     "dels_graph_destroy": (_int, [_ptr]),
+    "dels_packed_fp8_bytes": (_sz, [_i64, _i64, _int]),
+    "dels_pack_operand_fp8": (_int, [_ptr, _i64, _i64, _i64, _int, _ptr, _sz, _ptr]),
+    "dels_fused_argmax_fp8_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_fused_argmax_fp8": (_int, [_ptr, _i64, _ptr, _fptr, _ptr, _i64, _int, _ptr, _int, _fptr, _i64, _fptr,
+                                     _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_lowrank_argmax_fp8_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
+    "dels_lowrank_argmax_fp8": (_int, [_ptr, _i64, _ptr, _fptr, _ptr, _int, _ptr, _fptr, _ptr, _i64, _int, _ptr,
+                                       _int, _fptr, _i64, _fptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64,
+                                       _ptr, _sz, _ptr]),
 }
 
 _lock = threading.Lock()

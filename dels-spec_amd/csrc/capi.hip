@@ -72,6 +72,11 @@ static int check_bf16_matrix(const void* p, int64_t ld, int64_t cols, const char
 // Checks of a bf16 weight operand in either layout.
 static int check_weight(const void* p, int64_t ld, int64_t cols, int layout, const char* name) {
     if (layout == DELS_LAYOUT_ROWMAJOR) return check_bf16_matrix(p, ld, cols, name);
+    if (layout == DELS_LAYOUT_FP8_K128 || layout == DELS_LAYOUT_FP8_K32) {
+        if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+        if (!aligned16(p)) return fail(DELS_ERR_ALIGNMENT, "packed fp8 %s must be 16-byte aligned", name);
+        return DELS_OK;
+    }
     if (layout != DELS_LAYOUT_MFMA16) return fail(DELS_ERR_INVALID_ARGUMENT, "%s: unknown layout %d", name, layout);
     if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
     if (!aligned16(p)) return fail(DELS_ERR_ALIGNMENT, "packed %s must be 16-byte aligned", name);
@@ -444,6 +449,132 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     if (e != hipSuccess) return hip_fail(e, "rank projection launch");
     e = launch_fused_argmax(a, ws, L.argmax_off, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
+}
+
+// ---- fp8 variant ---------------------------------------------------------------
+
+static int check_scale(const float* p, const char* name) {
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+    if ((reinterpret_cast<uintptr_t>(p) & 3u) != 0) return fail(DELS_ERR_ALIGNMENT, "%s must be 4-byte aligned", name);
+    return DELS_OK;
+}
+
+static bool fp8_rank_ok(int64_t r) { return r == 128 || r == 256 || r == 512; }
+
+size_t dels_packed_fp8_bytes(int64_t rows, int64_t cols, int layout) {
+    if (rows <= 0 || cols <= 0 || (layout != DELS_LAYOUT_FP8_K128 && layout != DELS_LAYOUT_FP8_K32)) return 0;
+    return packed_fp8_bytes(rows, cols, layout == DELS_LAYOUT_FP8_K128 ? FP8_K128 : FP8_K32);
+}
+
+int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t cols, int layout, void* packed,
+                          size_t packed_bytes_, void* stream) {
+    if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
+    if (layout != DELS_LAYOUT_FP8_K128 && layout != DELS_LAYOUT_FP8_K32)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "unknown fp8 layout %d", layout);
+    if (rows == 0 || cols == 0) return DELS_OK;
+    if (!Wq) return fail(DELS_ERR_INVALID_ARGUMENT, "W (to pack) is NULL");
+    if (rows > 1 && ldw < cols) return fail(DELS_ERR_INVALID_ARGUMENT, "W leading dimension %lld < cols %lld",
+                                            (long long)ldw, (long long)cols);
+    if (!packed || !aligned16(packed)) return fail(DELS_ERR_ALIGNMENT, "packed output must be 16-byte aligned");
+    const size_t need = dels_packed_fp8_bytes(rows, cols, layout);
+    if (packed_bytes_ < need)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "packed output too small: %zu bytes given, %zu needed", packed_bytes_,
+                    need);
+    hipError_t e = launch_pack_fp8(static_cast<const uint8_t*>(Wq), ldw, rows, cols,
+                                   layout == DELS_LAYOUT_FP8_K128 ? FP8_K128 : FP8_K32, static_cast<uint8_t*>(packed),
+                                   static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 pack launch");
+}
+
+size_t dels_fused_argmax_fp8_ws_bytes(int64_t, int64_t, int64_t) { return kCtrlBytes; }
+
+static void fill_argmax_fp8(ArgmaxArgs& a, const void* Bq, const float* b_scale, const void* base, int64_t ldbase,
+                            int base_dtype, const void* prior, int prior_dtype, const float* alpha,
+                            int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t r,
+                            int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out) {
+    a.B = static_cast<const uint16_t*>(Bq); a.ldb = 0; a.b_packed = true;
+    a.b_scale = b_scale;
+    a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
+    a.prior = prior; a.prior_dtype = prior_dtype;
+    a.alpha = alpha; a.alpha_stride = alpha_stride;
+    a.beta = beta; a.beta_stride = beta_stride;
+    a.M = (int)M; a.r = (int)r; a.V = (int)V;
+    a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
+}
+
+int dels_fused_argmax_fp8(const void* rank, int64_t ldrank, const void* Bq, const float* b_scale, const void* base,
+                          int64_t ldbase, int base_dtype, const void* prior, int prior_dtype, const float* alpha,
+                          int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t r,
+                          int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
+                          void* stream) {
+    int rc = check_argmax_args(rank, ldrank, Bq, 0, DELS_LAYOUT_FP8_K128, base, ldbase, base_dtype, prior,
+                               prior_dtype, alpha, alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, true);
+    if (rc != DELS_OK) return rc;
+    if (!fp8_rank_ok(r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax needs r in {128, 256, 512} (got %lld)",
+                                     (long long)r);
+    if (!argmax_fp8_supported(M, r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax: too many rows");
+    if (M == 0) return DELS_OK;
+    if ((rc = check_scale(b_scale, "b_scale")) != DELS_OK) return rc;
+    if ((rc = check_ws(ws, ws_bytes, dels_fused_argmax_fp8_ws_bytes(M, r, V))) != DELS_OK) return rc;
+    ArgmaxArgs a{};
+    a.rank = static_cast<const uint16_t*>(rank); a.ldrank = ldrank;
+    fill_argmax_fp8(a, Bq, b_scale, base, ldbase, base_dtype, prior, prior_dtype, alpha, alpha_stride, beta,
+                    beta_stride, M, r, V, out_ids, out_score, ld_out);
+    hipError_t e = launch_fused_argmax_fp8(a, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
+}
+
+size_t dels_lowrank_argmax_fp8_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) {
+    return dels_lowrank_argmax_ws_bytes(M, d, r, V);
+}
+
+int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const float* a_scale, const void* bias,
+                            int act, const void* Bq, const float* b_scale, const void* base, int64_t ldbase,
+                            int base_dtype, const void* prior, int prior_dtype, const float* alpha,
+                            int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t d,
+                            int64_t r, int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws,
+                            size_t ws_bytes, void* stream) {
+    int rc = check_argmax_args(nullptr, r, Bq, 0, DELS_LAYOUT_FP8_K128, base, ldbase, base_dtype, prior, prior_dtype,
+                               alpha, alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, false);
+    if (rc != DELS_OK) return rc;
+    if (!fp8_rank_ok(r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax needs r in {128, 256, 512} (got %lld)",
+                                     (long long)r);
+    if (!argmax_fp8_supported(M, r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax: too many rows");
+    if (d <= 0 || d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8",
+                                          (long long)d);
+    if (act != DELS_ACT_IDENTITY && act != DELS_ACT_SILU)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
+    if (M == 0) return DELS_OK;
+    if ((rc = check_bf16_matrix(h, ldh, d, "h")) != DELS_OK) return rc;
+    if ((rc = check_weight(Aq, 0, d, DELS_LAYOUT_FP8_K32, "A_q (rank projection)")) != DELS_OK) return rc;
+    if ((rc = check_scale(a_scale, "a_scale")) != DELS_OK) return rc;
+    if ((rc = check_scale(b_scale, "b_scale")) != DELS_OK) return rc;
+    const LowrankLayout L = lowrank_layout(M, d, r, V);
+    if (!skinny_supported(L.plan)) return fail(DELS_ERR_UNSUPPORTED, "rank projection shape needs too many tiles");
+    if ((rc = check_ws(ws, ws_bytes, L.total)) != DELS_OK) return rc;
+    char* w = static_cast<char*>(ws);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint16_t* rank = reinterpret_cast<uint16_t*>(w + L.rank_off);
+    RankArgs ra{};
+    ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
+    ra.A = static_cast<const uint16_t*>(Aq); ra.lda = 0; ra.a_packed = true;
+    ra.a_scale = a_scale;
+    ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
+    ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
+    ra.rank = rank; ra.ldrank = r;
+    ArgmaxArgs a{};
+    a.rank = rank; a.ldrank = r;
+    fill_argmax_fp8(a, Bq, b_scale, base, ldbase, base_dtype, prior, prior_dtype, alpha, alpha_stride, beta,
+                    beta_stride, M, r, V, out_ids, out_score, ld_out);
+    hipError_t e;
+    if (decode8_eligible(M, d, r)) {
+        e = launch_lowrank_decode(ra, a, ws, L.decode_off, s);
+        return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused decode step launch");
+    }
+    e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
+    if (e != hipSuccess) return hip_fail(e, "fp8 rank projection launch");
+    e = launch_fused_argmax_fp8(a, ws, s);
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
 }
 
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {

@@ -42,6 +42,7 @@ bool skinny_supported(const SkinnyPlan& p);
 struct RankArgs {
     const uint16_t* h; int64_t ldh;
     const uint16_t* A; int64_t lda; bool a_packed;
+    const float* a_scale = nullptr;   // non-null: A is e4m3 in K32 blocks, this its per-column scale [r]
     const uint16_t* bias; int act;
     int M, d, r;
     uint16_t* rank; int64_t ldrank;
@@ -64,6 +65,7 @@ hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size
 struct ArgmaxArgs {
     const uint16_t* rank; int64_t ldrank;
     const uint16_t* B; int64_t ldb; bool b_packed;
+    const float* b_scale = nullptr;   // non-null: B is e4m3 in K128 blocks, this its per-row scale [V]
     const void* base; int64_t ldbase; int base_dtype;
     const void* prior; int prior_dtype;
     const float* alpha; int64_t alpha_stride;
@@ -78,13 +80,20 @@ bool argmax_supported(int64_t M, int64_t r, int64_t V);
 // `ws` is the workspace base (control area); partials go to ws + data_off.
 hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
+// fp8 argmax (b_scale set): r in {128, 256, 512}, any M up to kMaxKeyRows.
+bool argmax_fp8_supported(int64_t M, int64_t r);
+hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, hipStream_t s);
+
 // ---- fused decode step: rank projection + argmax in one launch (M <= 16) --------
 
 // Both weights packed, r/32 in {2, 4, 8, 16}, d a multiple of 32 and at most
 // 32 K blocks per split of the rank projection.
 bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed);
+// The fp8 decode step (A e4m3 K32, B e4m3 K128): as above with r in {128, 256, 512}.
+bool decode8_eligible(int64_t M, int64_t d, int64_t r);
 // Data-region bytes of the decode step (rank partials and the shared bf16 rank).
 size_t decode_data_bytes(int64_t M, int64_t d, int64_t r);
+// fp8 when ra.a_scale and aa.b_scale are set (decode8_eligible), bf16 otherwise.
 hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, size_t data_off,
                                  hipStream_t s);
 // Polls of the rank-ready count before a workgroup computes the rank itself
@@ -102,6 +111,15 @@ inline size_t packed_bytes(int64_t rows, int64_t cols) {
 }
 hipError_t launch_pack_mfma16(const uint16_t* W, int64_t ldw, int64_t rows, int64_t cols, uint16_t* P,
                               hipStream_t s);
+// e4m3 layouts: K128 (16 x 128 blocks of 2 KiB, the fp8 argmax's B) and K32
+// (16 x 32 blocks of 512 bytes, the fp8 rank projection's A).
+enum : int { FP8_K128 = 2, FP8_K32 = 3 };
+inline size_t packed_fp8_bytes(int64_t rows, int64_t cols, int layout) {
+    const int64_t kb = layout == FP8_K128 ? 128 : 32;
+    return (size_t)((rows + 15) / 16) * (size_t)((cols + kb - 1) / kb) * (size_t)(16 * kb);
+}
+hipError_t launch_pack_fp8(const uint8_t* W, int64_t ldw, int64_t rows, int64_t cols, int layout, uint8_t* P,
+                           hipStream_t s);
 
 // Device properties of the current device (cached per device id).
 int device_cu_count();

@@ -1,0 +1,126 @@
+// fp8 (OCP float8 e4m3fn) support: the format of the fp8 weights, its
+// conversions, and the operand pieces of the fp8 argmax kernels.
+//
+// e4m3fn: sign, 4 exponent bits (bias 7), 3 mantissa bits; no infinities,
+// 0x7F/0xFF are NaN, the largest finite magnitude is 448.  gfx950's fp8 MFMAs
+// (v_mfma_scale_f32_16x16x128_f8f6f4 with format code 0) read this format.
+//
+// Packed fp8 layouts (built by pack.hip):
+//  * K128 (B, the low-rank LM head): 16-row x 128-column blocks of 2 KiB,
+//    row-block-major.  Lane l of a wave owns row l%16 and the 32 consecutive
+//    columns 32*(l/16) .. +31 of the block, stored as two 1 KiB halves
+//    [half][lane][16 bytes], so each half is one coalesced dwordx4 per lane.
+//    The MFMA pairs the A and B operands by (lane group, byte), so any K order
+//    that both operands share gives the same dot product; the rank operand is
+//    built in this same order.
+//  * K32 (A, the rank projection weight): the MFMA-16 bf16 block order with
+//    one byte per element: 16-row x 32-column blocks of 512 bytes, lane l
+//    holding row l%16, columns 8*(l/16) .. +7.  The rank projection keeps h in
+//    bf16, so these bytes are widened to bf16 in registers (exactly: every
+//    e4m3 value is a bf16 value) and fed to the bf16 MFMA.
+#pragma once
+
+#include "dels_device.h"
+
+namespace dels {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kE4M3Max = 448.f;
+constexpr int kFp8K128Block = 2048;   // bytes of a K128 block
+constexpr int kFp8K32Block = 512;     // bytes of a K32 block
+
+// Round a finite fp32 value to the e4m3fn grid (to nearest, ties to even;
+// magnitudes from 464, the midpoint between 448 and the next binade step,
+// saturate to 448) and encode it.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+    const uint32_t sign = (__float_as_uint(x) >> 24) & 0x80u;
+    const float a = __builtin_fabsf(x);
+    uint32_t code;
+    if (a >= 464.f) {
+        code = 0x7Eu;
+    } else if (a < 0.015625f) {
+        // below 2^-6: the subnormal grid, quantum 2^-9; 8 encodes 2^-6, the first normal
+        code = (uint32_t)__builtin_rintf(a * 512.f);
+    } else {
+        uint32_t b = __float_as_uint(a);
+        b += 0x7FFFFu + ((b >> 20) & 1u);                       // 3 mantissa bits, ties to even
+        code = (((b >> 23) - 120u) << 3) | ((b >> 20) & 7u);    // exponent rebiased from 127 to 7
+    }
+    return sign | code;
+}
+
+// e4m3fn byte -> bf16 bits (exact).  NaN codes are not produced by absmax
+// quantisation and are not expected here.
+__device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t q) {
+    const uint32_t s = (q & 0x80u) << 8, e = (q >> 3) & 15u, m = q & 7u;
+    const uint32_t mag = e ? (((e + 120u) << 7) | (m << 4)) : (__float_as_uint((float)m * 0x1p-9f) >> 16);
+    return s | mag;
+}
+
+// Eight e4m3 bytes (little-endian in lo, hi) widened to the bf16x8 operand.
+__device__ __forceinline__ u32x4 widen_e4m3x8(uint32_t lo, uint32_t hi) {
+    u32x4 o;
+    o[0] = e4m3_to_bf16_bits(lo & 0xffu) | (e4m3_to_bf16_bits((lo >> 8) & 0xffu) << 16);
+    o[1] = e4m3_to_bf16_bits((lo >> 16) & 0xffu) | (e4m3_to_bf16_bits(lo >> 24) << 16);
+    o[2] = e4m3_to_bf16_bits(hi & 0xffu) | (e4m3_to_bf16_bits((hi >> 8) & 0xffu) << 16);
+    o[3] = e4m3_to_bf16_bits((hi >> 16) & 0xffu) | (e4m3_to_bf16_bits(hi >> 24) << 16);
+    return o;
+}
+
+// 16x16 fp32 += A(16 x 128 e4m3) . B(128 x 16 e4m3), unit block scales.
+__device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8& b, f32x4 acc) {
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
+}
+
+// The rank rows as the e4m3 A operand of KS8 K128 blocks.  `rowp` points at
+// element 32*(lane/16) of the lane's rank row (bf16, global or LDS); lanes of
+// rows outside the batch pass mok = false and get zeros.  Each row is
+// quantised on its own: scale = absmax / 448 (1 for an all-zero row),
+// q = e4m3(v / scale).  Returns the scale of the lane's row (l%16).
+template <int KS8>
+__device__ __forceinline__ float quantize_rank_rows(const uint16_t* rowp, bool mok, i32x8 (&rq)[KS8]) {
+#pragma clang fp contract(off)
+    u32x4 raw[KS8][4];
+#pragma unroll
+    for (int j = 0; j < KS8; ++j)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(rowp + 128 * j + 8 * p);
+            raw[j][p] = mok ? v : u32x4{0u, 0u, 0u, 0u};
+        }
+    float amax = 0.f;
+#pragma unroll
+    for (int j = 0; j < KS8; ++j)
+#pragma unroll
+        for (int p = 0; p < 4; ++p)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[j][p][e] << 16)));
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[j][p][e] & 0xffff0000u)));
+            }
+    // the row's four lane groups (lanes l, l^16, l^32, l^48)
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
+    const float scale = amax > 0.f ? amax / kE4M3Max : 1.f;
+#pragma unroll
+    for (int j = 0; j < KS8; ++j)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const float x0 = __uint_as_float(raw[j][p][e] << 16);
+                const float x1 = __uint_as_float(raw[j][p][e] & 0xffff0000u);
+                w0 |= (f32_to_e4m3(x0 / scale) | (f32_to_e4m3(x1 / scale) << 8)) << (16 * e);
+                const float y0 = __uint_as_float(raw[j][p][e + 2] << 16);
+                const float y1 = __uint_as_float(raw[j][p][e + 2] & 0xffff0000u);
+                w1 |= (f32_to_e4m3(y0 / scale) | (f32_to_e4m3(y1 / scale) << 8)) << (16 * e);
+            }
+            rq[j][2 * p] = (int)w0;
+            rq[j][2 * p + 1] = (int)w1;
+        }
+    return scale;
+}
+
+}  // namespace dels

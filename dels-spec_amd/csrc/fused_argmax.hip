@@ -3,6 +3,7 @@
 // rows) and of the MFMA-tiled kernel (fused_argmax_tiled.h, many rows).
 #include <algorithm>
 
+#include "fused_argmax_fp8.h"
 #include "fused_argmax_gemv.h"
 #include "fused_argmax_tiled.h"
 #include "lowrank_decode.h"
@@ -129,6 +130,34 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
     return launch_gemv_f32(ka, a.b_packed, pk, s);
 }
 
+// ---- fp8 argmax ------------------------------------------------------------
+
+bool argmax_fp8_supported(int64_t M, int64_t r) {
+    return (r == 128 || r == 256 || r == 512) && M >= 0 && M <= kMaxKeyRows;
+}
+
+hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, hipStream_t s) {
+    const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
+    char* w = static_cast<char*>(ws);
+    ArgmaxKArgs ka{};
+    ka.rank = a.rank; ka.ldrank = a.ldrank;
+    ka.B = a.B; ka.ldb = 0;
+    ka.b_scale = a.b_scale;
+    ka.base = a.base; ka.ldbase = a.ldbase;
+    ka.prior = a.prior;
+    ka.alpha = a.alpha; ka.alpha_stride = a.alpha_stride;
+    ka.beta = a.beta; ka.beta_stride = a.beta_stride;
+    ka.M = a.M; ka.r = a.r; ka.V = a.V;
+    ka.ksteps = a.r / 32;
+    ka.out_ids = a.out_ids; ka.out_score = a.out_score; ka.ld_out = a.ld_out;
+    ka.counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
+    ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
+    ka.key_stride = (int64_t)a.M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
+    if (a.base_dtype == 1) return launch_gemv8_bf16(ka, pk, s);
+    if (a.base_dtype == 2) return launch_gemv8_f16(ka, pk, s);
+    return launch_gemv8_f32(ka, pk, s);
+}
+
 // ---- fused decode step ------------------------------------------------------
 
 namespace {
@@ -160,6 +189,10 @@ bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_pack
     if (d < 32 || d % 32 != 0) return false;
     const DecodePlan p = decode_plan(d, r);
     return kDecodeWGs % p.nct == 0 && (p.kpz + 3) / 4 <= kDecodeMaxJ;
+}
+
+bool decode8_eligible(int64_t M, int64_t d, int64_t r) {
+    return (r == 128 || r == 256 || r == 512) && decode_eligible(M, d, r, true, true);
 }
 
 size_t decode_data_bytes(int64_t M, int64_t d, int64_t r) {
@@ -197,6 +230,13 @@ hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* 
     k.rank_buf = reinterpret_cast<uint16_t*>(w + data_off + align256((size_t)p.nct * p.nz * 256 * sizeof(float)));
     k.spin_limit = g_decode_spin_limit;
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
+    if (ra.a_scale != nullptr) {
+        k.a_scale = ra.a_scale;
+        ka.b_scale = a.b_scale;
+        if (a.base_dtype == 1) return launch_decode8_bf16(k, pk, s);
+        if (a.base_dtype == 2) return launch_decode8_f16(k, pk, s);
+        return launch_decode8_f32(k, pk, s);
+    }
     if (a.base_dtype == 1) return launch_decode_bf16(k, ka.ksteps, pk, s);
     if (a.base_dtype == 2) return launch_decode_f16(k, ka.ksteps, pk, s);
     return launch_decode_f32(k, ka.ksteps, pk, s);

@@ -1,11 +1,16 @@
 // Instantiations of the fused argmax GEMV kernel for float base logits (one
 // translation unit per base dtype keeps the build parallel).
+#include "fused_argmax_fp8.h"
 #include "fused_argmax_gemv.h"
 
 namespace dels {
 
 hipError_t launch_gemv_f32(const ArgmaxKArgs& ka, bool packed, int prior_kind, hipStream_t s) {
     return launch_gemv_for_base<float>(ka, packed, prior_kind, s);
+}
+
+hipError_t launch_gemv8_f32(const ArgmaxKArgs& ka, int prior_kind, hipStream_t s) {
+    return launch_gemv8_for_base<float>(ka, prior_kind, s);
 }
 
 }  // namespace dels

@@ -49,6 +49,7 @@ struct ArgmaxKArgs {
     unsigned long long* keys;   // row m at keys[m * key_stride]
     int64_t key_stride;
     unsigned int* counter;
+    const float* b_scale;       // fp8 B only: per-vocabulary-row scale [V]
 };
 
 // How the B operand is addressed.
@@ -99,6 +100,86 @@ __device__ __forceinline__ void load_tile(const ArgmaxKArgs& a, int t, int lane,
     for (int q = 0; q < 4; ++q) tr.base[q] = load_f32(brow[q] + vc);
     if constexpr (!is_no_prior<PriorT>::value) tr.prior = load_f32(prior + vc);
     else tr.prior = 0.f;
+}
+
+// End of a workgroup's share of the argmax over rows m0 .. m0+15: reduce the
+// lanes' running (score, index) pairs over the 16 vocabulary columns and the
+// four waves, fold each row into its 64-bit key with a device-scope atomic max,
+// count the workgroup in, and let the last one decode and clear the keys, the
+// counter and `also_clear` (when given).
+__device__ __forceinline__ void argmax_wg_finish(const ArgmaxKArgs& a, float (&best)[4], int (&bidx)[4], int m0,
+                                                 float (&s_val)[4][16], int (&s_idx)[4][16], int& s_last,
+                                                 unsigned int* also_clear) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int kg = lane >> 4;
+    // Reduce over the 16 vocabulary columns of each row (lanes sharing kg).
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const float ov = __shfl_xor(best[q], off, 64);
+            const int oi = __shfl_xor(bidx[q], off, 64);
+            if (argmax_better(ov, oi, best[q], bidx[q])) {
+                best[q] = ov;
+                bidx[q] = oi;
+            }
+        }
+    }
+    if (col == 0) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            s_val[wave][4 * kg + q] = best[q];
+            s_idx[wave][4 * kg + q] = bidx[q];
+        }
+    }
+    __syncthreads();
+
+    unsigned long long seen = 0;
+    if (threadIdx.x < 16) {
+        const int mi = threadIdx.x;
+        float bvv = s_val[0][mi];
+        int bii = s_idx[0][mi];
+#pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            if (argmax_better(s_val[w][mi], s_idx[w][mi], bvv, bii)) {
+                bvv = s_val[w][mi];
+                bii = s_idx[w][mi];
+            }
+        }
+        const int m = m0 + mi;
+        if (m < a.M && bii != INT_MAX)
+            seen = __hip_atomic_fetch_max(&a.keys[(int64_t)m * a.key_stride], pack_argmax(bvv, (uint32_t)bii),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Using the returned value makes the atomic a returning one: the branch
+    // below cannot resolve before the update has been performed.
+    if (seen == ~0ull) s_last = 2;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned total = gridDim.x * gridDim.y;
+        const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == total - 1);
+    }
+    __syncthreads();
+    if (s_last != 1) return;
+    for (int m = threadIdx.x; m < a.M; m += blockDim.x) {
+        const unsigned long long key = __hip_atomic_exchange(&a.keys[(int64_t)m * a.key_stride], 0ull,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t idx = ~(uint32_t)(key & 0xffffffffull);
+        float val = f32_from_order_key((uint32_t)(key >> 32));
+        if (key == 0ull || idx >= (uint32_t)a.V) {   // no candidate at all (every score NaN)
+            idx = 0;
+            val = -__builtin_inff();
+        }
+        a.out_ids[(int64_t)m * a.ld_out] = (int64_t)idx;
+        if (a.out_score) a.out_score[(int64_t)m * a.ld_out] = val;
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_exchange(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (also_clear) __hip_atomic_exchange(also_clear, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 template <int KSTEPS, int MODE, typename BaseT, typename PriorT>
@@ -193,69 +274,7 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
             consume(ta, t);
     }
 
-    // Reduce over the 16 vocabulary columns of each row (lanes sharing kg).
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-            const float ov = __shfl_xor(best[q], off, 64);
-            const int oi = __shfl_xor(bidx[q], off, 64);
-            if (argmax_better(ov, oi, best[q], bidx[q])) {
-                best[q] = ov;
-                bidx[q] = oi;
-            }
-        }
-    }
-    if (col == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            s_val[wave][4 * kg + q] = best[q];
-            s_idx[wave][4 * kg + q] = bidx[q];
-        }
-    }
-    __syncthreads();
-
-    unsigned long long seen = 0;
-    if (threadIdx.x < 16) {
-        const int mi = threadIdx.x;
-        float bvv = s_val[0][mi];
-        int bii = s_idx[0][mi];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            if (argmax_better(s_val[w][mi], s_idx[w][mi], bvv, bii)) {
-                bvv = s_val[w][mi];
-                bii = s_idx[w][mi];
-            }
-        }
-        const int m = m0 + mi;
-        if (m < a.M && bii != INT_MAX)
-            seen = __hip_atomic_fetch_max(&a.keys[(int64_t)m * a.key_stride], pack_argmax(bvv, (uint32_t)bii),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // Using the returned value makes the atomic a returning one: the branch
-    // below cannot resolve before the update has been performed.
-    if (seen == ~0ull) s_last = 2;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned total = gridDim.x * gridDim.y;
-        const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == total - 1);
-    }
-    __syncthreads();
-    if (s_last != 1) return;
-    for (int m = threadIdx.x; m < a.M; m += blockDim.x) {
-        const unsigned long long key = __hip_atomic_exchange(&a.keys[(int64_t)m * a.key_stride], 0ull,
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t idx = ~(uint32_t)(key & 0xffffffffull);
-        float val = f32_from_order_key((uint32_t)(key >> 32));
-        if (key == 0ull || idx >= (uint32_t)a.V) {   // no candidate at all (every score NaN)
-            idx = 0;
-            val = -__builtin_inff();
-        }
-        a.out_ids[(int64_t)m * a.ld_out] = (int64_t)idx;
-        if (a.out_score) a.out_score[(int64_t)m * a.ld_out] = val;
-    }
-    if (threadIdx.x == 0) __hip_atomic_exchange(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    argmax_wg_finish(a, best, bidx, m0, s_val, s_idx, s_last, nullptr);
 }
 
 // Launch of one instantiation on about one workgroup per CU in total (the

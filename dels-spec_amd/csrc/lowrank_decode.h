@@ -22,8 +22,14 @@
 // work shares the device), the workgroup computes the whole rank itself -- slow
 // but correct -- so the kernel always terminates.  The last workgroup of the
 // argmax reduction returns every counter to zero.
+//
+// The fp8 variant (lowrank_decode8_kernel) runs the same phases with the rank
+// projection weight A as e4m3 (K32 blocks, widened to bf16 in registers, its
+// per-column scale applied before the bias) and the argmax of fused_argmax_fp8.h
+// (the rank quantised per row to e4m3, B as e4m3 K128 blocks).
 #pragma once
 
+#include "fused_argmax_fp8.h"
 #include "fused_argmax_gemv.h"
 
 namespace dels {
@@ -34,7 +40,8 @@ constexpr int kDecodeMaxJ = 8;           // K steps per wave in the split rank p
 struct DecodeKArgs {
     ArgmaxKArgs am;                      // argmax part; am.rank is unused (rank_buf)
     const uint16_t* h; int64_t ldh;      // [M, d] bf16
-    const uint16_t* A;                   // [r, d] bf16 in MFMA-16 blocks: r/16 block rows x d/32 K blocks
+    const void* A;                       // [r, d] in blocks of 16 rows x 32 K: bf16 (1 KiB) or e4m3 (512 B)
+    const float* a_scale;                // e4m3 A only: per-rank-column scale [r]
     const uint16_t* bias; int act;
     int ksa;                             // d / 32
     int nct, nz, kpz;                    // rank column tiles (r/16), K splits, K blocks per split
@@ -47,26 +54,36 @@ struct DecodeKArgs {
 
 // fp32 dot of rank column tile c over K blocks [kb0, kb1) for the 16 rows,
 // this wave taking every 4th block from kb0 + wave (all loads issued first).
+// A8: A holds e4m3 bytes, widened to bf16 at use.
+template <bool A8>
 __device__ __forceinline__ f32x4 decode_rank_partial(const DecodeKArgs& d, int M, int c, int kb0, int kb1,
                                                      int wave, int lane) {
     const int col = lane & 15, kg = lane >> 4;
     const bool mok = col < M;
     const uint16_t* hp = d.h + (int64_t)(mok ? col : 0) * d.ldh + kg * 8;
-    const uint16_t* ap = d.A + (int64_t)c * d.ksa * 512 + lane * 8;
     u32x4 xv[kDecodeMaxJ], wv[kDecodeMaxJ];
 #pragma unroll
     for (int j = 0; j < kDecodeMaxJ; ++j) {
         const int kb = kb0 + wave + 4 * j;
         const int kc = kb < kb1 ? kb : min(kb0, d.ksa - 1);   // a valid block when masked
         xv[j] = *reinterpret_cast<const u32x4*>(hp + kc * 32);
-        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
+        if constexpr (A8) {
+            const uint8_t* ap = static_cast<const uint8_t*>(d.A) + ((int64_t)c * d.ksa + kc) * kFp8K32Block + lane * 8;
+            const u32x2 q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(ap));
+            wv[j] = u32x4{q[0], q[1], 0u, 0u};
+        } else {
+            const uint16_t* ap = static_cast<const uint16_t*>(d.A) + (int64_t)c * d.ksa * 512 + lane * 8;
+            wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
+        }
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kDecodeMaxJ; ++j) {
         const bool ok = kb0 + wave + 4 * j < kb1;
+        u32x4 w = wv[j];
+        if constexpr (A8) w = widen_e4m3x8(w[0], w[1]);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(masked_bf16x8(xv[j], (ok && mok) ? ~0u : 0u),
-                                                      masked_bf16x8(wv[j], ok ? ~0u : 0u), acc, 0, 0, 0);
+                                                      masked_bf16x8(w, ok ? ~0u : 0u), acc, 0, 0, 0);
     }
     return acc;
 }
@@ -87,9 +104,10 @@ __device__ __forceinline__ void decode_wave_sum(float* red, f32x4 acc, int wave,
     __syncthreads();
 }
 
-// rank = bf16(act(bf16(v + bias))) for column n.
+// rank = bf16(act(bf16(v * a_scale + bias))) for column n (no scale for bf16 A).
 __device__ __forceinline__ uint16_t decode_rank_epilogue(const DecodeKArgs& d, float v, int n) {
 #pragma clang fp contract(off)
+    if (d.a_scale) v = v * d.a_scale[n];
     if (d.bias) v = v + bf16_bits_to_f32(d.bias[n]);
     v = round_bf16(v);
     if (d.act == 1) v = round_bf16(silu_f32(v));
@@ -101,30 +119,20 @@ __device__ __forceinline__ float decode_tile_at(const float* red, int m, int n) 
     return red[(((m >> 2) * 16 + n) << 2) + (m & 3)];
 }
 
-template <int KSTEPS, typename BaseT, typename PriorT>
-__global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
+// Phases 1 and 2: workgroup g computes the partial of rank tile g % nct over
+// K slice g / nct and publishes it; the tile's last arrival reduces the tile,
+// publishes the bf16 rank tile and counts it in `done`.
+template <bool A8>
+__device__ __forceinline__ void decode_publish_rank(const DecodeKArgs& d, int M, int r, float* red, int& s_last) {
 #pragma clang fp contract(off)
-    const ArgmaxKArgs& a = d.am;
-    __shared__ float red[512];
-    __shared__ float s_val[4][16];
-    __shared__ int s_idx[4][16];
-    __shared__ int s_last;
-    __shared__ int s_ready;
-    __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * KSTEPS * 32];   // the rank, [16][r] bf16
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int col = lane & 15;
-    const int kg = lane >> 4;
-    const int r = KSTEPS * 32;
-
-    // ---- 1. partial of rank tile c over K slice z, published -----------------
     const int c = (int)blockIdx.x % d.nct;
     const int z = (int)blockIdx.x / d.nct;
     {
         const int kb0 = z * d.kpz;
         const int kb1 = min(d.ksa, kb0 + d.kpz);
-        const f32x4 acc = decode_rank_partial(d, a.M, c, kb0, kb1, wave, lane);
+        const f32x4 acc = decode_rank_partial<A8>(d, M, c, kb0, kb1, wave, lane);
         decode_wave_sum(red, acc, wave, lane);
     }
     float* mine = d.partial + ((int64_t)c * d.nz + z) * 256;
@@ -136,48 +144,88 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
         s_last = prev == (unsigned)(d.nz - 1);
     }
     __syncthreads();
+    if (!s_last) return;
+    float p[16];
+    const float* tp = d.partial + (int64_t)c * d.nz * 256 + threadIdx.x;
+    float v = 0.f;
+    for (int z0 = 0; z0 < d.nz; z0 += 16) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            p[i] = z0 + i < d.nz ? __hip_atomic_load(tp + (int64_t)(z0 + i) * 256, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT)
+                                 : 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v += p[i];
+    }
+    __syncthreads();
+    red[threadIdx.x] = v;
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        const int m = threadIdx.x >> 3, n = (threadIdx.x & 7) * 2;
+        const uint32_t lo = decode_rank_epilogue(d, decode_tile_at(red, m, n), c * 16 + n);
+        const uint32_t hi = decode_rank_epilogue(d, decode_tile_at(red, m, n + 1), c * 16 + n + 1);
+        __hip_atomic_store(reinterpret_cast<uint32_t*>(d.rank_buf + (int64_t)m * r + c * 16 + n), lo | (hi << 16),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);   // the rank tile has reached device coherence
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __hip_atomic_exchange(&d.tile_cnt[c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(d.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
 
-    // ---- 2. the tile's last arrival reduces it and publishes bf16 rank ----------
-    if (s_last) {
-        float p[16];
-        const float* tp = d.partial + (int64_t)c * d.nz * 256 + threadIdx.x;
-        float v = 0.f;
-        for (int z0 = 0; z0 < d.nz; z0 += 16) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-                p[i] = z0 + i < d.nz ? __hip_atomic_load(tp + (int64_t)(z0 + i) * 256, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT)
-                                     : 0.f;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v += p[i];
+// Phase 3: wait (bounded) until every rank tile is published, then bring the
+// rank ([16][r] bf16) into LDS: read once per workgroup with device-coherent
+// loads, a 64-byte share per thread -- or, if the wait timed out, computed
+// whole by this workgroup.  Ends with a barrier.
+template <int R, bool A8>
+__device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M, float* red, int& s_ready,
+                                                     uint16_t* s_rank) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (threadIdx.x == 0) {
+        int it = 0;
+        while (__hip_atomic_load(d.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)d.nct &&
+               it < d.spin_limit) {
+            __builtin_amdgcn_s_sleep(8);
+            ++it;
         }
-        __syncthreads();
-        red[threadIdx.x] = v;
-        __syncthreads();
-        if (threadIdx.x < 128) {
-            const int m = threadIdx.x >> 3, n = (threadIdx.x & 7) * 2;
-            const uint32_t lo = decode_rank_epilogue(d, decode_tile_at(red, m, n), c * 16 + n);
-            const uint32_t hi = decode_rank_epilogue(d, decode_tile_at(red, m, n + 1), c * 16 + n + 1);
-            __hip_atomic_store(reinterpret_cast<uint32_t*>(d.rank_buf + (int64_t)m * r + c * 16 + n), lo | (hi << 16),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __builtin_amdgcn_s_waitcnt(0);   // the rank tile has reached device coherence
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            __hip_atomic_exchange(&d.tile_cnt[c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_fetch_add(d.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_ready = it < d.spin_limit;
+    }
+    __syncthreads();
+    if (s_ready) {
+        constexpr int kPer = R / 64;   // 8-byte words per thread
+        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(d.rank_buf);
+        unsigned long long* dst = reinterpret_cast<unsigned long long*>(s_rank);
+        unsigned long long w[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+            w[i] = __hip_atomic_load(src + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = w[i];
+    } else {
+        for (int cc = 0; cc < d.nct; ++cc) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            for (int kb0 = 0; kb0 < d.ksa; kb0 += 4 * kDecodeMaxJ)
+                acc += decode_rank_partial<A8>(d, M, cc, kb0, min(d.ksa, kb0 + 4 * kDecodeMaxJ), wave, lane);
+            decode_wave_sum(red, acc, wave, lane);
+            {
+                const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
+                s_rank[m * R + cc * 16 + n] = decode_rank_epilogue(d, decode_tile_at(red, m, n), cc * 16 + n);
+            }
+            __syncthreads();   // red is rewritten by the next tile's sum
         }
     }
+    __syncthreads();
+}
 
-    // ---- 3. the rank, once every tile is published -----------------------------
-    const int nwaves = gridDim.x * 4;
-    int t = blockIdx.x * 4 + wave;
-    float al[4], be[4], best[4];
-    int bidx[4];
-    bool use_prior[4];
-    const BaseT* brow[4];
+// Per-lane argmax state of rows 4*(lane/16) + q (M <= 16: one row group).
+template <typename BaseT, typename PriorT>
+__device__ __forceinline__ void decode_rows(const ArgmaxKArgs& a, int kg, float (&al)[4], float (&be)[4],
+                                            bool (&use_prior)[4], const BaseT* (&brow)[4], float (&best)[4],
+                                            int (&bidx)[4]) {
     const BaseT* base = static_cast<const BaseT*>(a.base);
-    const PriorT* prior = static_cast<const PriorT*>(a.prior);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         const int m = 4 * kg + q;
@@ -189,6 +237,35 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
         best[q] = -__builtin_inff();
         bidx[q] = INT_MAX;
     }
+}
+
+template <int KSTEPS, typename BaseT, typename PriorT>
+__global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
+#pragma clang fp contract(off)
+    const ArgmaxKArgs& a = d.am;
+    constexpr int r = KSTEPS * 32;
+    __shared__ float red[512];
+    __shared__ float s_val[4][16];
+    __shared__ int s_idx[4][16];
+    __shared__ int s_last;
+    __shared__ int s_ready;
+    __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int kg = lane >> 4;
+
+    decode_publish_rank<false>(d, a.M, r, red, s_last);
+
+    const int nwaves = gridDim.x * 4;
+    int t = blockIdx.x * 4 + wave;
+    float al[4], be[4], best[4];
+    int bidx[4];
+    bool use_prior[4];
+    const BaseT* brow[4];
+    const PriorT* prior = static_cast<const PriorT*>(a.prior);
+    decode_rows<BaseT, PriorT>(a, kg, al, be, use_prior, brow, best, bidx);
     // The first two tiles of the argmax stream go in flight while the rank is finished.
     const int ntiles = (a.V + 15) >> 4;
     TileRegs<KSTEPS> ta, tb;
@@ -197,46 +274,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     if (have_a) load_tile<KSTEPS, B_PACKED_EXACT>(a, t, lane, brow, prior, ta);
     if (have_b) load_tile<KSTEPS, B_PACKED_EXACT>(a, t + nwaves, lane, brow, prior, tb);
 
-    if (threadIdx.x == 0) {
-        int it = 0;
-        while (__hip_atomic_load(d.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)d.nct &&
-               it < d.spin_limit) {
-            __builtin_amdgcn_s_sleep(8);
-            ++it;
-        }
-        s_ready = it < d.spin_limit;
-    }
-    __syncthreads();
-
-    // The rank lands in LDS (s_rank, 16 rows x r bf16) either way, then every
-    // wave takes its MFMA operands from there.
-    if (s_ready) {
-        // Published by the tile reducers: read once per workgroup, a 64-byte
-        // share per thread, with device-coherent loads.
-        constexpr int kPer = r / 64;   // 8-byte words per thread
-        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(d.rank_buf);
-        unsigned long long* dst = reinterpret_cast<unsigned long long*>(s_rank);
-        unsigned long long w[kPer];
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-            w[i] = __hip_atomic_load(src + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = w[i];
-    } else {
-        // Fallback: the whole rank in this workgroup, tile by tile.
-        for (int cc = 0; cc < d.nct; ++cc) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (int kb0 = 0; kb0 < d.ksa; kb0 += 4 * kDecodeMaxJ)
-                acc += decode_rank_partial(d, a.M, cc, kb0, min(d.ksa, kb0 + 4 * kDecodeMaxJ), wave, lane);
-            decode_wave_sum(red, acc, wave, lane);
-            {
-                const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
-                s_rank[m * r + cc * 16 + n] = decode_rank_epilogue(d, decode_tile_at(red, m, n), cc * 16 + n);
-            }
-            __syncthreads();   // red is rewritten by the next tile's sum
-        }
-    }
-    __syncthreads();
+    decode_rank_into_lds<r, false>(d, a.M, red, s_ready, s_rank);
     bf16x8 ra[KSTEPS];
     {
         const bool mok = col < a.M;
@@ -287,67 +325,57 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
         consume(ta, t);
     }
 
-    // ---- 5. cross-workgroup argmax (as fused_argmax_gemv_kernel) --------------
+    // ---- 5. cross-workgroup argmax --------------------------------------------
+    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, d.done);
+}
+
+// fp8 variant: A e4m3 (K32 blocks) with per-column scales in the rank
+// projection; rank quantised per row to e4m3; B e4m3 (K128 blocks) with
+// per-row scales in the argmax.  KS8 = r / 128.
+template <int KS8, typename BaseT, typename PriorT>
+__global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
+#pragma clang fp contract(off)
+    const ArgmaxKArgs& a = d.am;
+    constexpr int r = KS8 * 128;
+    __shared__ float red[512];
+    __shared__ float s_val[4][16];
+    __shared__ int s_idx[4][16];
+    __shared__ int s_last;
+    __shared__ int s_ready;
+    __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int kg = lane >> 4;
+
+    decode_publish_rank<true>(d, a.M, r, red, s_last);
+
+    const int nwaves = gridDim.x * 4;
+    const int t = blockIdx.x * 4 + wave;
+    float al[4], be[4], best[4];
+    int bidx[4];
+    bool use_prior[4];
+    const BaseT* brow[4];
+    const PriorT* prior = static_cast<const PriorT*>(a.prior);
+    decode_rows<BaseT, PriorT>(a, kg, al, be, use_prior, brow, best, bidx);
+    const int ntiles = (a.V + 15) >> 4;
+    TileRegs8<KS8> ta, tb;
+    if (t < ntiles) load_tile8<KS8>(a, t, lane, brow, prior, ta);
+    if (t + nwaves < ntiles) load_tile8<KS8>(a, t + nwaves, lane, brow, prior, tb);
+
+    decode_rank_into_lds<r, true>(d, a.M, red, s_ready, s_rank);
+    i32x8 rq[KS8];
+    float rsc[4];
+    {
+        const bool mok = col < a.M;
+        const float own = quantize_rank_rows<KS8>(&s_rank[col * r + 32 * kg], mok, rq);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) {
-            const float ov = __shfl_xor(best[q], off, 64);
-            const int oi = __shfl_xor(bidx[q], off, 64);
-            if (argmax_better(ov, oi, best[q], bidx[q])) {
-                best[q] = ov;
-                bidx[q] = oi;
-            }
-        }
+        for (int q = 0; q < 4; ++q) rsc[q] = __shfl(own, 4 * kg + q, 64);
     }
-    if (col == 0) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            s_val[wave][4 * kg + q] = best[q];
-            s_idx[wave][4 * kg + q] = bidx[q];
-        }
-    }
-    __syncthreads();
-    unsigned long long seen = 0;
-    if (threadIdx.x < 16) {
-        const int mi = threadIdx.x;
-        float bvv = s_val[0][mi];
-        int bii = s_idx[0][mi];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) {
-            if (argmax_better(s_val[w][mi], s_idx[w][mi], bvv, bii)) {
-                bvv = s_val[w][mi];
-                bii = s_idx[w][mi];
-            }
-        }
-        if (mi < a.M && bii != INT_MAX)
-            seen = __hip_atomic_fetch_max(&a.keys[(int64_t)mi * a.key_stride], pack_argmax(bvv, (uint32_t)bii),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (seen == ~0ull) s_last = 2;   // consume the returned value: the update has been performed
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == gridDim.x - 1);
-    }
-    __syncthreads();
-    if (s_last != 1) return;
-    for (int m = threadIdx.x; m < a.M; m += blockDim.x) {
-        const unsigned long long key = __hip_atomic_exchange(&a.keys[(int64_t)m * a.key_stride], 0ull,
-                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t idx = ~(uint32_t)(key & 0xffffffffull);
-        float val = f32_from_order_key((uint32_t)(key >> 32));
-        if (key == 0ull || idx >= (uint32_t)a.V) {
-            idx = 0;
-            val = -__builtin_inff();
-        }
-        a.out_ids[(int64_t)m * a.ld_out] = (int64_t)idx;
-        if (a.out_score) a.out_score[(int64_t)m * a.ld_out] = val;
-    }
-    if (threadIdx.x == 0) {
-        __hip_atomic_exchange(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_exchange(d.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    stream_tiles8<KS8>(a, rq, rsc, t, nwaves, ntiles, lane, brow, prior, al, be, use_prior, best, bidx, ta, tb,
+                       true);
+    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, d.done);
 }
 
 // Dispatch over K steps of B (r / 32) and the prior type for one base dtype.
@@ -375,8 +403,35 @@ hipError_t launch_decode_for_base(const DecodeKArgs& ka, int ksteps, int prior_k
     }
 }
 
+// fp8: dispatch over K128 blocks of B (r / 128) and the prior type.
+template <typename BaseT>
+hipError_t launch_decode8_for_base(const DecodeKArgs& ka, int prior_kind, hipStream_t s) {
+    auto go = [&](auto ks_tag, auto prior_tag) -> hipError_t {
+        constexpr int KS8 = decltype(ks_tag)::value;
+        using PT = decltype(prior_tag);
+        hipLaunchKernelGGL((lowrank_decode8_kernel<KS8, BaseT, PT>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
+        return hipGetLastError();
+    };
+    auto by_prior = [&](auto ks_tag) -> hipError_t {
+        switch (prior_kind) {
+            case 0: return go(ks_tag, no_prior_t{});
+            case 1: return go(ks_tag, float{});
+            case 2: return go(ks_tag, bf16_t{});
+            default: return go(ks_tag, f16_t{});
+        }
+    };
+    switch (ka.am.r / 128) {
+        case 1: return by_prior(std::integral_constant<int, 1>{});
+        case 2: return by_prior(std::integral_constant<int, 2>{});
+        default: return by_prior(std::integral_constant<int, 4>{});
+    }
+}
+
 hipError_t launch_decode_f32(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
 hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
 hipError_t launch_decode_f16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
+hipError_t launch_decode8_f32(const DecodeKArgs& ka, int prior_kind, hipStream_t s);
+hipError_t launch_decode8_bf16(const DecodeKArgs& ka, int prior_kind, hipStream_t s);
+hipError_t launch_decode8_f16(const DecodeKArgs& ka, int prior_kind, hipStream_t s);
 
 }  // namespace dels

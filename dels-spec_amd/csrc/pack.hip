@@ -48,4 +48,45 @@ hipError_t launch_pack_mfma16(const uint16_t* W, int64_t ldw, int64_t rows, int6
     return hipGetLastError();
 }
 
+// e4m3 weights (bytes, row-major W [rows, cols]) into the fp8 block layouts:
+//  * K128: block (bi, bj) covers rows 16*bi.. and columns 128*bj.. as 2 KiB
+//    [half h][lane l][16 bytes], lane l holding W[16*bi + l%16][128*bj + 32*(l/16) + 16*h + e];
+//  * K32: block (bi, bj) covers columns 32*bj.. as 512 bytes [lane l][8 bytes],
+//    lane l holding W[16*bi + l%16][32*bj + 8*(l/16) + e].
+// Blocks are row-block-major; out-of-range rows/columns are zero.  One thread
+// writes one 16-byte (K128) or 8-byte (K32) piece.
+__global__ void pack_fp8_kernel(const uint8_t* __restrict__ W, int64_t ldw, int64_t rows, int64_t cols,
+                                int64_t col_blocks, int k128, int64_t pieces, uint8_t* __restrict__ P) {
+    const int per_block = k128 ? 128 : 64;   // pieces per block
+    const int width = k128 ? 16 : 8;         // bytes per piece
+    for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < pieces;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(idx % per_block);
+        const int64_t blk = idx / per_block;
+        const int64_t bj = blk % col_blocks, bi = blk / col_blocks;
+        const int lane = c & 63, half = c >> 6;
+        const int64_t row = bi * 16 + (lane & 15);
+        const int64_t c0 = k128 ? bj * 128 + 32 * (lane >> 4) + 16 * half : bj * 32 + 8 * (lane >> 4);
+        uint8_t e[16];
+        for (int k = 0; k < 16; ++k) e[k] = 0;
+        if (row < rows)
+            for (int k = 0; k < width && c0 + k < cols; ++k) e[k] = W[row * ldw + c0 + k];
+        uint8_t* dst = P + blk * (int64_t)(per_block * width) + (int64_t)(k128 ? half * 1024 + lane * 16 : lane * 8);
+        for (int k = 0; k < width; ++k) dst[k] = e[k];
+    }
+}
+
+hipError_t launch_pack_fp8(const uint8_t* W, int64_t ldw, int64_t rows, int64_t cols, int layout, uint8_t* P,
+                           hipStream_t s) {
+    const bool k128 = layout == FP8_K128;
+    const int64_t kb = k128 ? 128 : 32;
+    const int64_t col_blocks = (cols + kb - 1) / kb;
+    const int64_t pieces = ((rows + 15) / 16) * col_blocks * (k128 ? 128 : 64);
+    if (pieces == 0) return hipSuccess;
+    const int blocks = (int)std::min<int64_t>(4096, (pieces + 255) / 256);
+    hipLaunchKernelGGL(pack_fp8_kernel, dim3(blocks), dim3(256), 0, s, W, ldw, rows, cols, col_blocks, k128 ? 1 : 0,
+                       pieces, P);
+    return hipGetLastError();
+}
+
 }  // namespace dels

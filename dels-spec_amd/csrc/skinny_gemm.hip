@@ -16,6 +16,7 @@
 #include <algorithm>
 
 #include "dels_device.h"
+#include "fp8.h"
 #include "dels_internal.h"
 
 namespace dels {
@@ -26,13 +27,14 @@ constexpr int kMaxKSplit = 16;   // workgroups per output tile along K (loads un
 
 struct SkinnyKArgs {
     const uint16_t* x; int64_t ldx;     // [M, K]; NULL means an all-zero X (GRU zero state)
-    const uint16_t* w; int64_t ldw;     // [wrows, K] row-major, or MFMA-16 blocks (WP)
+    const uint16_t* w; int64_t ldw;     // [wrows, K] row-major, or blocks of 16 rows x 32 K (WMODE)
     int M, K, wrows;
     int ncols;                          // output columns (N for rank, G for GRU)
     int ksteps, ksplit;
     float* partial;                     // [ksplit][m_wg][n_wg][WM*WN*256]
     unsigned int* counters;             // [m_wg][n_wg]
     // rank epilogue
+    const float* col_scale;             // e4m3 W only: per-column scale, applied before the bias
     const uint16_t* bias; int act;
     uint16_t* out; int64_t ldout;
     // GRU epilogue
@@ -61,6 +63,7 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyKArgs& a, const floa
             const int n = c0 + j * 16 + (lane & 15);
             if (m < a.M && n < a.ncols) {
                 float v = vals[e];
+                if (a.col_scale) v = v * a.col_scale[n];
                 if (a.bias) v = v + bf16_bits_to_f32(a.bias[n]);
                 v = round_bf16(v);
                 if (a.act == 1) v = round_bf16(silu_f32(v));
@@ -101,9 +104,12 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyKArgs& a, const floa
     }
 }
 
-// WP: W is in the MFMA-16 block layout (zero-padded, so no masking and every
-// operand load is one contiguous KiB per wave).
-template <int WM, int WN, int EPI, bool WP>
+// How W is stored: row-major bf16, MFMA-16 bf16 blocks (zero-padded, so no
+// masking and every operand load is one contiguous KiB per wave), or e4m3 in
+// the same block order (512-byte blocks, widened to bf16 at use).
+enum : int { W_ROWMAJOR = 0, W_PACKED = 1, W_PACKED_E4M3 = 2 };
+
+template <int WM, int WN, int EPI, int WMODE>
 __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
     constexpr int T = WM * WN;
     __shared__ float red[2 * T * 256];
@@ -141,9 +147,12 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
             const int c = wcol<EPI>(c0, j, a.ncols);   // first W row of sub-tile j (a multiple of 16)
-            if constexpr (WP) {
+            if constexpr (WMODE == W_PACKED) {
                 wok[j] = true;
                 wp[j] = a.w + ((int64_t)(c >> 4) * a.ksteps) * 512 + lane * 8;
+            } else if constexpr (WMODE == W_PACKED_E4M3) {
+                wok[j] = true;   // byte offset, in 16-bit units: 256 per block, 4 per lane
+                wp[j] = a.w + ((int64_t)(c >> 4) * a.ksteps) * 256 + lane * 4;
             } else {
                 const int n = c + lrow;
                 wok[j] = (n - (EPI == EPI_GRU ? j * a.ncols : 0)) < a.ncols && n < a.wrows;
@@ -170,9 +179,12 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
             for (int i = 0; i < WM; ++i) xv[i] = *reinterpret_cast<const u32x4*>(xp[i] + (kok ? k : 0));
 #pragma unroll
             for (int j = 0; j < WN; ++j) {
-                if constexpr (WP)
+                if constexpr (WMODE == W_PACKED) {
                     wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[j] + (int64_t)s * 512));
-                else
+                } else if constexpr (WMODE == W_PACKED_E4M3) {
+                    const u32x2 q = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wp[j] + (int64_t)s * 256));
+                    wv[j] = u32x4{q[0], q[1], 0u, 0u};
+                } else
                     wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[j] + (kok ? k : 0)));
             }
         };
@@ -185,8 +197,10 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
             for (int i = 0; i < WM; ++i) xo[i] = masked_bf16x8(xv[i], (kok && xok[i]) ? 0xffffffffu : 0u);
 #pragma unroll
             for (int j = 0; j < WN; ++j) {
-                if constexpr (WP)
+                if constexpr (WMODE == W_PACKED)
                     wo[j] = masked_bf16x8(wv[j], sok ? 0xffffffffu : 0u);
+                else if constexpr (WMODE == W_PACKED_E4M3)
+                    wo[j] = masked_bf16x8(widen_e4m3x8(wv[j][0], wv[j][1]), sok ? 0xffffffffu : 0u);
                 else
                     wo[j] = masked_bf16x8(wv[j], (kok && wok[j]) ? 0xffffffffu : 0u);
             }
@@ -322,12 +336,16 @@ size_t skinny_data_bytes(const SkinnyPlan& p) { return align256(p.partial_bytes)
 bool skinny_supported(const SkinnyPlan& p) { return (int64_t)p.m_wg * p.n_wg <= kMaxCounters; }
 
 template <int WM, int WN, int EPI>
-static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, bool packed, hipStream_t s) {
+static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, int wmode, hipStream_t s) {
     dim3 grid(p.n_wg, p.m_wg, p.ksplit);
-    if (packed)
-        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, true>), grid, dim3(256), 0, s, ka);
+    if (wmode == W_PACKED)
+        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, W_PACKED>), grid, dim3(256), 0, s, ka);
+    else if (wmode == W_ROWMAJOR)
+        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, W_ROWMAJOR>), grid, dim3(256), 0, s, ka);
+    else if constexpr (EPI == EPI_RANK)
+        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, W_PACKED_E4M3>), grid, dim3(256), 0, s, ka);
     else
-        hipLaunchKernelGGL((skinny_gemm_kernel<WM, WN, EPI, false>), grid, dim3(256), 0, s, ka);
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
@@ -344,11 +362,13 @@ hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, si
     ka.x = a.h; ka.ldx = a.ldh;
     ka.w = a.A; ka.ldw = a.lda;
     ka.M = a.M; ka.K = a.d; ka.wrows = a.r; ka.ncols = a.r;
+    ka.col_scale = a.a_scale;
     ka.bias = a.bias; ka.act = a.act;
     ka.out = a.rank; ka.ldout = a.ldrank;
     fill_ws(ka, p, ws, data_off);
-    if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, a.a_packed, s);
-    return launch_skinny<2, 2, EPI_RANK>(ka, p, a.a_packed, s);
+    const int wmode = a.a_scale ? W_PACKED_E4M3 : (a.a_packed ? W_PACKED : W_ROWMAJOR);
+    if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, wmode, s);
+    return launch_skinny<2, 2, EPI_RANK>(ka, p, wmode, s);
 }
 
 hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s) {
@@ -364,9 +384,10 @@ hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size
     SkinnyPlan q = p;
     if (a.h_in == nullptr) q.ksplit = 1;
     fill_ws(ka, q, ws, data_off);
-    if (q.wm == 1) return launch_skinny<1, 3, EPI_GRU>(ka, q, a.w_packed, s);
-    if (q.wm == 2) return launch_skinny<2, 3, EPI_GRU>(ka, q, a.w_packed, s);
-    return launch_skinny<4, 3, EPI_GRU>(ka, q, a.w_packed, s);
+    const int wmode = a.w_packed ? W_PACKED : W_ROWMAJOR;
+    if (q.wm == 1) return launch_skinny<1, 3, EPI_GRU>(ka, q, wmode, s);
+    if (q.wm == 2) return launch_skinny<2, 3, EPI_GRU>(ka, q, wmode, s);
+    return launch_skinny<4, 3, EPI_GRU>(ka, q, wmode, s);
 }
 
 }  // namespace dels

@@ -322,6 +322,157 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: Weight, lm_head_weight: Weight,
     return out_ids, out_score
 
 
+
+# ---- fp8 variant (e4m3 weights with per-output-channel scales) -----------------
+
+E4M3_MAX = 448.0
+FP8_LAYOUTS = {"k128": _lib.LAYOUT_FP8_K128, "k32": _lib.LAYOUT_FP8_K32}
+
+
+@dataclass
+class Fp8Weight:
+    """An e4m3 [rows, cols] weight, packed, with its per-row fp32 scale.
+
+    ``layout`` "k128" is the fp8 argmax's B operand (16 x 128 blocks of 2 KiB,
+    include/dels.h DELS_LAYOUT_FP8_K128); "k32" is the rank projection's A
+    (16 x 32 blocks of 512 bytes, DELS_LAYOUT_FP8_K32).  ``W ~= q * scale[:, None]``.
+    """
+
+    data: torch.Tensor    # packed e4m3 bytes (uint8)
+    scale: torch.Tensor   # [rows] fp32
+    rows: int
+    cols: int
+    layout: str
+
+
+def quantize_e4m3_rows(W: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row absmax e4m3fn quantisation: ``(q uint8 [rows, cols], scale fp32 [rows])``.
+
+    ``scale = absmax / 448`` (1 for an all-zero row) and ``q = e4m3(W / scale)``
+    rounded to nearest even (torch's float8_e4m3fn cast); every |W / scale| is
+    at most 448, so nothing saturates.  Weight preparation, not the hot path.
+    """
+    if W.dim() != 2:
+        raise ValueError("W must be 2-D")
+    w = W.float()
+    amax = w.abs().amax(dim=1)
+    scale = torch.where(amax > 0, amax / E4M3_MAX, torch.ones_like(amax))
+    q = (w / scale[:, None]).to(torch.float8_e4m3fn).view(torch.uint8)
+    return q.contiguous(), scale.contiguous()
+
+
+def pack_operand_fp8(q: torch.Tensor, scale: torch.Tensor, layout: str) -> Fp8Weight:
+    """Pack row-major e4m3 bytes ``q`` [rows, cols] (uint8 or float8_e4m3fn) into ``layout``."""
+    if layout not in FP8_LAYOUTS:
+        raise ValueError(f"layout must be one of {sorted(FP8_LAYOUTS)}")
+    _require_cuda(q, "q")
+    _require_cuda(scale, "scale")
+    if q.dtype == torch.float8_e4m3fn:
+        q = q.view(torch.uint8)
+    if q.dtype != torch.uint8 or q.dim() != 2:
+        raise ValueError("q must be a 2-D uint8 (e4m3fn bytes) tensor")
+    if q.shape[1] > 1 and q.stride(1) != 1:
+        raise ValueError("q must have unit column stride")
+    rows, cols = q.shape
+    if scale.dtype != torch.float32 or scale.numel() != rows:
+        raise ValueError("scale must be an fp32 vector with one entry per row")
+    lib = _lib.load()
+    code = FP8_LAYOUTS[layout]
+    nbytes = max(int(lib.dels_packed_fp8_bytes(rows, cols, code)), 16)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    _lib.check(lib.dels_pack_operand_fp8(q.data_ptr(), q.stride(0), rows, cols, code, buf.data_ptr(), buf.numel(),
+                                         _stream_ptr(q.device)), "dels_pack_operand_fp8")
+    return Fp8Weight(buf, scale.contiguous(), int(rows), int(cols), layout)
+
+
+def quantize_pack_fp8(W: torch.Tensor, layout: str) -> Fp8Weight:
+    """``quantize_e4m3_rows`` then ``pack_operand_fp8``."""
+    q, scale = quantize_e4m3_rows(W)
+    return pack_operand_fp8(q, scale, layout)
+
+
+def _fp8_weight(w: Fp8Weight, name: str, layout: str, cols: int) -> Fp8Weight:
+    if not isinstance(w, Fp8Weight) or w.layout != layout:
+        raise TypeError(f"{name} must be an Fp8Weight in the {layout!r} layout (pack_operand_fp8)")
+    if w.cols != cols:
+        raise ValueError(f"{name} has {w.cols} columns, expected {cols}")
+    _require_cuda(w.data, name)
+    return w
+
+
+def fused_argmax_fp8(rank: torch.Tensor, lm_head_weight: Fp8Weight, base_logits: torch.Tensor,
+                     baseline_logits: Optional[torch.Tensor] = None, alpha: Scalars = 1.0, beta: Scalars = 0.0,
+                     *, out_ids: Optional[torch.Tensor] = None,
+                     out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``fused_argmax`` with an e4m3 LM head (``Fp8Weight``, layout "k128").
+
+    Each rank row is quantised in the kernel to e4m3 (scale absmax/448); the
+    dot is ``fp32(R_q . B_q[v]) * sR[m] * sB[v]``.  r must be 128, 256 or 512.
+    """
+    if rank.dim() == 1:
+        rank = rank.unsqueeze(0)
+    M, r = rank.shape
+    _require_bf16_matrix(rank, "rank", cols=r)
+    B = _fp8_weight(lm_head_weight, "lm_head_weight", "k128", r)
+    V = B.rows
+    base = _base_view(base_logits, M, V)
+    prior = _prior_view(baseline_logits, V)
+    dev = rank.device
+    a, a_s = _rows_param(alpha, M, dev, "alpha")
+    b, b_s = _rows_param(beta, M, dev, "beta")
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_fused_argmax_fp8_ws_bytes(M, r, V))
+    _lib.check(lib.dels_fused_argmax_fp8(
+        rank.data_ptr(), rank.stride(0), B.data.data_ptr(), B.scale.data_ptr(),
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
+        prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
+        a.data_ptr(), a_s, b.data_ptr(), b_s, M, r, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_fused_argmax_fp8")
+    return out_ids, out_score
+
+
+def lowrank_argmax_fp8(h: torch.Tensor, rank_weight: Fp8Weight, lm_head_weight: Fp8Weight,
+                       base_logits: torch.Tensor, baseline_logits: Optional[torch.Tensor] = None,
+                       alpha: Scalars = 1.0, beta: Scalars = 0.0, act: str = "identity",
+                       rank_bias: Optional[torch.Tensor] = None, *, out_ids: Optional[torch.Tensor] = None,
+                       out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``lowrank_argmax`` with e4m3 weights: A (layout "k32") and B (layout "k128").
+
+    rank = bf16(act(bf16(fp32(h . A_q^T) * sA + bias))), then ``fused_argmax_fp8``.
+    """
+    if act not in _ACTS:
+        raise ValueError(f"Unsupported DeLS rank_activation={act!r}.")
+    if h.dim() == 1:
+        h = h.unsqueeze(0)
+    M, d = h.shape
+    _require_bf16_matrix(h, "h", cols=d)
+    A = _fp8_weight(rank_weight, "rank_weight", "k32", d)
+    r = A.rows
+    B = _fp8_weight(lm_head_weight, "lm_head_weight", "k128", r)
+    V = B.rows
+    base = _base_view(base_logits, M, V)
+    prior = _prior_view(baseline_logits, V)
+    rank_bias = _bias(rank_bias, r)
+    dev = h.device
+    a, a_s = _rows_param(alpha, M, dev, "alpha")
+    b, b_s = _rows_param(beta, M, dev, "beta")
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_lowrank_argmax_fp8_ws_bytes(M, d, r, V))
+    _lib.check(lib.dels_lowrank_argmax_fp8(
+        h.data_ptr(), h.stride(0), A.data.data_ptr(), A.scale.data_ptr(),
+        rank_bias.data_ptr() if rank_bias is not None else None, _ACTS[act],
+        B.data.data_ptr(), B.scale.data_ptr(),
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
+        prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
+        a.data_ptr(), a_s, b.data_ptr(), b_s, M, d, r, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_lowrank_argmax_fp8")
+    return out_ids, out_score
+
+
 def gru_step(gi_table: torch.Tensor, tokens: torch.Tensor, h_in: Optional[torch.Tensor],
              w_hh: Weight, b_hh: Optional[torch.Tensor] = None, *,
              out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -69,6 +69,19 @@ extern "C" {
  */
 #define DELS_LAYOUT_ROWMAJOR 0
 #define DELS_LAYOUT_MFMA16 1
+/*
+ * fp8 weight layouts (OCP float8 e4m3fn bytes; no counterpart in the
+ * reference, whose weights are bf16 -- the fp8 configuration stores A and B as
+ * e4m3 with a per-output-channel fp32 scale).  Written by dels_pack_operand_fp8
+ * from row-major e4m3 bytes, zero-padded:
+ *   DELS_LAYOUT_FP8_K128: 16-row x 128-column blocks of 2 KiB, row-block-major,
+ *     each as two 1 KiB halves [half][lane][16 bytes], lane l holding row l%16,
+ *     columns 32*(l/16) + 16*half .. +15 of the block (the low-rank LM head B);
+ *   DELS_LAYOUT_FP8_K32: the MFMA16 block order with one byte per element,
+ *     16-row x 32-column blocks of 512 bytes (the rank projection weight A).
+ */
+#define DELS_LAYOUT_FP8_K128 2
+#define DELS_LAYOUT_FP8_K32 3
 
 int dels_abi_version(void);
 const char* dels_strerror(int status);
@@ -148,6 +161,48 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
  * computation) and returns the previous one.  Not thread-safe.
  */
 int dels_debug_set_decode_spin_limit(int limit);
+
+/*
+ * fp8 variant (no counterpart in the reference: the fp8 configuration of the
+ * same draft step, with e4m3 weights and per-output-channel fp32 scales).
+ *
+ * dels_pack_operand_fp8: row-major e4m3 bytes W [rows, cols] (ldw bytes) into
+ * `layout` (DELS_LAYOUT_FP8_K128 or _K32); `packed` holds
+ * dels_packed_fp8_bytes(rows, cols, layout) bytes, 16-byte aligned.
+ *
+ * dels_fused_argmax_fp8: the fused argmax of dels_fused_argmax with
+ *   B_q [V, r] e4m3 (DELS_LAYOUT_FP8_K128) and b_scale [V] fp32; each rank row
+ *   is quantised in the kernel to e4m3 with scale sR = absmax / 448 and
+ *     dot[m, v] = fp32(R_q[m] . B_q[v]) * sR[m] * b_scale[v]
+ *   (rounded after each product), then the same combine and argmax.
+ *   r must be 128, 256 or 512.
+ *
+ * dels_lowrank_argmax_fp8: rank = bf16(act(bf16(fp32(h . A_q^T) * a_scale +
+ *   bias))) with A_q [r, d] e4m3 (DELS_LAYOUT_FP8_K32) and a_scale [r] fp32,
+ *   then dels_fused_argmax_fp8.  One launch for M <= 16 (d a multiple of 32).
+ */
+size_t dels_packed_fp8_bytes(int64_t rows, int64_t cols, int layout);
+int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t cols, int layout,
+                          void* packed, size_t packed_bytes, void* stream);
+size_t dels_fused_argmax_fp8_ws_bytes(int64_t M, int64_t r, int64_t V);
+int dels_fused_argmax_fp8(const void* rank, int64_t ldrank, const void* Bq, const float* b_scale,
+                          const void* base, int64_t ldbase, int base_dtype,
+                          const void* prior, int prior_dtype,
+                          const float* alpha, int64_t alpha_stride,
+                          const float* beta, int64_t beta_stride,
+                          int64_t M, int64_t r, int64_t V,
+                          int64_t* out_ids, float* out_score, int64_t ld_out,
+                          void* ws, size_t ws_bytes, void* stream);
+size_t dels_lowrank_argmax_fp8_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V);
+int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const float* a_scale,
+                            const void* bias, int act, const void* Bq, const float* b_scale,
+                            const void* base, int64_t ldbase, int base_dtype,
+                            const void* prior, int prior_dtype,
+                            const float* alpha, int64_t alpha_stride,
+                            const float* beta, int64_t beta_stride,
+                            int64_t M, int64_t d, int64_t r, int64_t V,
+                            int64_t* out_ids, float* out_score, int64_t ld_out,
+                            void* ws, size_t ws_bytes, void* stream);
 
 /*
  * One GRU local-head step h_out = GRUCell(gi_table[tokens], h_in).

@@ -49,6 +49,8 @@ __all__ = [
     "rollout",
     "unigram_log_prior",
     "rank_proj_fp8",
+    "fused_argmax_fp8",
+    "score_at_fp8",
     "lowrank_argmax_fp8",
     "check_parity",
 ]
@@ -400,14 +402,14 @@ def rank_proj_fp8(h, A_q, A_scale, bias=None, act: str = "identity") -> np.ndarr
     return rank
 
 
-def lowrank_argmax_fp8(h, A_q, A_scale, bias, act, B_q, B_scale, base, prior, alpha, beta,
-                       *, chunk: int = 8192):
-    """fp8 variant: rank quantised per row to e4m3, then an fp8 x fp8 contraction.
+def fused_argmax_fp8(rank, B_q, B_scale, base, prior, alpha, beta, *, chunk: int = 8192):
+    """fp8 argmax on a given rank: each rank row quantised to e4m3, then an fp8 x fp8 contraction.
 
-    ``dot[m, v] = sR[m] * sB[v] * sum_k R_q[m, k] * B_q[v, k]`` followed by the
-    same fp32 combine and argmax as the bf16 path.
+    ``R_q, sR = quantize_rows_e4m3(rank)``;
+    ``dot[m, v] = fp32(fp32(R_q[m] . B_q[v]) * sR[m]) * sB[v]`` followed by the
+    same fp32 combine and argmax as the bf16 path (``fused_argmax``).  Returns
+    ``(ids, best, second)``.
     """
-    rank = rank_proj_fp8(h, A_q, A_scale, bias, act)
     R_q, R_scale = quantize_rows_e4m3(rank)
     base = np.asarray(base, _F32)
     M, V = base.shape
@@ -433,7 +435,37 @@ def lowrank_argmax_fp8(h, A_q, A_scale, bias, act, B_q, B_scale, base, prior, al
         second = np.where(take, np.maximum(best, c2), np.maximum(second, c1)).astype(_F32)
         idx = np.where(take, i1 + v0, idx)
         best = np.where(take, c1, best).astype(_F32)
-    return rank, idx.astype(np.int64), best, second
+    return idx.astype(np.int64), best, second
+
+
+def score_at_fp8(rank, B_q, B_scale, base, prior, alpha, beta, ids) -> np.ndarray:
+    """The fp8 path's combined score of row m at vocabulary index ``ids[m]``."""
+    R_q, R_scale = quantize_rows_e4m3(rank)
+    base = np.asarray(base, _F32)
+    M = base.shape[0]
+    ids = np.asarray(ids, np.int64).reshape(-1)
+    alpha = _rowvec(alpha, M)
+    beta = _rowvec(beta, M)
+    Bv = np.asarray(B_q, _F32)[ids]
+    raw = np.einsum("mk,mk->m", R_q.astype(_F64), Bv.astype(_F64)).astype(_F32)
+    dot = ((raw * R_scale).astype(_F32) * np.asarray(B_scale, _F32)[ids]).astype(_F32)
+    s = (dot * alpha).astype(_F32)
+    s = (s + base[np.arange(M), ids]).astype(_F32)
+    if prior is not None:
+        p = np.asarray(prior, _F32).reshape(-1)[ids]
+        s = np.where(beta != 0, (s - (beta * p).astype(_F32)).astype(_F32), s)
+    return s.astype(_F32)
+
+
+def lowrank_argmax_fp8(h, A_q, A_scale, bias, act, B_q, B_scale, base, prior, alpha, beta,
+                       *, chunk: int = 8192):
+    """fp8 variant of a whole step: ``rank_proj_fp8`` then ``fused_argmax_fp8``.
+
+    Returns ``(rank, ids, best, second)``.
+    """
+    rank = rank_proj_fp8(h, A_q, A_scale, bias, act)
+    idx, best, second = fused_argmax_fp8(rank, B_q, B_scale, base, prior, alpha, beta, chunk=chunk)
+    return rank, idx, best, second
 
 
 # --------------------------------------------------------------------------
