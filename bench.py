@@ -48,6 +48,8 @@ def parse_args():
     ap.add_argument("--workload", default="qwen3_8b_m16", choices=["qwen3_8b_m16", "qwen3_4b_m16", "qwen3_8b_m512"])
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
     ap.add_argument("--also-m512", action=argparse.BooleanOptionalAction, default=True)
+    ap.add_argument("--also-fp8", action=argparse.BooleanOptionalAction, default=True,
+                    help="add the fp8 variant (e4m3 A and B with per-channel scales) of the workload's shape")
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -278,6 +280,53 @@ def bench_workload(pkg, name, args, dev, torch):
     return rec, x0
 
 
+
+def bench_fp8(pkg, name, args, dev, torch):
+    """The fp8 variant of a workload: e4m3 A and B (per-channel fp32 scales), same h/base/prior/alpha/beta.
+
+    Algorithmic bytes per step: r*V (B) + r*d (A) + 2*M*d (h) + s_base*M*V +
+    s_prior*V + 4*(V + r) (scales) + 12*M (outputs)."""
+    x0 = pkg.synth.config_inputs(name)
+    nsets = max(4, -(-512 * 2**20 // (set_bytes(x0) // 2)))
+    sets = make_sets(pkg, x0, nsets, dev)
+    s = x0.shape
+    M, d, r, V = s["M"], s["d"], s["r"], s["V"]
+    weights = [(pkg.quantize_pack_fp8(x.A, "k32"), pkg.quantize_pack_fp8(x.B, "k128")) for x in sets]
+    for x in sets:   # the bf16 weights are not read by the fp8 step
+        x.A = x.B = None
+    torch.cuda.empty_cache()
+    outs = [(torch.empty(M, dtype=torch.int64, device=dev), torch.empty(M, dtype=torch.float32, device=dev))
+            for _ in range(nsets)]
+
+    def step(i):
+        x = sets[i % nsets]
+        o = outs[i % nsets]
+        A8, B8 = weights[i % nsets]
+        pkg.lowrank_argmax_fp8(x.h, A8, B8, x.base, x.prior, x.alpha, x.beta, act=x.act, out_ids=o[0],
+                               out_score=o[1])
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize(dev)
+    eager = [(o[0].clone(), o[1].clone()) for o in outs]
+    steps = min(args.steps, 200)
+    ms_total, g = time_graph(torch, step, steps, dev)
+    del g
+    for i in range(nsets):
+        if not (torch.equal(outs[i][0], eager[i][0]) and torch.equal(outs[i][1], eager[i][1])):
+            raise RuntimeError(f"fp8 graph replay differs from eager results on set {i}")
+    us = ms_total * 1e3 / steps
+    sb = x0.base.element_size()
+    sp = x0.prior.element_size()
+    nbytes = r * V + r * d + 2 * M * d + sb * M * V + sp * V + 4 * (V + r) + 12 * M
+    return {"workload": name, "M": M, "d": d, "r": r, "V": V, "weights": "e4m3 (A K32, B K128 blocks)",
+            "kernel": "lowrank_decode8_kernel" if M <= 16 else
+            "skinny_gemm_kernel (e4m3 A) + fused_argmax_gemv8_kernel",
+            "rows_per_s": M / (us * 1e-6), "us_per_step": us, "algorithmic_bytes": nbytes,
+            "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "sets": nsets}
+
+
 def cpu_baseline(name, x0, seconds):
     """The oracle on full calls of the workload, repeated for about `seconds`."""
     import numpy as np
@@ -403,6 +452,11 @@ def main():
             out["m512"]["argmax_algorithmic_bytes"] = r512["argmax_bytes"]
         except Exception as e:  # informative record only
             out["m512"] = {"error": repr(e)}
+    if args.also_fp8 and args.workload != "qwen3_8b_m512":
+        try:
+            out["fp8"] = bench_fp8(pkg, args.workload, args, dev, torch)
+        except Exception as e:  # informative record only
+            out["fp8"] = {"error": repr(e)}
     if args.cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.workload, x0, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -114,6 +114,27 @@ __device__ __forceinline__ void dma4(const void* base, uint32_t off, void* lds) 
                  : : "v"(off), "s"(sgpr_ptr(base)), "{m0}"(lds_addr(lds)) : "memory");
 }
 
+// Element of an LDS array of base/prior values, widened to fp32.
+__device__ __forceinline__ float lds_f32(const float* p) { return *p; }
+__device__ __forceinline__ float lds_f32(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+__device__ __forceinline__ float lds_f32(const f16_t* p) {
+    const uint16_t b = p->bits;
+    _Float16 h;
+    __builtin_memcpy(&h, &b, 2);
+    return (float)h;
+}
+
+// Wait until at most `pending` groups of PER direct-to-LDS loads are in flight
+// (pending is wave-uniform, 0 .. 3; s_waitcnt takes an immediate).
+template <int PER>
+__device__ __forceinline__ void wait_dma_groups(int pending) {
+    static_assert(3 * PER <= 63, "vmcnt holds at most 63");
+    if (pending <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (pending == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(PER) : "memory");
+    else if (pending == 2) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * PER) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * PER) : "memory");
+}
+
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }

@@ -73,54 +73,75 @@ __device__ __forceinline__ f32x4 mfma_e4m3_16x16x128(const i32x8& a, const i32x8
     return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
 }
 
-// The rank rows as the e4m3 A operand of KS8 K128 blocks.  `rowp` points at
-// element 32*(lane/16) of the lane's rank row (bf16, global or LDS); lanes of
-// rows outside the batch pass mok = false and get zeros.  Each row is
-// quantised on its own: scale = absmax / 448 (1 for an all-zero row),
-// q = e4m3(v / scale).  Returns the scale of the lane's row (l%16).
-template <int KS8>
-__device__ __forceinline__ float quantize_rank_rows(const uint16_t* rowp, bool mok, i32x8 (&rq)[KS8]) {
+// Workgroup-cooperative e4m3 quantisation of the 16 rank rows m0 .. m0+15 (r =
+// R bf16 values each, row stride ld) into LDS: thread x handles row x/16 and
+// the R/16 consecutive values from (x%16)*R/16.  Each row: amax = absmax,
+// inv = 448 / amax, q = e4m3(v * inv), scale = amax / 448 (1 and zeros for an
+// all-zero row; rows from m_valid on are zeros).  s_rq holds [16][R + 16]
+// bytes (the pad spreads the operand reads over the banks), s_rsc [16].
+// Ends with a barrier that waits for LDS traffic only, so loads in flight
+// (the first streamed tiles) stay in flight.
+template <int R>
+__device__ __forceinline__ void quantize_rank_coop(const uint16_t* rows, int64_t ld, int m_valid, uint8_t* s_rq,
+                                                   float* s_rsc) {
 #pragma clang fp contract(off)
-    u32x4 raw[KS8][4];
+    constexpr int PER = R / 16;   // values per thread: 8, 16 or 32
+    static_assert(PER % 8 == 0, "whole 16-byte pieces");
+    const int m = threadIdx.x >> 4, seg = threadIdx.x & 15;
+    const bool ok = m < m_valid;
+    const uint16_t* src = rows + (int64_t)(ok ? m : 0) * ld + seg * PER;
+    u32x4 raw[PER / 8];
 #pragma unroll
-    for (int j = 0; j < KS8; ++j)
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(rowp + 128 * j + 8 * p);
-            raw[j][p] = mok ? v : u32x4{0u, 0u, 0u, 0u};
-        }
+    for (int i = 0; i < PER / 8; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(src + 8 * i);
+        raw[i] = ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
     float amax = 0.f;
 #pragma unroll
-    for (int j = 0; j < KS8; ++j)
+    for (int i = 0; i < PER / 8; ++i)
 #pragma unroll
-        for (int p = 0; p < 4; ++p)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[j][p][e] << 16)));
-                amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[j][p][e] & 0xffff0000u)));
-            }
-    // the row's four lane groups (lanes l, l^16, l^32, l^48)
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16, 64));
-    amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32, 64));
-    const float scale = amax > 0.f ? amax / kE4M3Max : 1.f;
-#pragma unroll
-    for (int j = 0; j < KS8; ++j)
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-            uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                const float x0 = __uint_as_float(raw[j][p][e] << 16);
-                const float x1 = __uint_as_float(raw[j][p][e] & 0xffff0000u);
-                w0 |= (f32_to_e4m3(x0 / scale) | (f32_to_e4m3(x1 / scale) << 8)) << (16 * e);
-                const float y0 = __uint_as_float(raw[j][p][e + 2] << 16);
-                const float y1 = __uint_as_float(raw[j][p][e + 2] & 0xffff0000u);
-                w1 |= (f32_to_e4m3(y0 / scale) | (f32_to_e4m3(y1 / scale) << 8)) << (16 * e);
-            }
-            rq[j][2 * p] = (int)w0;
-            rq[j][2 * p + 1] = (int)w1;
+        for (int e = 0; e < 4; ++e) {
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[i][e] << 16)));
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(raw[i][e] & 0xffff0000u)));
         }
-    return scale;
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+#pragma unroll
+    for (int i = 0; i < PER / 8; ++i) {
+        uint32_t w[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t x0 = raw[i][2 * h], x1 = raw[i][2 * h + 1];
+            w[h] = f32_to_e4m3(__uint_as_float(x0 << 16) * inv) |
+                   (f32_to_e4m3(__uint_as_float(x0 & 0xffff0000u) * inv) << 8) |
+                   (f32_to_e4m3(__uint_as_float(x1 << 16) * inv) << 16) |
+                   (f32_to_e4m3(__uint_as_float(x1 & 0xffff0000u) * inv) << 24);
+        }
+        *reinterpret_cast<u32x2*>(s_rq + m * (R + 16) + seg * PER + 8 * i) = u32x2{w[0], w[1]};
+    }
+    if (seg == 0) s_rsc[m] = amax > 0.f ? amax / kE4M3Max : 1.f;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// The lane's e4m3 A operand (row lane%16, bytes 32*(lane/16) .. of each K128
+// block) and the scales of its output rows 4*(lane/16) + q, from LDS.
+template <int KS8>
+__device__ __forceinline__ void load_rank_operand(const uint8_t* s_rq, const float* s_rsc, int lane,
+                                                  i32x8 (&rq)[KS8], float (&rsc)[4]) {
+    constexpr int R = KS8 * 128;
+    const int col = lane & 15, kg = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < KS8; ++j) {
+        const uint8_t* p = s_rq + col * (R + 16) + 128 * j + 32 * kg;
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(p);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(p + 16);
+        rq[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rsc[q] = s_rsc[4 * kg + q];
 }
 
 }  // namespace dels

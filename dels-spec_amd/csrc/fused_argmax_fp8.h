@@ -64,7 +64,7 @@ __device__ __forceinline__ void consume_tile8(const ArgmaxKArgs& a, const i32x8 
         float sc = dot * al[q];
         sc = sc + tr.base[q];
         if (use_prior[q]) sc = sc - be[q] * tr.prior;
-        const bool take = v < a.V && argmax_better(sc, v, best[q], bidx[q]);
+        const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
         best[q] = take ? sc : best[q];
         bidx[q] = take ? v : bidx[q];
     }
@@ -96,6 +96,7 @@ __device__ __forceinline__ void stream_tiles8(const ArgmaxKArgs& a, const i32x8 
             break;
         }
         load_tile8<KS8>(a, t + 2 * nwaves, lane, brow, prior, ta);
+        __builtin_amdgcn_sched_barrier(0);   // the refill is issued before the other tile is touched
         t += nwaves;
         consume_tile8<KS8>(a, rq, rsc, tb, t, col, al, be, use_prior, best, bidx);
         if (t + 2 * nwaves >= ntiles) {
@@ -103,33 +104,164 @@ __device__ __forceinline__ void stream_tiles8(const ArgmaxKArgs& a, const i32x8 
             break;
         }
         load_tile8<KS8>(a, t + 2 * nwaves, lane, brow, prior, tb);
+        __builtin_amdgcn_sched_barrier(0);
         t += nwaves;
     }
 }
 
+// ---- LDS-ring stream -------------------------------------------------------
+//
+// Register-held prefetch tiles cross the loop back-edge, where the compiler may
+// move them between register classes and wait for every load in flight (the
+// stream then degrades to one tile at a time).  The ring variant lands every
+// streamed operand -- the B blocks, the tile's base logits, prior and row
+// scales -- in a per-wave LDS ring with direct-to-LDS loads the compiler does
+// not track, and waits with explicit vmcnt counts: R tiles in flight, exactly.
+// Needs 16-byte-aligned rows (V a multiple of 16, base rows and the prior and
+// scale vectors 16-byte aligned); see ring8_eligible on the host.
+
+template <int KS8>
+struct Ring8 {
+    static constexpr int kB = KS8 * kFp8K128Block;   // B blocks of the tile
+    static constexpr int kBase = kB;                  // [16 rows][16 columns] of base (fp32 or 16-bit)
+    static constexpr int kPrior = kBase + 1024;       // 16 prior values
+    static constexpr int kScale = kPrior + 64;        // 16 row scales of B
+    static constexpr int kSlot = kScale + 64;         // bytes per tile slot
+    static_assert(kSlot % 128 == 0, "slot alignment");
+};
+
+template <typename T> struct elem_bytes { static constexpr int value = 2; };
+template <> struct elem_bytes<float> { static constexpr int value = 4; };
+
+template <typename PriorT>
+constexpr int ring8_dmas_per_tile(int ks8) { return 2 * ks8 + 2 + (is_no_prior<PriorT>::value ? 0 : 1); }
+
+// Put tile t's operands in flight into `slot`.  `row_off` is the lane's byte
+// offset of its base row (fp32: row lane/4; 16-bit: row lane/2 for lanes < 32;
+// rows beyond the batch clamped to row 0).
 template <int KS8, typename BaseT, typename PriorT>
+__device__ __forceinline__ void issue_tile8_lds(const ArgmaxKArgs& a, int t, int lane, uint32_t row_off, char* slot) {
+    using RS = Ring8<KS8>;
+    const uint8_t* bsrc = reinterpret_cast<const uint8_t*>(a.B) + (int64_t)t * KS8 * kFp8K128Block;
+#pragma unroll
+    for (int j = 0; j < KS8; ++j) {
+        dma16(bsrc, (uint32_t)(j * kFp8K128Block + lane * 16), slot + j * kFp8K128Block);
+        dma16(bsrc, (uint32_t)(j * kFp8K128Block + 1024 + lane * 16), slot + j * kFp8K128Block + 1024);
+    }
+    constexpr int EB = elem_bytes<BaseT>::value;
+    const char* base_t = static_cast<const char*>(a.base) + (int64_t)t * 16 * EB;
+    if constexpr (EB == 4) {
+        dma16(base_t, row_off + (uint32_t)(lane & 3) * 16, slot + RS::kBase);
+    } else {
+        if (lane < 32) dma16(base_t, row_off + (uint32_t)(lane & 1) * 16, slot + RS::kBase);
+    }
+    if constexpr (!is_no_prior<PriorT>::value) {
+        constexpr int PB = elem_bytes<PriorT>::value;
+        if (lane < PB) dma16(static_cast<const char*>(a.prior) + (int64_t)t * 16 * PB, (uint32_t)lane * 16,
+                             slot + RS::kPrior);
+    }
+    if (lane < 4) dma16(a.b_scale + (int64_t)t * 16, (uint32_t)lane * 16, slot + RS::kScale);
+}
+
+// Contract tile `tile` from its LDS slot and fold it into the running argmax.
+template <int KS8, typename BaseT, typename PriorT>
+__device__ __forceinline__ void consume_tile8_lds(const ArgmaxKArgs& a, const i32x8 (&rq)[KS8], const float (&rsc)[4],
+                                                  const char* slot, int tile, int lane, const float (&al)[4],
+                                                  const float (&be)[4], const bool (&use_prior)[4],
+                                                  float (&best)[4], int (&bidx)[4]) {
+#pragma clang fp contract(off)
+    using RS = Ring8<KS8>;
+    const int col = lane & 15, kg = lane >> 4;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KS8; ++j) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(slot + j * kFp8K128Block + lane * 16);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(slot + j * kFp8K128Block + 1024 + lane * 16);
+        const i32x8 b = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2],
+                         (int)hi[3]};
+        acc = mfma_e4m3_16x16x128(rq[j], b, acc);
+    }
+    const BaseT* bl = reinterpret_cast<const BaseT*>(slot + RS::kBase);
+    float pr = 0.f;
+    if constexpr (!is_no_prior<PriorT>::value) pr = lds_f32(reinterpret_cast<const PriorT*>(slot + RS::kPrior) + col);
+    const float bsc = reinterpret_cast<const float*>(slot + RS::kScale)[col];
+    const int v = tile * 16 + col;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float dot = acc[q] * rsc[q];
+        dot = dot * bsc;
+        float sc = dot * al[q];
+        sc = sc + lds_f32(bl + (4 * kg + q) * 16 + col);
+        if (use_prior[q]) sc = sc - be[q] * pr;
+        const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);
+        best[q] = take ? sc : best[q];
+        bidx[q] = take ? v : bidx[q];
+    }
+}
+
+// Byte offset of the lane's base row for issue_tile8_lds.
+template <typename BaseT>
+__device__ __forceinline__ uint32_t ring8_row_off(const ArgmaxKArgs& a, int m0, int lane) {
+    constexpr int EB = elem_bytes<BaseT>::value;
+    const int row = m0 + (EB == 4 ? (lane >> 2) : ((lane >> 1) & 15));
+    return (uint32_t)((int64_t)(row < a.M ? row : 0) * a.ldbase * EB);
+}
+
+// The wave's tiles t0, t0 + stride, ... through an R-slot LDS ring.  The first
+// `issued` (<= R) tiles may already be in flight (issued by the caller in
+// order into slots 0, 1, ...).
+template <int KS8, int R, typename BaseT, typename PriorT>
+__device__ __forceinline__ void stream_tiles8_lds(const ArgmaxKArgs& a, const i32x8 (&rq)[KS8], const float (&rsc)[4],
+                                                  int t0, int stride, int ntiles, int lane, uint32_t row_off,
+                                                  char* ring, int issued, const float (&al)[4],
+                                                  const float (&be)[4], const bool (&use_prior)[4],
+                                                  float (&best)[4], int (&bidx)[4]) {
+    using RS = Ring8<KS8>;
+    constexpr int PER = ring8_dmas_per_tile<PriorT>(KS8);
+    static_assert(R <= 4, "wait_dma_groups covers up to 3 pending groups");
+    const int nk = t0 < ntiles ? (ntiles - 1 - t0) / stride + 1 : 0;
+    const int first = nk < R ? nk : R;
+    for (int i = issued; i < first; ++i) issue_tile8_lds<KS8, BaseT, PriorT>(a, t0 + i * stride, lane, row_off,
+                                                                             ring + i * RS::kSlot);
+    int in_flight = first;   // tiles issued so far
+    for (int k = 0; k < nk; ++k) {
+        wait_dma_groups<PER>(in_flight - k - 1);
+        char* slot = ring + (k % R) * RS::kSlot;
+        consume_tile8_lds<KS8, BaseT, PriorT>(a, rq, rsc, slot, t0 + k * stride, lane, al, be, use_prior, best,
+                                              bidx);
+        if (k + R < nk) {
+            // every LDS read of the slot has been consumed above; refill it
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue_tile8_lds<KS8, BaseT, PriorT>(a, t0 + (k + R) * stride, lane, row_off, slot);
+            ++in_flight;
+        }
+    }
+}
+
+constexpr int kGemv8Ring = 4;   // LDS ring slots per wave (GEMV)
+
+template <int KS8, typename BaseT, typename PriorT, bool RING>
 __global__ __launch_bounds__(256) void fused_argmax_gemv8_kernel(ArgmaxKArgs a) {
 #pragma clang fp contract(off)
     __shared__ float s_val[4][16];
     __shared__ int s_idx[4][16];
     __shared__ int s_last;
+    __shared__ __attribute__((aligned(1024))) char s_ring[RING ? 4 : 1][RING ? kGemv8Ring : 1]
+                                                        [RING ? Ring8<KS8>::kSlot : 16];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int col = lane & 15;
     const int kg = lane >> 4;
     const int m0 = blockIdx.y * 16;
 
-    // e4m3 rank operand of the 16 rows (row m0 + col, K bytes 32*kg .. of each block).
+    // e4m3 rank operand of the 16 rows, quantised once per workgroup.
+    __shared__ __attribute__((aligned(16))) uint8_t s_rq[16 * (KS8 * 128 + 16)];
+    __shared__ float s_rsc[16];
+    quantize_rank_coop<KS8 * 128>(a.rank + (int64_t)m0 * a.ldrank, a.ldrank, a.M - m0, s_rq, s_rsc);
     i32x8 rq[KS8];
     float rsc[4];
-    {
-        const int mrow = m0 + col;
-        const bool mok = mrow < a.M;
-        const float own = quantize_rank_rows<KS8>(a.rank + (int64_t)(mok ? mrow : 0) * a.ldrank + 32 * kg, mok, rq);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rsc[q] = __shfl(own, 4 * kg + q, 64);   // lane 4*kg+q owns row 4*kg+q
-    }
+    load_rank_operand<KS8>(s_rq, s_rsc, lane, rq, rsc);
 
     float al[4], be[4], best[4];
     int bidx[4];
@@ -150,10 +282,24 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv8_kernel(ArgmaxKArgs a) 
     }
     const int ntiles = (a.V + 15) >> 4;
     const int nwaves = gridDim.x * 4;
-    TileRegs8<KS8> ta, tb;
-    stream_tiles8<KS8>(a, rq, rsc, blockIdx.x * 4 + wave, nwaves, ntiles, lane, brow, prior, al, be, use_prior,
-                       best, bidx, ta, tb, false);
+    if constexpr (RING) {
+        stream_tiles8_lds<KS8, kGemv8Ring, BaseT, PriorT>(a, rq, rsc, blockIdx.x * 4 + wave, nwaves, ntiles, lane,
+                                                          ring8_row_off<BaseT>(a, m0, lane), &s_ring[wave][0][0], 0,
+                                                          al, be, use_prior, best, bidx);
+    } else {
+        TileRegs8<KS8> ta, tb;
+        stream_tiles8<KS8>(a, rq, rsc, blockIdx.x * 4 + wave, nwaves, ntiles, lane, brow, prior, al, be, use_prior,
+                           best, bidx, ta, tb, false);
+    }
     argmax_wg_finish(a, best, bidx, m0, s_val, s_idx, s_last, nullptr);
+}
+
+// The LDS ring needs every streamed row 16-byte aligned (see the ring notes above).
+inline bool ring8_eligible(const ArgmaxKArgs& ka, int base_bytes, int prior_bytes) {
+    auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if (ka.V % 16 != 0 || !al16(ka.base) || (ka.ldbase * base_bytes) % 16 != 0 || !al16(ka.b_scale)) return false;
+    if ((int64_t)ka.M * ka.ldbase * base_bytes >= ((int64_t)1 << 31)) return false;
+    return ka.prior == nullptr || (al16(ka.prior) && prior_bytes > 0);
 }
 
 template <int KS8, typename BaseT, typename PriorT>
@@ -162,7 +308,13 @@ hipError_t launch_gemv8_inst(const ArgmaxKArgs& ka, hipStream_t s) {
     const int groups = (ka.M + 15) / 16;
     const int cus = device_cu_count();
     const int gx = std::max(1, std::min((ntiles + 3) / 4, (cus + groups - 1) / groups));
-    hipLaunchKernelGGL((fused_argmax_gemv8_kernel<KS8, BaseT, PriorT>), dim3(gx, groups, 1), dim3(256), 0, s, ka);
+    const int pb = is_no_prior<PriorT>::value ? 0 : elem_bytes<PriorT>::value;
+    if (ring8_eligible(ka, elem_bytes<BaseT>::value, pb))
+        hipLaunchKernelGGL((fused_argmax_gemv8_kernel<KS8, BaseT, PriorT, true>), dim3(gx, groups, 1), dim3(256), 0,
+                           s, ka);
+    else
+        hipLaunchKernelGGL((fused_argmax_gemv8_kernel<KS8, BaseT, PriorT, false>), dim3(gx, groups, 1), dim3(256), 0,
+                           s, ka);
     return hipGetLastError();
 }
 

@@ -111,7 +111,7 @@ __device__ __forceinline__ void argmax_wg_finish(const ArgmaxKArgs& a, float (&b
                                                  float (&s_val)[4][16], int (&s_idx)[4][16], int& s_last,
                                                  unsigned int* also_clear) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int col = lane & 15;
     const int kg = lane >> 4;
     // Reduce over the 16 vocabulary columns of each row (lanes sharing kg).
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
     __shared__ int s_last;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int col = lane & 15;
     const int kg = lane >> 4;
     const int m0 = blockIdx.y * 16;
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
             float sc = acc[q] * al[q];
             sc = sc + tr.base[q];
             if (use_prior[q]) sc = sc - be[q] * tr.prior;
-            const bool take = v < a.V && argmax_better(sc, v, best[q], bidx[q]);
+            const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];
         }

@@ -126,7 +126,7 @@ template <bool A8>
 __device__ __forceinline__ void decode_publish_rank(const DecodeKArgs& d, int M, int r, float* red, int& s_last) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int c = (int)blockIdx.x % d.nct;
     const int z = (int)blockIdx.x / d.nct;
     {
@@ -183,7 +183,7 @@ template <int R, bool A8>
 __device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M, float* red, int& s_ready,
                                                      uint16_t* s_rank) {
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     if (threadIdx.x == 0) {
         int it = 0;
         while (__hip_atomic_load(d.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)d.nct &&
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int col = lane & 15;
     const int kg = lane >> 4;
 
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
             float sc = acc[q] * al[q];
             sc = sc + tr.base[q];
             if (use_prior[q]) sc = sc - be[q] * tr.prior;
-            const bool take = v < a.V && argmax_better(sc, v, best[q], bidx[q]);
+            const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];
         }
@@ -332,7 +332,9 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
 // fp8 variant: A e4m3 (K32 blocks) with per-column scales in the rank
 // projection; rank quantised per row to e4m3; B e4m3 (K128 blocks) with
 // per-row scales in the argmax.  KS8 = r / 128.
-template <int KS8, typename BaseT, typename PriorT>
+constexpr int kDecode8Ring = 3;   // LDS ring slots per wave (the rank takes 16 KB of LDS too)
+
+template <int KS8, typename BaseT, typename PriorT, bool RING>
 __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
 #pragma clang fp contract(off)
     const ArgmaxKArgs& a = d.am;
@@ -343,9 +345,11 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     __shared__ int s_last;
     __shared__ int s_ready;
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
+    __shared__ __attribute__((aligned(1024))) char s_ring[RING ? 4 : 1][RING ? kDecode8Ring : 1]
+                                                        [RING ? Ring8<KS8>::kSlot : 16];
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     const int col = lane & 15;
     const int kg = lane >> 4;
 
@@ -360,21 +364,33 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     const PriorT* prior = static_cast<const PriorT*>(a.prior);
     decode_rows<BaseT, PriorT>(a, kg, al, be, use_prior, brow, best, bidx);
     const int ntiles = (a.V + 15) >> 4;
+    // The first tiles of the argmax stream go in flight while the rank is finished.
     TileRegs8<KS8> ta, tb;
-    if (t < ntiles) load_tile8<KS8>(a, t, lane, brow, prior, ta);
-    if (t + nwaves < ntiles) load_tile8<KS8>(a, t + nwaves, lane, brow, prior, tb);
+    uint32_t row_off = 0;
+    int issued = 0;
+    if constexpr (RING) {
+        row_off = ring8_row_off<BaseT>(a, 0, lane);
+        for (int i = 0; i < kDecode8Ring && t + i * nwaves < ntiles; ++i, ++issued)
+            issue_tile8_lds<KS8, BaseT, PriorT>(a, t + i * nwaves, lane, row_off, &s_ring[wave][i][0]);
+    } else {
+        if (t < ntiles) load_tile8<KS8>(a, t, lane, brow, prior, ta);
+        if (t + nwaves < ntiles) load_tile8<KS8>(a, t + nwaves, lane, brow, prior, tb);
+    }
 
     decode_rank_into_lds<r, true>(d, a.M, red, s_ready, s_rank);
+    __shared__ __attribute__((aligned(16))) uint8_t s_rq[16 * (r + 16)];
+    __shared__ float s_rsc[16];
+    quantize_rank_coop<r>(s_rank, r, a.M, s_rq, s_rsc);
     i32x8 rq[KS8];
     float rsc[4];
-    {
-        const bool mok = col < a.M;
-        const float own = quantize_rank_rows<KS8>(&s_rank[col * r + 32 * kg], mok, rq);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rsc[q] = __shfl(own, 4 * kg + q, 64);
-    }
-    stream_tiles8<KS8>(a, rq, rsc, t, nwaves, ntiles, lane, brow, prior, al, be, use_prior, best, bidx, ta, tb,
-                       true);
+    load_rank_operand<KS8>(s_rq, s_rsc, lane, rq, rsc);
+    if constexpr (RING)
+        stream_tiles8_lds<KS8, kDecode8Ring, BaseT, PriorT>(a, rq, rsc, t, nwaves, ntiles, lane, row_off,
+                                                            &s_ring[wave][0][0], issued, al, be, use_prior, best,
+                                                            bidx);
+    else
+        stream_tiles8<KS8>(a, rq, rsc, t, nwaves, ntiles, lane, brow, prior, al, be, use_prior, best, bidx, ta, tb,
+                           true);
     argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, d.done);
 }
 
@@ -409,7 +425,11 @@ hipError_t launch_decode8_for_base(const DecodeKArgs& ka, int prior_kind, hipStr
     auto go = [&](auto ks_tag, auto prior_tag) -> hipError_t {
         constexpr int KS8 = decltype(ks_tag)::value;
         using PT = decltype(prior_tag);
-        hipLaunchKernelGGL((lowrank_decode8_kernel<KS8, BaseT, PT>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
+        const int pb = is_no_prior<PT>::value ? 0 : elem_bytes<PT>::value;
+        if (ring8_eligible(ka.am, elem_bytes<BaseT>::value, pb))
+            hipLaunchKernelGGL((lowrank_decode8_kernel<KS8, BaseT, PT, true>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
+        else
+            hipLaunchKernelGGL((lowrank_decode8_kernel<KS8, BaseT, PT, false>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
         return hipGetLastError();
     };
     auto by_prior = [&](auto ks_tag) -> hipError_t {

@@ -37,6 +37,7 @@ __all__ = [
     "bf16_bits_to_f32",
     "e4m3_round",
     "quantize_rows_e4m3",
+    "quantize_rank_e4m3",
     "sigmoid_f32",
     "silu_f32",
     "rank_proj",
@@ -405,12 +406,12 @@ def rank_proj_fp8(h, A_q, A_scale, bias=None, act: str = "identity") -> np.ndarr
 def fused_argmax_fp8(rank, B_q, B_scale, base, prior, alpha, beta, *, chunk: int = 8192):
     """fp8 argmax on a given rank: each rank row quantised to e4m3, then an fp8 x fp8 contraction.
 
-    ``R_q, sR = quantize_rows_e4m3(rank)``;
+    ``R_q, sR = quantize_rank_e4m3(rank)``;
     ``dot[m, v] = fp32(fp32(R_q[m] . B_q[v]) * sR[m]) * sB[v]`` followed by the
     same fp32 combine and argmax as the bf16 path (``fused_argmax``).  Returns
     ``(ids, best, second)``.
     """
-    R_q, R_scale = quantize_rows_e4m3(rank)
+    R_q, R_scale = quantize_rank_e4m3(rank)
     base = np.asarray(base, _F32)
     M, V = base.shape
     alpha = _rowvec(alpha, M)
@@ -438,9 +439,28 @@ def fused_argmax_fp8(rank, B_q, B_scale, base, prior, alpha, beta, *, chunk: int
     return idx.astype(np.int64), best, second
 
 
+def quantize_rank_e4m3(rank) -> tuple[np.ndarray, np.ndarray]:
+    """Per-row e4m3 quantisation of the rank inside the fp8 kernels.
+
+    ``inv = fp32(448 / absmax)``, ``q = e4m3(fp32(rank * inv))`` and
+    ``scale = fp32(absmax / 448)`` (1 and zeros for an all-zero row): one
+    division per row instead of one per element, so the rounding differs from
+    ``quantize_rows_e4m3`` (``w / scale``) by at most one fp32 ulp of the
+    quotient before the e4m3 rounding.
+    """
+    w = np.asarray(rank, dtype=_F32)
+    amax = np.abs(w).max(axis=1)
+    nz = amax > 0
+    safe = np.where(nz, amax, _F32(1.0)).astype(_F32)
+    inv = np.where(nz, (_F32(_E4M3_MAX) / safe).astype(_F32), _F32(1.0)).astype(_F32)
+    scale = np.where(nz, (safe / _F32(_E4M3_MAX)).astype(_F32), _F32(1.0)).astype(_F32)
+    q = e4m3_round((w * inv[:, None]).astype(_F32))
+    return q, scale
+
+
 def score_at_fp8(rank, B_q, B_scale, base, prior, alpha, beta, ids) -> np.ndarray:
     """The fp8 path's combined score of row m at vocabulary index ``ids[m]``."""
-    R_q, R_scale = quantize_rows_e4m3(rank)
+    R_q, R_scale = quantize_rank_e4m3(rank)
     base = np.asarray(base, _F32)
     M = base.shape[0]
     ids = np.asarray(ids, np.int64).reshape(-1)

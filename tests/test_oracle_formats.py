@@ -117,7 +117,8 @@ def test_fused_argmax_fp8_brute_force_with_torch_casts():
     for m in range(M):
         amax = np.float32(np.abs(rank[m]).max())
         sR = np.float32(amax / np.float32(448.0)) if amax > 0 else np.float32(1.0)
-        rq = torch.from_numpy((rank[m] / sR).astype(np.float32)).to(torch.float8_e4m3fn).float().numpy()
+        inv = np.float32(np.float32(448.0) / amax) if amax > 0 else np.float32(1.0)
+        rq = torch.from_numpy((rank[m] * inv).astype(np.float32)).to(torch.float8_e4m3fn).float().numpy()
         scores = []
         for v in range(V):
             raw = np.float32(sum(float(a) * float(b) for a, b in zip(rq, Bq[v])))
@@ -144,3 +145,20 @@ def test_fused_argmax_fp8_scale_equivariance():
     b = oracle.fused_argmax_fp8(rank, q2, s2, base, None, 0.5, 0.0)
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x, y)
+
+
+def test_quantize_rank_e4m3_against_torch_and_division_form():
+    rng = np.random.default_rng(34)
+    rank = torch.from_numpy((rng.standard_normal((40, 512)) * 3).astype(np.float32)).bfloat16().float().numpy()
+    rank[7] = 0.0
+    q, s = oracle.quantize_rank_e4m3(rank)
+    assert s[7] == 1.0 and np.all(q[7] == 0)
+    amax = np.abs(rank).max(axis=1)
+    inv = np.where(amax > 0, np.float32(448.0) / np.where(amax > 0, amax, 1), 1).astype(np.float32)
+    ref = torch.from_numpy((rank * inv[:, None]).astype(np.float32)).to(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(q, ref)
+    np.testing.assert_array_equal(np.abs(q).max(axis=1)[np.arange(40) != 7], 448.0)
+    # against the per-element division form: equal but for rare quotients within an fp32 ulp of a midpoint
+    qd, sd = oracle.quantize_rows_e4m3(rank)
+    np.testing.assert_array_equal(s, sd)
+    assert (q != qd).mean() < 1e-3
