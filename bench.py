@@ -292,6 +292,7 @@ def bench_fp8(pkg, name, args, dev, torch):
     s = x0.shape
     M, d, r, V = s["M"], s["d"], s["r"], s["V"]
     weights = [(pkg.quantize_pack_fp8(x.A, "k32"), pkg.quantize_pack_fp8(x.B, "k128")) for x in sets]
+    ranks = [pkg.rank_proj(x.h, x.A, None, x.act) for x in sets]   # for the argmax-only timing
     for x in sets:   # the bf16 weights are not read by the fp8 step
         x.A = x.B = None
     torch.cuda.empty_cache()
@@ -316,6 +317,18 @@ def bench_fp8(pkg, name, args, dev, torch):
         if not (torch.equal(outs[i][0], eager[i][0]) and torch.equal(outs[i][1], eager[i][1])):
             raise RuntimeError(f"fp8 graph replay differs from eager results on set {i}")
     us = ms_total * 1e3 / steps
+
+    def argmax_only(i):
+        x = sets[i % nsets]
+        o = outs[i % nsets]
+        pkg.fused_argmax_fp8(ranks[i % nsets], weights[i % nsets][1], x.base, x.prior, x.alpha, x.beta,
+                             out_ids=o[0], out_score=o[1])
+
+    argmax_only(0)
+    torch.cuda.synchronize(dev)
+    ms_arg, g = time_graph(torch, argmax_only, steps, dev)
+    del g
+    us_arg = ms_arg * 1e3 / steps
     sb = x0.base.element_size()
     sp = x0.prior.element_size()
     nbytes = r * V + r * d + 2 * M * d + sb * M * V + sp * V + 4 * (V + r) + 12 * M
@@ -324,7 +337,11 @@ def bench_fp8(pkg, name, args, dev, torch):
             "skinny_gemm_kernel (e4m3 A) + fused_argmax_gemv8_kernel",
             "rows_per_s": M / (us * 1e-6), "us_per_step": us, "algorithmic_bytes": nbytes,
             "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "sets": nsets}
+            "sets": nsets,
+            "fused_argmax_only": {"kernel": "fused_argmax_gemv8_kernel", "us_per_launch": us_arg,
+                                  "algorithmic_bytes": nbytes - r * d - 2 * M * d - 4 * r + 2 * M * r,
+                                  "hbm_frac": (nbytes - r * d - 2 * M * d - 4 * r + 2 * M * r) / (us_arg * 1e-6)
+                                  / 1e9 / HBM_PEAK_GBS}}
 
 
 def cpu_baseline(name, x0, seconds):

@@ -125,14 +125,22 @@ __device__ __forceinline__ float lds_f32(const f16_t* p) {
 }
 
 // Wait until at most `pending` groups of PER direct-to-LDS loads are in flight
-// (pending is wave-uniform, 0 .. 3; s_waitcnt takes an immediate).
+// (pending is wave-uniform, 0 .. 4; s_waitcnt takes an immediate).
 template <int PER>
 __device__ __forceinline__ void wait_dma_groups(int pending) {
-    static_assert(3 * PER <= 63, "vmcnt holds at most 63");
+    static_assert(4 * PER <= 63, "vmcnt holds at most 63");
     if (pending <= 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     else if (pending == 1) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(PER) : "memory");
     else if (pending == 2) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(2 * PER) : "memory");
-    else asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * PER) : "memory");
+    else if (pending == 3) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(3 * PER) : "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" : : "n"(4 * PER) : "memory");
+}
+
+// Barrier for LDS traffic only: loads still in flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + expf(-x)); }

@@ -121,9 +121,7 @@ __device__ __forceinline__ void quantize_rank_coop(const uint16_t* rows, int64_t
         *reinterpret_cast<u32x2*>(s_rq + m * (R + 16) + seg * PER + 8 * i) = u32x2{w[0], w[1]};
     }
     if (seg == 0) s_rsc[m] = amax > 0.f ? amax / kE4M3Max : 1.f;
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
+    lds_barrier();
 }
 
 // The lane's e4m3 A operand (row lane%16, bytes 32*(lane/16) .. of each K128

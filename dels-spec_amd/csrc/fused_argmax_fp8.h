@@ -238,7 +238,7 @@ __device__ __forceinline__ void stream_tiles8_lds(const ArgmaxKArgs& a, const i3
     }
 }
 
-constexpr int kGemv8Ring = 4;   // LDS ring slots per wave (GEMV)
+constexpr int kGemv8Ring = 3;   // LDS ring slots per wave (GEMV; the rank rows take 16 KB of LDS too)
 
 template <int KS8, typename BaseT, typename PriorT, bool RING>
 __global__ __launch_bounds__(256) void fused_argmax_gemv8_kernel(ArgmaxKArgs a) {
@@ -255,41 +255,83 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv8_kernel(ArgmaxKArgs a) 
     const int kg = lane >> 4;
     const int m0 = blockIdx.y * 16;
 
-    // e4m3 rank operand of the 16 rows, quantised once per workgroup.
-    __shared__ __attribute__((aligned(16))) uint8_t s_rq[16 * (KS8 * 128 + 16)];
+    __shared__ __attribute__((aligned(16))) uint8_t s_rq[16 * (KS8 * 128 + 16)];   // e4m3 rank operand rows
     __shared__ float s_rsc[16];
-    quantize_rank_coop<KS8 * 128>(a.rank + (int64_t)m0 * a.ldrank, a.ldrank, a.M - m0, s_rq, s_rsc);
-    i32x8 rq[KS8];
-    float rsc[4];
-    load_rank_operand<KS8>(s_rq, s_rsc, lane, rq, rsc);
-
     float al[4], be[4], best[4];
     int bidx[4];
     bool use_prior[4];
-    const BaseT* brow[4];
-    const BaseT* base = static_cast<const BaseT*>(a.base);
-    const PriorT* prior = static_cast<const PriorT*>(a.prior);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int m = m0 + 4 * kg + q;
-        const bool mok = m < a.M;
-        al[q] = mok ? a.alpha[(int64_t)m * a.alpha_stride] : 0.f;
-        be[q] = mok ? a.beta[(int64_t)m * a.beta_stride] : 0.f;
-        use_prior[q] = !is_no_prior<PriorT>::value && (be[q] != 0.f);
-        brow[q] = base + (int64_t)(mok ? m : 0) * a.ldbase;
-        best[q] = -__builtin_inff();
-        bidx[q] = INT_MAX;
-    }
     const int ntiles = (a.V + 15) >> 4;
     const int nwaves = gridDim.x * 4;
+    const int t0 = blockIdx.x * 4 + wave;
+    i32x8 rq[KS8];
+    float rsc[4];
     if constexpr (RING) {
-        stream_tiles8_lds<KS8, kGemv8Ring, BaseT, PriorT>(a, rq, rsc, blockIdx.x * 4 + wave, nwaves, ntiles, lane,
-                                                          ring8_row_off<BaseT>(a, m0, lane), &s_ring[wave][0][0], 0,
-                                                          al, be, use_prior, best, bidx);
+        // Every load is direct-to-LDS, in this order: alpha/beta (wave 0), this
+        // wave's four rank rows, the first ring tiles.  One explicit wait then
+        // covers alpha/beta and the rank while the tiles stay in flight, so the
+        // rank's quantisation overlaps the first HBM burst (a compiler-counted
+        // load here would make its wait cover the whole burst).
+        constexpr int R = KS8 * 128;
+        constexpr int PER = ring8_dmas_per_tile<PriorT>(KS8);
+        __shared__ __attribute__((aligned(16))) uint16_t s_rk[16 * R];   // the 16 rank rows, bf16
+        __shared__ __attribute__((aligned(16))) float s_ab[2][16];      // alpha, beta of the rows
+        const int mrow = m0 + (lane & 15);
+        const uint32_t ab_row = (uint32_t)(mrow < a.M ? mrow : m0);
+        if (wave == 0 && lane < 16) {
+            dma4(a.alpha, ab_row * (uint32_t)a.alpha_stride * 4u, &s_ab[0][0]);
+            dma4(a.beta, ab_row * (uint32_t)a.beta_stride * 4u, &s_ab[1][0]);
+        }
+        constexpr int kLanesPerRow = R / 8;          // 16-byte pieces per rank row
+        constexpr int kRowsPerLoad = 64 / kLanesPerRow;
+#pragma unroll
+        for (int i = 0; i < KS8; ++i) {
+            const int row = 4 * wave + i * kRowsPerLoad;                 // first row of this load
+            const int g = m0 + row + lane / kLanesPerRow;
+            const uint32_t off = (uint32_t)((int64_t)(g < a.M ? g : m0) * a.ldrank * 2) +
+                                 (uint32_t)(lane % kLanesPerRow) * 16u;
+            dma16(a.rank, off, &s_rk[row * R]);
+        }
+        const uint32_t row_off = ring8_row_off<BaseT>(a, m0, lane);
+        const int nk = t0 < ntiles ? (ntiles - 1 - t0) / nwaves + 1 : 0;
+        const int first = nk < kGemv8Ring ? nk : kGemv8Ring;
+        for (int i = 0; i < first; ++i)
+            issue_tile8_lds<KS8, BaseT, PriorT>(a, t0 + i * nwaves, lane, row_off, &s_ring[wave][i][0]);
+        wait_dma_groups<PER>(first);
+        lds_barrier();
+        quantize_rank_coop<R>(s_rk, R, a.M - m0, s_rq, s_rsc);
+        load_rank_operand<KS8>(s_rq, s_rsc, lane, rq, rsc);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const bool mok = m0 + 4 * kg + q < a.M;
+            al[q] = mok ? s_ab[0][4 * kg + q] : 0.f;
+            be[q] = mok ? s_ab[1][4 * kg + q] : 0.f;
+            use_prior[q] = !is_no_prior<PriorT>::value && (be[q] != 0.f);
+            best[q] = -__builtin_inff();
+            bidx[q] = INT_MAX;
+        }
+        stream_tiles8_lds<KS8, kGemv8Ring, BaseT, PriorT>(a, rq, rsc, t0, nwaves, ntiles, lane, row_off,
+                                                          &s_ring[wave][0][0], first, al, be, use_prior, best,
+                                                          bidx);
     } else {
+        quantize_rank_coop<KS8 * 128>(a.rank + (int64_t)m0 * a.ldrank, a.ldrank, a.M - m0, s_rq, s_rsc);
+        load_rank_operand<KS8>(s_rq, s_rsc, lane, rq, rsc);
+        const BaseT* brow[4];
+        const BaseT* base = static_cast<const BaseT*>(a.base);
+        const PriorT* prior = static_cast<const PriorT*>(a.prior);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int m = m0 + 4 * kg + q;
+            const bool mok = m < a.M;
+            al[q] = mok ? a.alpha[(int64_t)m * a.alpha_stride] : 0.f;
+            be[q] = mok ? a.beta[(int64_t)m * a.beta_stride] : 0.f;
+            use_prior[q] = !is_no_prior<PriorT>::value && (be[q] != 0.f);
+            brow[q] = base + (int64_t)(mok ? m : 0) * a.ldbase;
+            best[q] = -__builtin_inff();
+            bidx[q] = INT_MAX;
+        }
         TileRegs8<KS8> ta, tb;
-        stream_tiles8<KS8>(a, rq, rsc, blockIdx.x * 4 + wave, nwaves, ntiles, lane, brow, prior, al, be, use_prior,
-                           best, bidx, ta, tb, false);
+        stream_tiles8<KS8>(a, rq, rsc, t0, nwaves, ntiles, lane, brow, prior, al, be, use_prior, best, bidx, ta, tb,
+                           false);
     }
     argmax_wg_finish(a, best, bidx, m0, s_val, s_idx, s_last, nullptr);
 }
@@ -299,6 +341,11 @@ inline bool ring8_eligible(const ArgmaxKArgs& ka, int base_bytes, int prior_byte
     auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (ka.V % 16 != 0 || !al16(ka.base) || (ka.ldbase * base_bytes) % 16 != 0 || !al16(ka.b_scale)) return false;
     if ((int64_t)ka.M * ka.ldbase * base_bytes >= ((int64_t)1 << 31)) return false;
+    // rank rows and alpha/beta by direct-to-LDS loads: 16-byte rows, 32-bit offsets
+    if (ka.rank != nullptr && (!al16(ka.rank) || ka.ldrank % 8 != 0 || (int64_t)ka.M * ka.ldrank * 2 >= ((int64_t)1 << 31)))
+        return false;
+    if ((reinterpret_cast<uintptr_t>(ka.alpha) & 3) != 0 || (reinterpret_cast<uintptr_t>(ka.beta) & 3) != 0) return false;
+    if ((int64_t)ka.M * (ka.alpha_stride + ka.beta_stride) * 4 >= ((int64_t)1 << 31)) return false;
     return ka.prior == nullptr || (al16(ka.prior) && prior_bytes > 0);
 }
 
