@@ -2,6 +2,8 @@
 
 Public surface (mirrors the reference's interface for this path):
   * ``DeLSGraphRunner``          -- drop-in hipGraph suffix-rollout runner
+  * ``DeLSDraftStep``            -- a whole draft block (target LM head, first
+    argmax, rollout) as one graph
   * ``DeLSLocalHead``            -- local-head module the runner consumes
   * ``parse_scalar_schedule``, ``load_unigram_log_prior``
   * ``fused_argmax``, ``lowrank_argmax``, ``rank_proj``, ``gru_step`` -- the
@@ -14,14 +16,17 @@ Public surface (mirrors the reference's interface for this path):
 
 from .local_head import (DeLSLocalHead, load_unigram_log_prior, parse_scalar_schedule,
                          unigram_log_prior_from_counts)
-from .ops import (Fp8Weight, PackedWeight, fused_argmax, fused_argmax_fp8, gru_step, lowrank_argmax,
+from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gru_step, lowrank_argmax,
                   lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows, quantize_pack_fp8,
                   rank_proj)
+from .draft_step import DeLSDraftStep
 from .runner import DeLSGraphRunner
 from . import synth
 
 __all__ = [
     "DeLSGraphRunner",
+    "DeLSDraftStep",
+    "argmax_rows",
     "DeLSLocalHead",
     "parse_scalar_schedule",
     "load_unigram_log_prior",

@@ -16,6 +16,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime first, so the library b
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
 
+ABI_VERSION = 2
 DELS_OK = 0
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_IDENTITY, ACT_SILU = 0, 1
@@ -42,7 +43,7 @@ class RolloutParams(ctypes.Structure):
         ("batch", _i64), ("steps", _i64), ("G", _i64), ("r", _i64), ("V", _i64),
         ("weights_layout", _int),
         ("prefix_ids", _ptr),
-        ("base", _ptr), ("base_dtype", _int),
+        ("base", _ptr), ("base_dtype", _int), ("ld_base", _i64),
         ("out_ids", _ptr), ("out_scores", _ptr),
         ("h_a", _ptr), ("h_b", _ptr),
         ("rank", _ptr),
@@ -78,6 +79,8 @@ SIGNATURES = {
     "dels_graph_create": (_int, [ctypes.POINTER(RolloutParams), ctypes.POINTER(_ptr)]),
     "dels_graph_launch": (_int, [_ptr, _ptr]),
     "dels_graph_destroy": (_int, [_ptr]),
+    "dels_argmax_rows_ws_bytes": (_sz, [_i64, _i64]),
+    "dels_argmax_rows": (_int, [_ptr, _i64, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_packed_fp8_bytes": (_sz, [_i64, _i64, _int]),
     "dels_pack_operand_fp8": (_int, [_ptr, _i64, _i64, _i64, _int, _ptr, _sz, _ptr]),
     "dels_fused_argmax_fp8_ws_bytes": (_sz, [_i64, _i64, _i64]),
@@ -118,7 +121,7 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.dels_abi_version() != 1:
+        if lib.dels_abi_version() != ABI_VERSION:
             raise RuntimeError("DeLS HIP library ABI version mismatch")
         _lib = lib
     return _lib

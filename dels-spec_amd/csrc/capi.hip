@@ -193,7 +193,10 @@ static int check_rollout(const dels_rollout* p) {
     if (rc != DELS_OK) return rc;
     if ((rc = check_bf16_matrix(p->h_b, p->G, p->G, "h_b")) != DELS_OK) return rc;
     if ((rc = check_weight(p->rank_w, p->G, p->G, p->weights_layout, "rank_w")) != DELS_OK) return rc;
-    if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->weights_layout, p->base, p->steps * p->V, p->base_dtype, p->prior,
+    if (p->ld_base != 0 && p->ld_base < p->steps * p->V)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "rollout ld_base %lld < steps * V", (long long)p->ld_base);
+    if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->weights_layout, p->base,
+                                p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->prior,
                                 p->prior_dtype, p->alpha, 0, p->beta, 0, p->batch, p->r, p->V, p->out_ids,
                                 p->steps, true)) != DELS_OK)
         return rc;
@@ -245,7 +248,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.B = static_cast<const uint16_t*>(p->lm_w); aa.ldb = r;
         aa.b_packed = p->weights_layout == DELS_LAYOUT_MFMA16;
         aa.base = static_cast<const char*>(p->base) + (size_t)step * V * esz;
-        aa.ldbase = p->steps * (int64_t)V;
+        aa.ldbase = p->ld_base ? p->ld_base : p->steps * (int64_t)V;
         aa.base_dtype = p->base_dtype;
         aa.prior = p->prior; aa.prior_dtype = p->prior_dtype;
         aa.alpha = p->alpha + step; aa.alpha_stride = 0;
@@ -575,6 +578,27 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
     if (e != hipSuccess) return hip_fail(e, "fp8 rank projection launch");
     e = launch_fused_argmax_fp8(a, ws, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
+}
+
+size_t dels_argmax_rows_ws_bytes(int64_t, int64_t) { return kCtrlBytes; }
+
+int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V, int64_t* out_ids, float* out_score,
+                     int64_t ld_out, void* ws, size_t ws_bytes, void* stream) {
+    if (M < 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape M=%lld V=%lld", (long long)M, (long long)V);
+    if (M > kMaxKeyRows || V >= INT32_MAX) return fail(DELS_ERR_UNSUPPORTED, "argmax rows: M <= %d and V < 2^31-1",
+                                                       kMaxKeyRows);
+    if (M == 0) return DELS_OK;
+    if (!x) return fail(DELS_ERR_INVALID_ARGUMENT, "logits pointer is NULL");
+    if (!valid_dtype(dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown logits dtype %d", dtype);
+    if (M > 1 && ldx < V) return fail(DELS_ERR_INVALID_ARGUMENT, "logits leading dimension %lld < V %lld",
+                                      (long long)ldx, (long long)V);
+    if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+    if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    int rc = check_ws(ws, ws_bytes, kCtrlBytes);
+    if (rc != DELS_OK) return rc;
+    hipError_t e = launch_argmax_rows(x, ldx, dtype, (int)M, (int)V, out_ids, out_score, ld_out, ws,
+                                      static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "argmax rows launch");
 }
 
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {

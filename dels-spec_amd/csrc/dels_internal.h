@@ -80,6 +80,10 @@ bool argmax_supported(int64_t M, int64_t r, int64_t V);
 // `ws` is the workspace base (control area); partials go to ws + data_off.
 hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
+// Plain per-row argmax of logits [M, V] (dtype 0 fp32, 1 bf16, 2 fp16), M <= kMaxKeyRows.
+hipError_t launch_argmax_rows(const void* x, int64_t ldx, int dtype, int M, int V, int64_t* out_ids,
+                              float* out_score, int64_t ld_out, void* ws, hipStream_t s);
+
 // fp8 argmax (b_scale set): r in {128, 256, 512}, any M up to kMaxKeyRows.
 bool argmax_fp8_supported(int64_t M, int64_t r);
 hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, hipStream_t s);

@@ -130,6 +130,108 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
     return launch_gemv_f32(ka, a.b_packed, pk, s);
 }
 
+// ---- plain row argmax ------------------------------------------------------------
+//
+// sample() at temperature 0 (code/dflash.py:31-33: torch.argmax over the last
+// dimension): the lowest index of each row's maximum.  Rows are split into
+// chunks over workgroups; each folds its best (value, index) into the row's
+// 64-bit key with a device-scope atomic max, and the last workgroup decodes and
+// clears the keys and the counter (as the fused argmax).  NaN entries are
+// skipped and an all -inf row gives index 0 with score -inf, as in the fused
+// argmax.
+
+namespace {
+
+template <typename T>
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x, int64_t ldx, int M, int V,
+                                                          int chunk, unsigned long long* keys, int64_t key_stride,
+                                                          unsigned int* counter, int64_t* out_ids, float* out_score,
+                                                          int64_t ld_out) {
+    __shared__ float s_val[4];
+    __shared__ int s_idx[4];
+    __shared__ int s_last;
+    const int m = blockIdx.y;
+    const int v0 = blockIdx.x * chunk;
+    const int v1 = min(V, v0 + chunk);
+    const T* row = x + (int64_t)m * ldx;
+    float best = -__builtin_inff();
+    int bi = INT_MAX;
+    for (int v = v0 + (int)threadIdx.x; v < v1; v += 256) {
+        const float sv = load_f32(row + v);
+        const bool take = argmax_better(sv, v, best, bi);
+        best = take ? sv : best;
+        bi = take ? v : bi;
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (argmax_better(ov, oi, best, bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        s_val[wave] = best;
+        s_idx[wave] = bi;
+    }
+    __syncthreads();
+    unsigned long long seen = 0;
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (argmax_better(s_val[w], s_idx[w], best, bi)) {
+                best = s_val[w];
+                bi = s_idx[w];
+            }
+        if (bi != INT_MAX)
+            seen = __hip_atomic_fetch_max(&keys[(int64_t)m * key_stride], pack_argmax(best, (uint32_t)bi),
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the returned value orders the count after the update
+        const unsigned prev = __hip_atomic_fetch_add(counter, seen == ~0ull ? 2u : 1u, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == gridDim.x * gridDim.y - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    for (int r = threadIdx.x; r < M; r += blockDim.x) {
+        const unsigned long long key = __hip_atomic_exchange(&keys[(int64_t)r * key_stride], 0ull, __ATOMIC_RELAXED,
+                                                             __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t idx = ~(uint32_t)(key & 0xffffffffull);
+        float val = f32_from_order_key((uint32_t)(key >> 32));
+        if (key == 0ull || idx >= (uint32_t)V) {
+            idx = 0;
+            val = -__builtin_inff();
+        }
+        out_ids[(int64_t)r * ld_out] = (int64_t)idx;
+        if (out_score) out_score[(int64_t)r * ld_out] = val;
+    }
+    if (threadIdx.x == 0) __hip_atomic_exchange(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+hipError_t launch_argmax_rows(const void* x, int64_t ldx, int dtype, int M, int V, int64_t* out_ids,
+                              float* out_score, int64_t ld_out, void* ws, hipStream_t s) {
+    char* w = static_cast<char*>(ws);
+    auto* counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
+    auto* keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
+    const int64_t key_stride = (int64_t)M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
+    const int gx = std::max(1, std::min(64, (V + 4095) / 4096));
+    const int chunk = (V + gx - 1) / gx;
+    const dim3 grid(gx, M);
+    if (dtype == 1)
+        hipLaunchKernelGGL(argmax_rows_kernel<bf16_t>, grid, dim3(256), 0, s, static_cast<const bf16_t*>(x), ldx, M, V,
+                           chunk, keys, key_stride, counter, out_ids, out_score, ld_out);
+    else if (dtype == 2)
+        hipLaunchKernelGGL(argmax_rows_kernel<f16_t>, grid, dim3(256), 0, s, static_cast<const f16_t*>(x), ldx, M, V,
+                           chunk, keys, key_stride, counter, out_ids, out_score, ld_out);
+    else
+        hipLaunchKernelGGL(argmax_rows_kernel<float>, grid, dim3(256), 0, s, static_cast<const float*>(x), ldx, M, V,
+                           chunk, keys, key_stride, counter, out_ids, out_score, ld_out);
+    return hipGetLastError();
+}
+
 // ---- fp8 argmax ------------------------------------------------------------
 
 bool argmax_fp8_supported(int64_t M, int64_t r) {

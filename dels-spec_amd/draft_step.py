@@ -1,0 +1,114 @@
+"""DeLSDraftStep: one whole DeLS draft block on the device, as a single hipGraph.
+
+The graph path of ``spec_generate`` for one block (code/dflash.py:452-486):
+
+    base_logits = target.lm_head(parallel_hiddens)            # [B, k, V] (k = k_draft)
+    verify_ids[:, 1] = sample(base_logits[:, :1])             # plain argmax of position 0
+    verify_ids[:, 2:k+1] = graph_runner(verify_ids[:, 1:2], base_logits[:, 1:k])
+
+Here the LM-head GEMM is a plain library GEMM (``torch.mm`` -> hipBLASLt, as
+``nn.Linear`` does in the reference), the first-position argmax is
+``dels_argmax_rows`` and the suffix rollout is ``dels_rollout_enqueue`` over the
+runner's packed weights, reading ``base_logits[:, 1:k]`` in place (row stride
+k * V).  All three are captured once into one graph and replayed per block.
+The drafter that produces ``parallel_hiddens`` is outside this path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .ops import new_workspace
+from .runner import DeLSGraphRunner
+
+
+class DeLSDraftStep:
+    """One draft block: target LM head, first-position argmax and the DeLS rollout in one graph.
+
+    ``k_draft`` is the block's draft count (block_size - 1 unshifted,
+    code/dflash.py:442); the rollout runs ``k_draft - 1`` DeLS steps, so the
+    alpha/beta schedules have that length (code/dflash.py:477).
+    ``__call__(parallel_hiddens [B, k_draft, d] bf16) -> int64 [B, k_draft]``
+    returns verify ids 1 .. k_draft of the block (a fresh tensor).
+    """
+
+    def __init__(self, *, local_head, lm_head_weight: torch.Tensor, batch_size: int, k_draft: int,
+                 vocab_size: int, alpha_values: list[float], beta_values: list[float],
+                 baseline_logits: Optional[torch.Tensor], device: torch.device):
+        if k_draft < 2:
+            raise ValueError(f"DeLSDraftStep needs k_draft >= 2 (at least one DeLS step), got {k_draft}.")
+        self.runner = DeLSGraphRunner(local_head=local_head, batch_size=batch_size, steps=k_draft - 1,
+                                      vocab_size=vocab_size, alpha_values=alpha_values, beta_values=beta_values,
+                                      baseline_logits=baseline_logits, device=device)
+        device = self.runner.device
+        self.device = device
+        B, k, V = int(batch_size), int(k_draft), int(vocab_size)
+        W = lm_head_weight.detach().to(device)
+        if W.dtype != torch.bfloat16 or W.dim() != 2 or int(W.shape[0]) != V:
+            raise ValueError("lm_head_weight must be a bfloat16 [vocab_size, hidden] matrix")
+        self.lm_head_weight = W.contiguous()
+        d = int(W.shape[1])
+        self.batch_size, self.k_draft, self.vocab_size, self.hidden_size = B, k, V, d
+        self.static_hidden = torch.zeros(B, k, d, dtype=torch.bfloat16, device=device)
+        self.static_base = torch.empty(B, k, V, dtype=torch.bfloat16, device=device)
+        self.static_first = torch.zeros(B, dtype=torch.int64, device=device)
+        self.static_first_score = torch.zeros(B, dtype=torch.float32, device=device)
+        self.static_rest = torch.zeros(B, k - 1, dtype=torch.int64, device=device)
+        self.static_rest_scores = torch.zeros(B, k - 1, dtype=torch.float32, device=device)
+        self.static_out = torch.zeros(B, k, dtype=torch.int64, device=device)
+        lib = _lib.load()
+        self._ws = new_workspace(device, max(lib.dels_rollout_ws_bytes(B, self.runner.gru_hidden_dim,
+                                                                        self.runner.rank_dim, V),
+                                             lib.dels_argmax_rows_ws_bytes(B, V)))
+        self._params = self.runner._rollout_params(self.static_base[:, 1:, :], k * V, self.static_first,
+                                                   self.static_rest, self.static_rest_scores, self._ws)
+        self._graph = None
+        self._capture()
+
+    def _enqueue(self, stream: torch.cuda.Stream) -> None:
+        B, k, V, d = self.batch_size, self.k_draft, self.vocab_size, self.hidden_size
+        lib = _lib.load()
+        # base logits of the whole block: [B*k, d] . W^T, as nn.Linear
+        torch.mm(self.static_hidden.view(B * k, d), self.lm_head_weight.t(), out=self.static_base.view(B * k, V))
+        _lib.check(lib.dels_argmax_rows(self.static_base.data_ptr(), k * V, _lib.DTYPE_BF16, B, V,
+                                        self.static_first.data_ptr(), self.static_first_score.data_ptr(), 1,
+                                        self._ws.data_ptr(), self._ws.numel(), stream.cuda_stream),
+                   "dels_argmax_rows")
+        _lib.check(lib.dels_rollout_enqueue(ctypes.byref(self._params), stream.cuda_stream), "dels_rollout_enqueue")
+        self.static_out[:, 0].copy_(self.static_first)
+        self.static_out[:, 1:].copy_(self.static_rest)
+
+    def _capture(self) -> None:
+        side = torch.cuda.Stream(device=self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            self._enqueue(side)                      # warm-up outside the capture (library plans, workspaces)
+            torch.cuda.synchronize(self.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=side):
+                self._enqueue(side)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self._graph = graph
+
+    def replay(self) -> None:
+        """Run the captured block on the current stream (inputs already in ``static_hidden``)."""
+        self._graph.replay()
+
+    def enqueue_eager(self) -> None:
+        """The same work without the graph, on the current stream."""
+        self._enqueue(torch.cuda.current_stream(self.device))
+
+    @torch.inference_mode()
+    def __call__(self, parallel_hiddens: torch.Tensor) -> torch.Tensor:
+        self.static_hidden.copy_(parallel_hiddens)
+        self.replay()
+        return self.static_out.clone()
+
+    def close(self) -> None:
+        self._graph = None
+        self.runner.close()

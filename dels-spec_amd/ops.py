@@ -323,6 +323,30 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: Weight, lm_head_weight: Weight,
 
 
 
+
+def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,
+                out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``sample()`` at temperature 0 (code/dflash.py:31-33): the lowest index of
+    each row's maximum over the last dimension.  ``logits`` [M, V] (any row
+    stride, unit column stride) fp32/bf16/fp16.  NaN entries are skipped; an all
+    -inf row gives id 0.  Returns ``(ids int64[M], score fp32[M])``."""
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    _require_cuda(logits, "logits")
+    if logits.dtype not in _DTYPES:
+        raise TypeError(f"logits must be float32, bfloat16 or float16, got {logits.dtype}")
+    if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
+        raise ValueError("logits must be an [M, V] matrix with unit column stride")
+    M, V = logits.shape
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, logits.device)
+    lib = _lib.load()
+    ws = workspace(logits.device, lib.dels_argmax_rows_ws_bytes(M, V))
+    _lib.check(lib.dels_argmax_rows(logits.data_ptr(), logits.stride(0), _DTYPES[logits.dtype], M, V,
+                                    out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(),
+                                    _stream_ptr(logits.device)), "dels_argmax_rows")
+    return out_ids, out_score
+
+
 # ---- fp8 variant (e4m3 weights with per-output-channel scales) -----------------
 
 E4M3_MAX = 448.0

@@ -115,9 +115,23 @@ class DeLSGraphRunner:
             self._beta = torch.tensor(self.beta_values, dtype=torch.float32, device=device)
 
         lib = _lib.load()
-        ws_bytes = lib.dels_rollout_ws_bytes(B, G, r, V)
-        self._ws = new_workspace(device, ws_bytes)
+        self._ws = new_workspace(device, lib.dels_rollout_ws_bytes(B, G, r, V))
+        p = self._rollout_params(self.static_base_logits, S * V, self.static_prefix_ids, self.static_out,
+                                 self.static_scores, self._ws)
+        self._params = p
+        torch.cuda.synchronize(device)
+        handle = ctypes.c_void_p()
+        with torch.cuda.device(device):
+            _lib.check(lib.dels_graph_create(ctypes.byref(p), ctypes.byref(handle)), "dels_graph_create")
+        self._graph = handle
+
+    def _rollout_params(self, base: torch.Tensor, ld_base: int, prefix_ids: torch.Tensor, out_ids: torch.Tensor,
+                        out_scores: torch.Tensor, ws: torch.Tensor) -> "_lib.RolloutParams":
+        """The C rollout description over these weights, reading ``base`` rows ``ld_base`` elements apart
+        (steps * V for a [B, steps, V] tensor) and writing ``out_ids``/``out_scores`` [B, steps]."""
+        B, G, r, V, S = self.batch_size, self.gru_hidden_dim, self.rank_dim, self.vocab_size, self.steps
         prior = self.baseline_logits if self.has_baseline else None
+        dtype = self.rank_weight.dtype
         p = _lib.RolloutParams()
         p.gi_table = self._gru_input_proj_table.data_ptr()
         p.ld_gi = self._gru_input_proj_table.stride(0)
@@ -134,22 +148,18 @@ class DeLSGraphRunner:
         p.beta = self._beta.data_ptr()
         p.batch, p.steps, p.G, p.r, p.V = B, S, G, r, V
         p.weights_layout = _lib.LAYOUT_MFMA16 if self._packed else _lib.LAYOUT_ROWMAJOR
-        p.prefix_ids = self.static_prefix_ids.data_ptr()
-        p.base = self.static_base_logits.data_ptr()
-        p.base_dtype = _DTYPES[dtype]
-        p.out_ids = self.static_out.data_ptr()
-        p.out_scores = self.static_scores.data_ptr()
+        p.prefix_ids = prefix_ids.data_ptr()
+        p.base = base.data_ptr()
+        p.base_dtype = _DTYPES[base.dtype]
+        p.ld_base = int(ld_base)
+        p.out_ids = out_ids.data_ptr()
+        p.out_scores = out_scores.data_ptr()
         p.h_a = self._h_a.data_ptr()
         p.h_b = self._h_b.data_ptr()
         p.rank = self._rank.data_ptr()
-        p.ws = self._ws.data_ptr()
-        p.ws_bytes = self._ws.numel()
-        self._params = p
-        torch.cuda.synchronize(device)
-        handle = ctypes.c_void_p()
-        with torch.cuda.device(device):
-            _lib.check(lib.dels_graph_create(ctypes.byref(p), ctypes.byref(handle)), "dels_graph_create")
-        self._graph = handle
+        p.ws = ws.data_ptr()
+        p.ws_bytes = ws.numel()
+        return p
 
     def replay(self) -> None:
         """Launch the captured rollout on the current stream (no copies)."""

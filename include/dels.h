@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define DELS_ABI_VERSION 1
+#define DELS_ABI_VERSION 2
 
 /* status codes */
 #define DELS_OK 0
@@ -163,6 +163,19 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
 int dels_debug_set_decode_spin_limit(int limit);
 
 /*
+ * Plain argmax of each row of logits: sample() at temperature 0
+ * (code/dflash.py:31-33; torch.argmax over the vocabulary), as used for the
+ * first draft position (code/dflash.py:473).  x [M, V] with row stride ldx,
+ * dtype DELS_DTYPE_*; out_ids[m*ld_out] int64, out_score[m*ld_out] fp32 (or
+ * NULL).  Ties go to the lowest index; NaN entries are skipped; a row of -inf
+ * gives id 0 and score -inf.
+ */
+size_t dels_argmax_rows_ws_bytes(int64_t M, int64_t V);
+int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V,
+                     int64_t* out_ids, float* out_score, int64_t ld_out,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/*
  * fp8 variant (no counterpart in the reference: the fp8 configuration of the
  * same draft step, with e4m3 weights and per-output-channel fp32 scales).
  *
@@ -247,8 +260,9 @@ typedef struct dels_rollout {
     int64_t batch, steps, G, r, V;
     int weights_layout;     /* DELS_LAYOUT_* of w_hh, rank_w and lm_w */
     const int64_t* prefix_ids; /* [batch] int64 */
-    const void* base;       /* [batch, steps, V] */
+    const void* base;       /* [batch, steps, V]: row b, step s at base + (b * ld_base + s * V) */
     int base_dtype;
+    int64_t ld_base;        /* elements between batch rows of base (0: steps * V) */
     int64_t* out_ids;       /* [batch, steps] int64 */
     float* out_scores;      /* [batch, steps] fp32 or NULL */
     void* h_a;              /* [batch, G] bf16 state buffers (ping-pong) */
@@ -260,6 +274,7 @@ typedef struct dels_rollout {
 } dels_rollout;
 
 size_t dels_rollout_ws_bytes(int64_t batch, int64_t G, int64_t r, int64_t V);
+/* (A draft step feeds base_logits[:, 1:k, :] of its [batch, k, V] logits in place: ld_base = k * V.) */
 int dels_rollout_enqueue(const dels_rollout* p, void* stream);
 
 /*

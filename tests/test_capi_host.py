@@ -55,7 +55,7 @@ def test_rollout_struct_layout_matches_header(pkg):
 
 def test_abi_version_and_strerror(pkg):
     lib = pkg._lib.load()
-    assert lib.dels_abi_version() == 1
+    assert lib.dels_abi_version() == pkg._lib.ABI_VERSION == 2
     assert lib.dels_strerror(0) == b"success"
     assert lib.dels_strerror(-3) == b"misaligned operand"
     assert lib.dels_strerror(-99) == b"unknown status"

@@ -1,0 +1,91 @@
+"""GPU tests of the plain row argmax (sample() at temperature 0) and of the whole
+draft block as one graph (target LM head GEMM, first-position argmax, rollout).
+
+The LM-head GEMM is a library GEMM (hipBLASLt through torch.mm, as nn.Linear in
+the reference); its bf16 output is checked against a float32 CPU product within
+bf16 rounding, and the argmax and the rollout are then checked on the device's
+own base logits (the rollout teacher-forced on the device's ids, as for
+DeLSGraphRunner).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from test_gpu_parity import _Head
+
+pytestmark = pytest.mark.gpu
+
+
+def f(t):
+    return t.detach().float().cpu().numpy()
+
+
+def np_first_argmax(x):
+    """Lowest index of each row's maximum, NaN skipped, all -inf -> 0."""
+    x = np.where(np.isnan(x), -np.inf, x)
+    return np.argmax(x, axis=1)
+
+
+@pytest.mark.parametrize("M,V,dtype,stride_pad", [(8, 151936, torch.bfloat16, 0), (5, 4099, torch.float32, 7),
+                                                  (33, 20011, torch.float16, 0), (1, 1, torch.float32, 0)])
+def test_argmax_rows(pkg, dev, M, V, dtype, stride_pad):
+    print(f"case argmax_rows M={M} V={V} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(M + V)
+    full = (torch.randn(M, V + stride_pad, generator=g) * 3).to(dtype)
+    x = full[:, :V]
+    if M > 2 and V > 10:
+        x[0, 3] = x[0, V - 2] = 100.0                   # equal maxima: the lower index wins
+        x[1].fill_(-float("inf"))                        # all -inf -> 0
+        x[2, 5] = float("nan")                           # NaN is skipped
+    ids, score = pkg.argmax_rows(x.to(dev))
+    torch.cuda.synchronize()
+    xn = f(x)
+    ref = np_first_argmax(xn)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref)
+    np.testing.assert_array_equal(score.cpu().numpy(), np.where(np.isnan(xn), -np.inf, xn)[np.arange(M), ref])
+
+
+@pytest.mark.parametrize("B,k,d,V,E,G,r,act,with_prior", [(3, 6, 256, 5003, 32, 64, 64, "silu", True),
+                                                          (8, 15, 512, 30000, 64, 128, 256, "identity", False)])
+def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
+    print(f"case draft_step B={B} k={k} d={d} V={V} G={G} r={r}", flush=True)
+    head = _Head(V, E, G, r, act, False, seed=B + V, std=0.2).to(dev)
+    g = torch.Generator().manual_seed(7)
+    W = (torch.randn(V, d, generator=g) * 0.05).bfloat16()
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0) if with_prior else None
+    steps = k - 1
+    alphas = [0.1 + 0.05 * i for i in range(steps)]
+    betas = [0.3 if with_prior else 0.0] * steps
+    step = pkg.DeLSDraftStep(local_head=head, lm_head_weight=W.to(dev), batch_size=B, k_draft=k, vocab_size=V,
+                             alpha_values=alphas, beta_values=betas, baseline_logits=prior, device=dev)
+    hid = (torch.randn(B, k, d, generator=g)).bfloat16()
+    out = step(hid.to(dev))
+    torch.cuda.synchronize()
+    base = step.static_base.clone()
+    # replays and the eager path give the same ids
+    out2 = step(hid.to(dev))
+    step.enqueue_eager()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out2, out, rtol=0, atol=0)
+    torch.testing.assert_close(step.static_out, out, rtol=0, atol=0)
+    assert out.shape == (B, k) and out.dtype == torch.int64
+    # the GEMM is the LM head: base = bf16(hidden . W^T)
+    ref_base = (f(hid).reshape(B * k, d) @ f(W).T).reshape(B, k, V)
+    np.testing.assert_allclose(f(base), ref_base, rtol=2e-2, atol=2e-2)
+    # first position: plain argmax of the device's base logits
+    bn = f(base)
+    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), np_first_argmax(bn[:, 0, :]))
+    # the rollout on base[:, 1:], teacher-forced on the device's own ids
+    prior_np = f(prior.to(torch.bfloat16)) if with_prior else None
+    dev_ids = out[:, 1:].cpu().numpy()
+    rid, rsc, rsec = oracle.rollout(
+        out[:, 0].cpu().numpy(), bn[:, 1:, :], embed=f(head.embed_tokens.weight), W_ih=f(head.prefix_gru.weight_ih_l0),
+        W_hh=f(head.prefix_gru.weight_hh_l0), b_hh=None, A=f(head.rank_proj.weight), rank_bias=None, act=act,
+        B=f(head.low_rank_lm_head.weight), prior=prior_np, alphas=alphas, betas=betas, forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(step.static_rest_scores).reshape(-1), rid.reshape(-1),
+                              rsc.reshape(-1), rsec.reshape(-1))
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["max_score_err"] < 2e-2, res
+    step.close()
