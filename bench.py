@@ -48,6 +48,8 @@ def parse_args():
     ap.add_argument("--workload", default="qwen3_8b_m16", choices=["qwen3_8b_m16", "qwen3_4b_m16", "qwen3_8b_m512"])
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0: enough for > 512 MB)")
     ap.add_argument("--also-m512", action=argparse.BooleanOptionalAction, default=True)
+    ap.add_argument("--also-draft-step", action=argparse.BooleanOptionalAction, default=True,
+                    help="add the whole draft block (target LM head + first argmax + DeLS rollout, one graph)")
     ap.add_argument("--also-fp8", action=argparse.BooleanOptionalAction, default=True,
                     help="add the fp8 variant (e4m3 A and B with per-channel scales) of the workload's shape")
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
@@ -344,6 +346,69 @@ def bench_fp8(pkg, name, args, dev, torch):
                                   / 1e9 / HBM_PEAK_GBS}}
 
 
+
+def bench_draft_step(pkg, args, dev, torch):
+    """One whole draft block as one graph: batch 8, block 16 unshifted (k_draft 15: one
+    plain argmax + 14 DeLS steps), target LM head W [151936, 4096] bf16 ~ N(0, 0.02),
+    local head hidden 1024 (embeddings 1024, rank 256, silu), per-position alpha/beta
+    U[0, 0.6], the Zipf log-prior; hidden states ~ N(0, 1).
+
+    Algorithmic bytes: the LM head (W once, hidden, base logits written) + the
+    first-position argmax + per DeLS step the low-rank head, rank projection,
+    base rows and prior, and per GRU step W_hh and the input-table rows."""
+    B, k, d, V, E, G, r = 8, 15, 4096, 151936, 1024, 1024, 256
+    steps = k - 1
+    head = pkg.synth.SyntheticLocalHead(V, E, G, r, act="silu", device=dev, seed=3)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    W = (torch.randn(V, d, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    x0 = pkg.synth.config_inputs("qwen3_8b_m16")
+    prior = x0.prior.to(dev)
+    ab = torch.rand(2, steps, generator=g, device=dev) * 0.6
+    step = pkg.DeLSDraftStep(local_head=head, lm_head_weight=W, batch_size=B, k_draft=k, vocab_size=V,
+                             alpha_values=ab[0].tolist(), beta_values=ab[1].tolist(), baseline_logits=prior,
+                             device=dev)
+    hiddens = [torch.randn(B, k, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(3)]
+    for i in range(3):
+        step(hiddens[i])
+    torch.cuda.synchronize(dev)
+    n = 20
+    cur = torch.cuda.current_stream(dev)
+
+    def timed(fn):
+        best = None
+        for _ in range(3):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize(dev)
+            e0.record(cur)
+            for i in range(n):
+                fn(i)
+            e1.record(cur)
+            torch.cuda.synchronize(dev)
+            ms = e0.elapsed_time(e1) / n
+            best = ms if best is None else min(best, ms)
+        return best * 1e3
+
+    def block(i):
+        step.static_hidden.copy_(hiddens[i % 3])
+        step.replay()
+
+    us_block = timed(block)
+    us_gemm = timed(lambda i: torch.mm(hiddens[i % 3].view(B * k, d), W.t(), out=step.static_base.view(B * k, V)))
+    us_rollout = timed(lambda i: step.runner.replay())
+    gemm_bytes = 2 * V * d + 2 * B * k * d + 2 * B * k * V
+    step_bytes = 2 * V * r + 2 * r * G + 2 * B * V + 2 * V + 12 * B      # low-rank head, A, base rows, prior, outputs
+    gru_bytes = 2 * 3 * G * G + 2 * B * 3 * G + 4 * B * G                  # W_hh, input-table rows, state
+    total = gemm_bytes + 2 * B * V + steps * step_bytes + steps * gru_bytes
+    step.close()
+    return {"workload": "draft block: batch 8, block 16 (k_draft 15), d 4096, V 151936, local head G 1024 r 256",
+            "us_per_block": us_block, "draft_tokens_per_s": B * k / (us_block * 1e-6),
+            "us_lm_head_gemm": us_gemm, "us_rollout_14_steps": us_rollout,
+            "algorithmic_bytes": total, "GBs": total / (us_block * 1e-6) / 1e9,
+            "hbm_frac": total / (us_block * 1e-6) / 1e9 / HBM_PEAK_GBS}
+
+
 def cpu_baseline(name, x0, seconds):
     """The oracle on full calls of the workload, repeated for about `seconds`."""
     import numpy as np
@@ -469,6 +534,11 @@ def main():
             out["m512"]["argmax_algorithmic_bytes"] = r512["argmax_bytes"]
         except Exception as e:  # informative record only
             out["m512"] = {"error": repr(e)}
+    if args.also_draft_step and args.workload != "qwen3_8b_m512":
+        try:
+            out["draft_step"] = bench_draft_step(pkg, args, dev, torch)
+        except Exception as e:  # informative record only
+            out["draft_step"] = {"error": repr(e)}
     if args.also_fp8 and args.workload != "qwen3_8b_m512":
         try:
             out["fp8"] = bench_fp8(pkg, args.workload, args, dev, torch)

@@ -103,3 +103,29 @@ def config_inputs(name: str, *, seed: int = 0, base_dtype: Optional[torch.dtype]
         bd = base_dtype or torch.bfloat16
         return lowrank_inputs(512, per_position=True, base_dtype=bd, prior_dtype=bd, seed=seed, **QWEN3_8B)
     raise KeyError(name)
+
+
+class SyntheticLocalHead(torch.nn.Module):
+    """A DeLS local head of the reference's architecture (code/dels.py:186-192:
+    embedding, one-layer GRU without bias, rank projection, low-rank LM head)
+    with seeded random bf16 weights drawn on the device: the attributes
+    DeLSGraphRunner reads.  Weights ~ N(0, std), embeddings ~ N(0, 1)."""
+
+    def __init__(self, V: int, E: int, G: int, r: int, *, act: str = "silu", device="cuda", seed: int = 0,
+                 std: float = 0.02):
+        super().__init__()
+        dev = torch.device(device)
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        kw = dict(device=dev, dtype=torch.bfloat16)
+        self.embed_tokens = torch.nn.Embedding(V, E, **kw)
+        self.prefix_gru = torch.nn.GRU(E, G, num_layers=1, batch_first=True, bias=False, **kw)
+        self.rank_proj = torch.nn.Linear(G, r, bias=False, **kw)
+        self.low_rank_lm_head = torch.nn.Linear(r, V, bias=False, **kw)
+        self.rank_activation = act
+        with torch.no_grad():
+            self.embed_tokens.weight.copy_(torch.randn(V, E, generator=g, device=dev))
+            self.prefix_gru.weight_ih_l0.copy_(torch.randn(3 * G, E, generator=g, device=dev) * std)
+            self.prefix_gru.weight_hh_l0.copy_(torch.randn(3 * G, G, generator=g, device=dev) * std)
+            self.rank_proj.weight.copy_(torch.randn(r, G, generator=g, device=dev) * std)
+            self.low_rank_lm_head.weight.copy_(torch.randn(V, r, generator=g, device=dev) * std)
