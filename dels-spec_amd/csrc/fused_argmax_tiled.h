@@ -17,22 +17,31 @@
 // of a tie), and the base logits it needs are four runs of four consecutive
 // elements of one row.
 //
-// Workgroup: 8 waves, 2 per SIMD.  Wave w keeps the rank operand of its 32
-// rows in VGPRs for the whole kernel (r/16 K steps x 16 bytes per lane); a
-// workgroup covers 256 rows and a contiguous chunk of 32-column vocabulary
-// tiles, one tile per pipeline stage.  A stage's B tile is two consecutive
-// 16-row block rows of the MFMA-16 layout -- one contiguous run of HBM -- and
-// is copied HBM -> LDS with direct-to-LDS loads (global_load_lds_dwordx4, no
-// VGPR staging) that gather it into K-step-major MFMA-32 operand order,
-// together with each wave's base-logit tile (laid out so that the epilogue
-// reads it lane-contiguously) and the prior slice.
-// NBUF stage buffers (as many as fit in 160 KiB of LDS, up to 4) keep NBUF-1
-// stages of loads in flight; each wave waits for its own loads of the stage
-// with an explicit vmcnt count (every wave issues the same number of loads
-// per stage) and a barrier then publishes the stage to all waves.  The
-// buffers are distinct LDS objects named statically in an NBUF-way unrolled
-// loop, so the compiler can tell the reads of one buffer from the loads in
-// flight into the others and adds no waits of its own.
+// Workgroup: kWaves = 8 waves, 2 per SIMD.  Wave w keeps the rank operand of
+// its kRowBlocks = 1 block of 32 rows in VGPRs for the whole kernel (r/16 K
+// steps x 16 bytes per lane); a workgroup covers 256 rows and a contiguous
+// chunk of 32-column vocabulary tiles, one tile per pipeline stage.  (The code
+// also runs 4 waves of two 32-row blocks each, one wave per SIMD, so that
+// every B operand read from LDS feeds two MFMAs: measured 20 % slower, a
+// single wave per SIMD cannot cover its own LDS and DMA issue.)  A stage's B
+// tile is two consecutive 16-row block rows of the MFMA-16 layout -- one
+// contiguous run of HBM -- and is copied HBM -> LDS with direct-to-LDS loads
+// (global_load_lds_dwordx4, no VGPR staging) that gather it into
+// K-step-major MFMA-32 operand order, together with each wave's base-logit
+// tile (laid out so that the epilogue reads it lane-contiguously) and the
+// prior slice.  NBUF stage buffers (as many as fit in 160 KiB of LDS, up to 4)
+// keep NBUF-1 stages of loads in flight; each wave waits for its own loads of
+// the stage with an explicit vmcnt count (every wave issues the same number
+// of loads per stage) and a barrier then publishes the stage to all waves.
+// The buffers are distinct LDS objects named statically in an NBUF-way
+// unrolled loop, so the compiler can tell the reads of one buffer from the
+// loads in flight into the others and adds no waits of its own.
+//
+// The combine + argmax of stage st-1 (the epilogue) runs between the MFMAs of
+// stage st: its accumulators and base/prior values are held in registers
+// (the latter read from the stage buffer during st-1's own contraction), so
+// the matrix core does not idle while a wave combines, and a stage buffer is
+// free for new loads as soon as its contraction is done.
 //
 // Workgroups sharing a vocabulary chunk (the row groups) have linear ids that
 // differ by a multiple of 8, so they run on the same XCD and the second read of
@@ -71,14 +80,16 @@ namespace tiled {
 
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kRowsPerWave = 32;
+constexpr int kRowBlocks = 1;                         // 32-row MFMA blocks per wave
+constexpr int kRowsPerWave = 32 * kRowBlocks;
 constexpr int kRowsPerWG = kWaves * kRowsPerWave;
 constexpr int kTileCols = 32;
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kPriorBytesPerWave = 256;
+constexpr int kOperandAhead = 4;
 
 // Stage buffer parts: B tile (two 16-row block rows of KS 1 KiB blocks), each
-// wave's base tile (32 rows x 32 columns) and each wave's prior slice.
+// wave's base tile (its rows x 32 columns) and each wave's prior slice.
 template <int KS>
 constexpr int b_bytes() { return 2 * KS * 1024; }
 template <typename BaseT>
@@ -95,7 +106,7 @@ constexpr int num_buffers() {
 // Direct-to-LDS load instructions one wave issues per stage.
 template <int KS, typename BaseT, bool PRIOR>
 constexpr int loads_per_stage() {
-    return (2 * KS) / kWaves + (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0);
+    return (2 * KS) / kWaves + kRowBlocks * (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0);
 }
 
 // Wait until at most N of this wave's vector-memory operations are
@@ -112,30 +123,22 @@ __device__ __forceinline__ void stage_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Value `hi` (0: low half, 1: high half) of a packed pair of 16-bit values, widened.
 template <typename T>
-__device__ __forceinline__ void cvt4(const char* p, float (&o)[4]) {
-    if constexpr (sizeof(T) == 4) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(p);
-        o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
+__device__ __forceinline__ float half_at(uint32_t w, int hi) {
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
     } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
-        const uint32_t w[2] = {v.x, v.y};
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            if constexpr (std::is_same<T, bf16_t>::value) {
-                o[2 * i] = bf16_bits_to_f32(w[i] & 0xffffu);
-                o[2 * i + 1] = bf16_bits_to_f32(w[i] >> 16);
-            } else {
-                _Float16 h0, h1;
-                const uint16_t b0 = (uint16_t)(w[i] & 0xffffu), b1 = (uint16_t)(w[i] >> 16);
-                __builtin_memcpy(&h0, &b0, 2);
-                __builtin_memcpy(&h1, &b1, 2);
-                o[2 * i] = (float)h0;
-                o[2 * i + 1] = (float)h1;
-            }
-        }
+        const uint16_t b = (uint16_t)(hi ? (w >> 16) : (w & 0xffffu));
+        _Float16 x;
+        __builtin_memcpy(&x, &b, 2);
+        return (float)x;
     }
 }
+
+// -inf as a 16-bit value of type T.
+template <typename T>
+constexpr uint32_t half_neg_inf() { return std::is_same<T, bf16_t>::value ? 0xff80u : 0xfc00u; }
 
 }  // namespace tiled
 
@@ -146,12 +149,21 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     constexpr int kSteps = 2 * KS;                       // 16-deep K steps
     constexpr int kB = b_bytes<KS>();
     constexpr int kBaseW = base_bytes_per_wave<BaseT>();
+    constexpr int kBaseRB = kBaseW / kRowBlocks;         // base bytes of one row block
     constexpr bool kPrior = !is_no_prior<PriorT>::value;
     constexpr int NBUF = num_buffers<KS, BaseT>();
     constexpr int P = NBUF - 1;                          // stages in flight
     constexpr int E = loads_per_stage<KS, BaseT, kPrior>();
+    constexpr int nb = kSteps / kWaves;                  // B blocks per wave and stage
+    constexpr int nbase = sizeof(BaseT) == 4 ? 4 : 2;    // base loads per row block
+    constexpr int kWB = sizeof(BaseT) == 4 ? 16 : 8;     // words of one row block's base values
+    constexpr int kWP = sizeof(PriorT) == 4 ? 16 : 8;    // words of the prior values
+    constexpr int kSlots = kSteps * kRowBlocks;          // MFMAs per stage
+    constexpr int kCands = 16 * kRowBlocks;              // epilogue candidates per stage
+    constexpr int kAhead = kOperandAhead;                // B operand reads in flight per wave
     static_assert(NBUF >= 2, "stage does not fit twice in LDS");
     static_assert((2 * KS) % kWaves == 0, "B blocks per stage must split over the waves");
+    static_assert(E <= 31, "vmcnt holds the loads of two stages");
 
     struct __attribute__((aligned(1024))) Stage {
         char b[kB];
@@ -164,8 +176,8 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     __shared__ std::conditional_t<(NBUF > 3), Stage, NoStage> lds3;
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int rl = lane & 31;       // row of this lane within the wave's 32
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar control
+    const int rl = lane & 31;       // row of this lane within a 32-row block
     const int h = lane >> 5;        // K half of the operands / vocabulary quad of the results
     const int mw = blockIdx.y * kRowsPerWG + wave * kRowsPerWave;   // first row of this wave
     const bool wave_active = mw < a.M;
@@ -177,25 +189,36 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     const int nst = (int)(((int64_t)(blockIdx.x + 1) * a.ntiles) / gridDim.x) - T0;
     auto tile_of = [&](int st) { return T0 + st; };
 
-    // Rank operand of the wave's rows, resident for the whole kernel.
-    const int mrow = min(mw + rl, a.M - 1);
-    bf16x8 ra[kSteps];
-    {
+    // Rank operand of the wave's rows, resident for the whole kernel; rows past
+    // M repeat row M-1 (their results are not written).
+    bf16x8 ra[kRowBlocks][kSteps];
+    float al[kRowBlocks], be[kRowBlocks], best[kRowBlocks];
+    int bidx[kRowBlocks];
+    bool use_prior[kRowBlocks];
+    uint32_t row_off[kRowBlocks];   // byte offset of the lane's base row (M * ldbase * size < 2^31)
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+        const int mrow = min(mw + 32 * rb + rl, a.M - 1);
         const uint16_t* rp = a.rank + (int64_t)mrow * a.ldrank + h * 8;
 #pragma unroll
-        for (int s = 0; s < kSteps; ++s) ra[s] = load_bf16x8(rp + s * 16);
+        for (int s = 0; s < kSteps; ++s) ra[rb][s] = load_bf16x8(rp + s * 16);
+        al[rb] = a.alpha[(int64_t)mrow * a.alpha_stride];
+        be[rb] = a.beta[(int64_t)mrow * a.beta_stride];
+        use_prior[rb] = kPrior && be[rb] != 0.f;
+        best[rb] = -__builtin_inff();
+        bidx[rb] = INT_MAX;
+        row_off[rb] = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
     }
-    const float al = a.alpha[(int64_t)mrow * a.alpha_stride];
-    const float be = a.beta[(int64_t)mrow * a.beta_stride];
-    const bool use_prior = kPrior && be != 0.f;
-    float best = -__builtin_inff();
-    int bidx = INT_MAX;
+    // Wait for the rank (and alpha/beta) loads here, before any direct-to-LDS
+    // load is issued.  The compiler's wait insertion does not see those asm
+    // loads and joins the state before the stage loop into every iteration:
+    // with these loads still pending there it would wait for them -- that is,
+    // for every stage load in flight -- before each MFMA of every stage.
+    __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));   // vmcnt(0); expcnt and lgkmcnt left free
 
     const char* Bg = reinterpret_cast<const char*>(a.B);
     const char* baseg = static_cast<const char*>(a.base);
     const char* priorg = static_cast<const char*>(a.prior);
-    // byte offset of this lane's base row (the host keeps M * ldbase * size below 2^31)
-    const uint32_t row_off = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
 
     // Direct-to-LDS loads of stage `st` into buffer S: exactly E instructions
     // per wave.  Addresses past the data are clamped to valid memory; their
@@ -209,11 +232,9 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     const uint32_t b_lane = ((lane & 15) + 16 * h) * 16;
     const uint32_t b_hi = ((lane >> 4) & 1) ? (uint32_t)KS * 1024 : 0u;
     // Load `piece` (0 <= piece < E) of stage `st` into buffer S: pieces 0..nb-1
-    // are B blocks, then the base-logit loads, then the prior slice.  `piece` is
-    // a constant wherever this is called (unrolled loops), so the chain of
-    // tests folds away.
-    constexpr int nb = kSteps / kWaves;
-    constexpr int nbase = sizeof(BaseT) == 4 ? 4 : 2;
+    // are B blocks, then the base-logit loads of each row block, then the prior
+    // slice.  `piece` is a constant wherever this is called (unrolled loops), so
+    // the chain of tests folds away.
     auto issue_piece = [&](Stage& S, int st, int piece) {
         const int T = tile_of(st);
         const int vs = T * kTileCols;
@@ -224,16 +245,17 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
             const char* bt = Bg + (int64_t)rb0 * KS * 1024;
             const int step = wave * nb + piece;                  // K step of this load
             dma16(bt, b_lane + (two ? b_hi : 0u) + (step >> 1) * 1024 + (step & 1) * 512, S.b + step * 1024);
-        } else if (piece < nb + nbase) {
-            const int g = piece - nb;
+        } else if (piece < nb + kRowBlocks * nbase) {
+            const int rb = (piece - nb) / nbase, g = (piece - nb) % nbase;
+            char* dst = S.base[wave] + rb * kBaseRB + g * 1024;
             if constexpr (sizeof(BaseT) == 4) {
                 // load g: lane L -> row L%32, 4-column chunk 2g + L/32
                 const int v = min(vs + 4 * (2 * g + h), a.V - 4);
-                dma16(baseg, row_off + (uint32_t)v * 4u, S.base[wave] + g * 1024);
+                dma16(baseg, row_off[rb] + (uint32_t)v * 4u, dst);
             } else {
                 // load g: lane L -> row L%32, 8-column chunk 2g + L/32
                 const int v = min(vs + 8 * (2 * g + h), a.V - 8);
-                dma16(baseg, row_off + (uint32_t)v * 2u, S.base[wave] + g * 1024);
+                dma16(baseg, row_off[rb] + (uint32_t)v * 2u, dst);
             }
         } else if constexpr (kPrior) {
             if constexpr (sizeof(PriorT) == 4) {
@@ -250,83 +272,147 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
         for (int piece = 0; piece < E; ++piece) issue_piece(S, st, piece);
     };
 
-    // Epilogue operands of one stage: base[g][q] and prior[g][q] of column
-    // 8g + 4h + q.  (No load in flight targets this buffer until the next
-    // barrier, so they are read from LDS right where they are used.)
-    auto read_epilogue = [&](const Stage& S, int g, float (&b4)[4], float (&p4)[4]) {
-        if constexpr (sizeof(BaseT) == 4)
-            cvt4<BaseT>(S.base[wave] + g * 1024 + lane * 16, b4);
-        else
-            cvt4<BaseT>(S.base[wave] + (g >> 1) * 1024 + (rl + 32 * (g & 1)) * 16 + h * 8, b4);
-        if constexpr (kPrior)
-            cvt4<PriorT>(S.prior[wave] + (8 * g + 4 * h) * (int)sizeof(PriorT), p4);
-        else
-            p4[0] = p4[1] = p4[2] = p4[3] = 0.f;
+    // Epilogue operands of one stage in registers: per row block the base
+    // values of the lane's 16 columns 8g + 4h + q (candidate j = 4g + q; fp32
+    // words, or 16-bit pairs with j in word j/2), and the prior values of the
+    // same columns.  Columns past V carry a -inf base, which never wins.
+    struct EpiRegs {
+        uint32_t b[kRowBlocks][kWB];
+        uint32_t p[kWP];
+    };
+    constexpr uint32_t kNegInf = sizeof(BaseT) == 4 ? 0xff800000u : half_neg_inf<BaseT>();
+    // Group g (candidates 4g .. 4g+3) of row block rb of stage st from S; the
+    // prior group with the last row block (the last reader of the old values).
+    auto load_epi_group = [&](const Stage& S, int st, int rb, int g, EpiRegs& e) {
+        const int vs = tile_of(st) * kTileCols;
+        const int v = vs + 8 * g + 4 * h;   // column of candidate 4g
+        const bool partial = vs + kTileCols > a.V;   // only the last tile of the vocabulary
+        if constexpr (sizeof(BaseT) == 4) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(S.base[wave] + rb * kBaseRB + g * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) e.b[rb][4 * g + q] = (partial && v + q >= a.V) ? kNegInf : w[q];
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2*>(S.base[wave] + rb * kBaseRB + (g >> 1) * 1024 +
+                                                            (rl + 32 * (g & 1)) * 16 + h * 8);
+            uint32_t w0 = w.x, w1 = w.y;
+            if (partial) {
+                w0 = v < a.V ? w0 : ((w0 & 0xffff0000u) | kNegInf);
+                w0 = v + 1 < a.V ? w0 : ((w0 & 0xffffu) | (kNegInf << 16));
+                w1 = v + 2 < a.V ? w1 : ((w1 & 0xffff0000u) | kNegInf);
+                w1 = v + 3 < a.V ? w1 : ((w1 & 0xffffu) | (kNegInf << 16));
+            }
+            e.b[rb][2 * g] = w0;
+            e.b[rb][2 * g + 1] = w1;
+        }
+        if constexpr (kPrior) {
+            if (rb == kRowBlocks - 1) {
+                const char* pp = S.prior[wave] + (8 * g + 4 * h) * (int)sizeof(PriorT);
+                if constexpr (sizeof(PriorT) == 4) {
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(pp);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) e.p[4 * g + q] = w[q];
+                } else {
+                    const uint2 w = *reinterpret_cast<const uint2*>(pp);
+                    e.p[2 * g] = w.x;
+                    e.p[2 * g + 1] = w.y;
+                }
+            }
+        }
+    };
+    auto word_to_base = [&](uint32_t w, int j) -> float {
+        if constexpr (sizeof(BaseT) == 4) return __uint_as_float(w);
+        else return half_at<BaseT>(w, j & 1);
+    };
+    auto word_to_prior = [&](uint32_t w, int j) -> float {
+        if constexpr (sizeof(PriorT) == 4) return __uint_as_float(w);
+        else return half_at<PriorT>(w, j & 1);
+    };
+    // Candidate j of row block rb of stage stp.
+    // The empty volatile asm statements pin the candidate's work to its place
+    // between the MFMAs: pure arithmetic is otherwise free to be gathered
+    // after the last MFMA of the stage, which is where the compiler puts it.
+    auto epi_one = [&](const f32x16 (&accp)[kRowBlocks], const EpiRegs& e, int stp, int rb, int j) {
+        float av = accp[rb][j];
+        uint32_t bw = e.b[rb][sizeof(BaseT) == 4 ? j : (j >> 1)];
+        asm volatile("" : "+v"(av), "+v"(bw));
+        float sc = __builtin_fmaf(av, al[rb], word_to_base(bw, j));
+        if constexpr (kPrior) {
+            uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
+            asm volatile("" : "+v"(pw));
+            const float scp = __builtin_fmaf(-be[rb], word_to_prior(pw, j), sc);
+            sc = use_prior[rb] ? scp : sc;
+        }
+        // candidates arrive in increasing index order: strict ">" keeps the lowest index
+        const bool take = sc > best[rb];
+        best[rb] = take ? sc : best[rb];
+        bidx[rb] = take ? stp * 16 + j : bidx[rb];
+        asm volatile("" : "+v"(best[rb]), "+v"(bidx[rb]));
     };
 
-    // Contraction of one stage (one accumulation chain, operands read two steps
-    // ahead) and the fused combine + running argmax.  The running index is kept
-    // as a wave-uniform candidate slot st*16 + c (c = 4g + q), decoded at the end.
-    // `next` / `nst_next`: the buffer and stage whose loads are spread over this
-    // contraction (one piece every kSteps/E steps), so that they pass through
-    // the address unit while the matrix cores work (nst_next < 0: none).
-    auto consume_stage = [&](const Stage& S, int st, Stage& next, int st_next) {
-        f32x16 acc;
+    // Contraction of stage st from S (one accumulation chain per row block,
+    // operands read kAhead steps ahead), with three kinds of work spread between
+    // its MFMAs: the epilogue of the previous stage (accp, ep, stp), the reads
+    // of stage st's epilogue operands into ep_next (group by group, each after
+    // the same group of ep is done), and the loads of stage st_next into next.
+    auto contract = [&](const Stage& S, int st, Stage& next, int st_next, f32x16 (&acc)[kRowBlocks],
+                        const f32x16 (&accp)[kRowBlocks], const EpiRegs& ep, int stp, EpiRegs& ep_next) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        for (int rb = 0; rb < kRowBlocks; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[rb][i] = 0.f;
         const char* ap = S.b + lane * 16;
         auto opnd = [&](int s) { return *reinterpret_cast<const bf16x8*>(ap + s * 1024); };
         const bool issue = st_next >= 0;
-        // The scheduling barriers pin the order read(s+2), mma(s): the read
-        // latency hides behind two contractions instead of stalling each one.
-        bf16x8 a0 = opnd(0), a1 = opnd(1);
+        // operand ring: the read of step s + kAhead is issued before the MFMAs of step s
+        bf16x8 opq[kAhead];
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) opq[i] = opnd(i < kSteps ? i : 0);
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) {
-            const bf16x8 nx = s + 2 < kSteps ? opnd(s + 2) : a1;
-            __builtin_amdgcn_sched_barrier(0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, ra[s], acc, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
+            const bf16x8 a0 = opq[s % kAhead];
+            if (s + kAhead < kSteps) opq[s % kAhead] = opnd(s + kAhead);
 #pragma unroll
-            for (int piece = 0; piece < E; ++piece)
-                if (s == piece * kSteps / E && issue) issue_piece(next, st_next, piece);
-            a0 = a1;
-            a1 = nx;
-        }
-        const int vs = tile_of(st) * kTileCols;
-        auto epilogue = [&](auto masked) {
+            for (int rb = 0; rb < kRowBlocks; ++rb) {
+                const int slot = s * kRowBlocks + rb;
+                __builtin_amdgcn_sched_barrier(0);
+                acc[rb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, ra[rb][s], acc[rb], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                // candidates c in [slot * kCands / kSlots, (slot + 1) * kCands / kSlots): row block c / 16, j = c % 16
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float b4[4], p4[4];
-                read_epilogue(S, g, b4, p4);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    float sc = __builtin_fmaf(acc[4 * g + q], al, b4[q]);
-                    const float scp = __builtin_fmaf(-be, p4[q], sc);
-                    sc = use_prior ? scp : sc;
-                    if constexpr (decltype(masked)::value)
-                        sc = vs + 8 * g + 4 * h + q < a.V ? sc : -__builtin_inff();
-                    // candidates arrive in increasing index order: strict ">" keeps the lowest index
-                    const bool take = sc > best;
-                    best = take ? sc : best;
-                    bidx = take ? st * 16 + 4 * g + q : bidx;
+                for (int c = slot * kCands / kSlots; c < (slot + 1) * kCands / kSlots; ++c) {
+                    epi_one(accp, ep, stp, c >> 4, c & 15);
+                    if ((c & 3) == 3) load_epi_group(S, st, c >> 4, (c & 15) >> 2, ep_next);
                 }
+#pragma unroll
+                for (int piece = 0; piece < E; ++piece)
+                    if (slot == piece * kSlots / E && issue) issue_piece(next, st_next, piece);
             }
-        };
-        if (vs + kTileCols > a.V)   // only the last tile of the vocabulary is partial
-            epilogue(std::true_type{});
-        else
-            epilogue(std::false_type{});
+        }
     };
 
     // Pipeline: stages 0..P-1 are issued up front; at stage st each wave waits
     // for its own loads of st (the younger stages may stay in flight), the
     // barrier publishes st, the freed buffer of st-1 takes stage st+P, and st
-    // is contracted.
+    // is contracted while st-1 is combined.
     auto buf = [&](int i) -> Stage& {
         if constexpr (NBUF > 3) { if (i == 3) return lds3; }
         if constexpr (NBUF > 2) { if (i == 2) return lds2; }
         return i == 1 ? lds1 : lds0;
     };
+    f32x16 acc_prev[kRowBlocks];
+    EpiRegs ep_prev, ep_cur;
+    int st_prev = 0;
+    // no stage before stage 0: a -inf base makes its epilogue a no-op
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc_prev[rb][i] = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWB; ++i) ep_prev.b[rb][i] = sizeof(BaseT) == 4 ? kNegInf : kNegInf * 0x10001u;
+    }
+#pragma unroll
+    for (int i = 0; i < kWP; ++i) ep_prev.p[i] = 0u;
+
 #pragma unroll
     for (int i = 0; i < P; ++i)
         if (i < nst) issue_stage(buf(i), i);
@@ -348,30 +434,43 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
                 }
                 const int st_next = st + P < nst ? st + P : -1;
                 if (wave_active) {
-                    consume_stage(buf(u), st, buf((u + P) % NBUF), st_next);
+                    f32x16 acc[kRowBlocks];
+                    contract(buf(u), st, buf((u + P) % NBUF), st_next, acc, acc_prev, ep_prev, st_prev, ep_cur);
+#pragma unroll
+                    for (int rb = 0; rb < kRowBlocks; ++rb) acc_prev[rb] = acc[rb];
+                    ep_prev = ep_cur;
+                    st_prev = st;
                 } else if (st_next >= 0) {
                     issue_stage(buf((u + P) % NBUF), st_next);
                 }
             }
         }
     }
+    if (wave_active && nst > 0) {
+        // the epilogue of the last stage
+#pragma unroll
+        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, st_prev, c >> 4, c & 15);
+    }
 
-    // Decode the candidate slot into the vocabulary index, then merge the two
-    // vocabulary quads of each row (lanes l and l^32).
-    {
-        if (bidx != INT_MAX) {
-            const int st = bidx >> 4, c = bidx & 15;
-            bidx = tile_of(st) * kTileCols + 8 * (c >> 2) + 4 * h + (c & 3);
+    // Decode the candidate slot st*16 + j into the vocabulary index, then merge
+    // the two vocabulary quads of each row (lanes l and l^32).
+#pragma unroll
+    for (int rb = 0; rb < kRowBlocks; ++rb) {
+        float bv = best[rb];
+        int bi = bidx[rb];
+        if (bi != INT_MAX) {
+            const int st = bi >> 4, c = bi & 15;
+            bi = tile_of(st) * kTileCols + 8 * (c >> 2) + 4 * h + (c & 3);
         }
-        const float ov = __shfl_xor(best, 32, 64);
-        const int oi = __shfl_xor(bidx, 32, 64);
-        if (argmax_better(ov, oi, best, bidx)) {
-            best = ov;
-            bidx = oi;
+        const float ov = __shfl_xor(bv, 32, 64);
+        const int oi = __shfl_xor(bi, 32, 64);
+        if (argmax_better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
         }
-        const int m = mw + rl;
+        const int m = mw + 32 * rb + rl;
         if (h == 0 && m < a.M) {
-            const unsigned long long key = bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx);
+            const unsigned long long key = bi == INT_MAX ? 0ull : pack_argmax(bv, (uint32_t)bi);
             a.part[(int64_t)blockIdx.x * a.M + m] = key;
         }
     }
