@@ -25,7 +25,11 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // ---- skinny GEMM: rank projection and fused GRU step -----------------------
 
+// Rows from which the rank projection uses the LDS-tiled kernel.
+constexpr int kRankTiledMinRows = 64;
+
 struct SkinnyPlan {
+    bool tiled;        // rank projection by the LDS-tiled 64 x 64 kernel (many rows)
     int wm, wn;        // 16x16 MFMA sub-tiles per wave (rows x cols)
     int m_wg, n_wg;    // workgroup grid (row tiles, col tiles)
     int ksplit;        // workgroups sharing one output tile along K

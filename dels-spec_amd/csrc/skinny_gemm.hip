@@ -302,6 +302,260 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Many rows (M >= 64): an LDS-tiled rank projection.
+//
+// The skinny kernel reads its operands straight from global memory, each
+// wave's load touching 32 B of 32 different rows; at M = 512 that re-reads h
+// and A sixteen times over through the caches and is latency bound (16 us at
+// the Qwen3-8B shape).  Here a workgroup owns a 64 x 64 output tile and a
+// range of 64-deep K chunks.  Each chunk's 64 x 64 slices of h and of A are
+// copied HBM -> LDS with direct-to-LDS loads of whole 128-byte lines (eight
+// rows per instruction), into a ring of kRgStages chunk buffers, so that
+// kRgStages - 1 chunks of loads are in flight; its four waves each contract a
+// 32 x 32 quadrant with v_mfma_f32_32x32x16_bf16 from LDS.  The 16-byte
+// pieces of a row are stored XOR-swizzled by row (piece q of row r in slot
+// q ^ (r % 8)), so the operand reads of 32 rows spread over all LDS banks.
+// K is split over 8 workgroups per tile so that the grid covers the device;
+// their fp32 partials go to the workspace with plain stores and a second
+// kernel sums them in split order (deterministic) and runs the epilogue.
+// Needs K % 64 == 0 and r % 8 == 0 (the plan falls back to the skinny kernel otherwise).
+// ---------------------------------------------------------------------------
+
+constexpr int kRgTile = 64;                 // output tile edge
+constexpr int kRgChunk = 64;                // K per LDS chunk
+constexpr int kRgStages = 4;                // chunk buffers in the LDS ring (two workgroups fit a CU)
+
+// Direct-to-LDS loads per wave and chunk: h (8 instructions of 8 rows) and W
+// (row-major: 8 like h; MFMA-16 blocks: 8 of 1 KiB; e4m3 blocks: 16 of 256 B),
+// spread over the 4 waves.
+template <int WMODE>
+constexpr int rg_loads_per_wave() { return (8 + (WMODE == W_PACKED_E4M3 ? 16 : 8)) / 4; }
+
+template <int N>
+__device__ __forceinline__ void rg_wait_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);   // vmcnt(N), lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int WMODE>
+__global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
+    constexpr int L = rg_loads_per_wave<WMODE>();
+    constexpr int kWBytes = WMODE == W_PACKED_E4M3 ? 4096 : 8192;
+    struct __attribute__((aligned(1024))) Chunk {
+        char h[8192];        // 64 rows x 128 B, pieces swizzled
+        char w[kWBytes];     // row-major: as h; blocked: 8 blocks (4 row blocks x 2 K blocks)
+    };
+    __shared__ Chunk ring[kRgStages];
+    // the output tile (pitch 68 floats) reuses the ring once the K loop is done
+    static_assert(sizeof(Chunk) * kRgStages >= kRgTile * (kRgTile + 4) * sizeof(float), "ring too small");
+    float* red = reinterpret_cast<float*>(&ring[0]);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;    // quadrant of this wave
+    // Grid (ksplit, column tiles, row tiles): consecutive workgroups -- which
+    // the dispatcher deals round-robin over the 8 XCDs -- take different K
+    // splits, so with ksplit = 8 each XCD works on one K slice of h and A and
+    // its L2 fetches that slice once instead of all of h and A.
+    const int z = blockIdx.x;
+    const int n0 = blockIdx.y * kRgTile, m0 = blockIdx.z * kRgTile;
+    const int nchunks = a.K / kRgChunk;
+    const int cps = (nchunks + a.ksplit - 1) / a.ksplit;
+    const int c0 = z * cps, c1 = min(nchunks, c0 + cps);
+    const int nch = max(0, c1 - c0);
+
+    // Load instruction g (0 .. 4L-1) of chunk c into slot S: g < 8 is h
+    // (rows 8g .. 8g+7), the rest W.  Rows past M or r repeat the last row
+    // (their results are never stored).
+    // Byte offsets are taken from the tile's first row (or row block), so they
+    // stay far below 2^32 whatever the matrix size.
+    const int prow = lane >> 3, piece = lane & 7;
+    const uint16_t* hbase = a.x + (int64_t)m0 * a.ldx;
+    const int nbw = (n0 >> 4);   // first row block of W (blocked layouts)
+    const uint16_t* wbase = WMODE == W_ROWMAJOR ? a.w + (int64_t)n0 * a.ldw
+                          : a.w + (int64_t)nbw * a.ksteps * (WMODE == W_PACKED ? 512 : 256);
+    const int nbl = (a.wrows + 15) / 16 - 1 - nbw;   // last row block, relative to nbw
+    auto issue = [&](int c, Chunk& S, int g) {
+        const int k0 = c * kRgChunk;
+        if (g < 8) {
+            const int row = 8 * g + prow;
+            const int mr = min(m0 + row, a.M - 1) - m0;
+            const int q = piece ^ (row & 7);   // the piece this lane fetches: slot `piece` holds piece q
+            dma16(hbase, (uint32_t)(mr * a.ldx + k0 + 8 * q) * 2u, S.h + g * 1024);
+        } else if constexpr (WMODE == W_ROWMAJOR) {
+            const int row = 8 * (g - 8) + prow;
+            const int nr = min(n0 + row, a.wrows - 1) - n0;
+            const int q = piece ^ (row & 7);
+            dma16(wbase, (uint32_t)(nr * a.ldw + k0 + 8 * q) * 2u, S.w + (g - 8) * 1024);
+        } else if constexpr (WMODE == W_PACKED) {
+            const int b = g - 8;                      // block (row block b/2, K block b%2)
+            const int blk = min(b >> 1, nbl) * a.ksteps + (k0 >> 5) + (b & 1);
+            dma16(wbase, (uint32_t)(blk * 1024 + lane * 16), S.w + b * 1024);
+        } else {
+            const int b = (g - 8) >> 1, half = (g - 8) & 1;   // 512-byte e4m3 blocks, two 256-byte halves
+            const int blk = min(b >> 1, nbl) * a.ksteps + (k0 >> 5) + (b & 1);
+            dma4(wbase, (uint32_t)(blk * 512 + half * 256 + lane * 4), S.w + b * 512 + half * 256);
+        }
+    };
+    auto issue_chunk = [&](int c, Chunk& S) {
+#pragma unroll
+        for (int j = 0; j < L; ++j) issue(c, S, wave * L + j);
+    };
+
+    // v_mfma_f32_32x32x16_bf16 with the h quadrant as the A operand (lane l:
+    // row l%32, K 8*(l/32) .. +7 of the step) and the W quadrant as the B
+    // operand: lane l ends with columns n = l%32 and rows 8*(i/4) + 4*(l/32) + i%4.
+    const int rl = lane & 31, kh = lane >> 5;
+    auto contract = [&](const Chunk& S, f32x16& acc) {
+        const int hr = 32 * wm + rl, wr = 32 * wn + rl;
+#pragma unroll
+        for (int s = 0; s < kRgChunk / 16; ++s) {
+            const int q = 2 * s + kh;   // 16-byte piece of the row
+            const bf16x8 av = *reinterpret_cast<const bf16x8*>(S.h + hr * 128 + ((q ^ (hr & 7)) << 4));
+            bf16x8 bv;
+            if constexpr (WMODE == W_ROWMAJOR) {
+                bv = *reinterpret_cast<const bf16x8*>(S.w + wr * 128 + ((q ^ (wr & 7)) << 4));
+            } else if constexpr (WMODE == W_PACKED) {
+                const int b = (wr >> 4) * 2 + (s >> 1);
+                bv = *reinterpret_cast<const bf16x8*>(S.w + b * 1024 + ((wr & 15) + 16 * (2 * (s & 1) + kh)) * 16);
+            } else {
+                const int b = (wr >> 4) * 2 + (s >> 1);
+                const u32x2 e = *reinterpret_cast<const u32x2*>(S.w + b * 512 + ((wr & 15) + 16 * (2 * (s & 1) + kh)) * 8);
+                bv = __builtin_bit_cast(bf16x8, widen_e4m3x8(e[0], e[1]));
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+        }
+    };
+
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+    // Ring: chunks 0 .. kRgStages-2 issued up front; at chunk i each wave waits
+    // for its own loads of i (younger chunks stay in flight), the barrier
+    // publishes i and frees the slot of i-1, which takes chunk i + kRgStages-1.
+    constexpr int P = kRgStages - 1;
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+        if (i < nch) issue_chunk(c0 + i, ring[i]);
+    for (int i0 = 0; i0 < nch; i0 += kRgStages) {
+#pragma unroll
+        for (int u = 0; u < kRgStages; ++u) {
+            const int i = i0 + u;
+            if (i >= nch) break;
+            const int younger = min(P - 1, nch - 1 - i);   // chunks issued after i, in flight
+            static_assert(kRgStages <= 4, "the wait switch covers up to 2 younger chunks");
+            switch (younger) {
+                case 2: rg_wait_barrier<2 * L>(); break;
+                case 1: rg_wait_barrier<1 * L>(); break;
+                default: rg_wait_barrier<0>(); break;
+            }
+            if (i + P < nch) issue_chunk(c0 + i + P, ring[(u + P) % kRgStages]);
+            contract(ring[u], acc);
+        }
+    }
+
+    // the quadrant into the tile red[m][n] (pitch 68 floats)
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int m = 32 * wm + 8 * (i >> 2) + 4 * kh + (i & 3);
+        red[m * (kRgTile + 4) + 32 * wn + rl] = acc[i];
+    }
+    __syncthreads();
+
+    if (a.ksplit > 1) {
+        // Split K: the fp32 partial tile goes to partial[z][M][ncols] with plain
+        // stores; rank_splitk_epilogue_kernel, launched next on the same
+        // stream, sums the splits in order (the kernel boundary makes every
+        // partial visible to it) and runs the epilogue.
+        float* mine = a.partial + (int64_t)z * a.M * a.ncols;
+        for (int e = tid; e < kRgTile * kRgTile / 4; e += 256) {
+            const int mm = e >> 4, nn = 4 * (e & 15);
+            const int m = m0 + mm, n = n0 + nn;
+            if (m >= a.M || n >= a.ncols) continue;
+            const float* src = &red[mm * (kRgTile + 4) + nn];
+            // ncols is a multiple of 8, so the 4 columns are in range
+            *reinterpret_cast<f32x4*>(mine + (int64_t)m * a.ncols + n) = f32x4{src[0], src[1], src[2], src[3]};
+        }
+        return;
+    }
+
+    // Epilogue: rank = bf16(act(bf16(v * col_scale + bias))), two columns per store.
+    {
+#pragma clang fp contract(off)
+        for (int e = tid; e < kRgTile * kRgTile / 2; e += 256) {
+            const int mm = e >> 5, nn = 2 * (e & 31);
+            const int m = m0 + mm, n = n0 + nn;
+            if (m >= a.M || n >= a.ncols) continue;
+            uint32_t packed = 0;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                float v = red[mm * (kRgTile + 4) + nn + t];
+                if (a.col_scale) v = v * a.col_scale[n + t];
+                if (a.bias) v = v + bf16_bits_to_f32(a.bias[n + t]);
+                v = round_bf16(v);
+                if (a.act == 1) v = round_bf16(silu_f32(v));
+                packed |= (uint32_t)f32_to_bf16_bits(v) << (16 * t);
+            }
+            // ncols is a multiple of 8, so both columns are in range
+            uint16_t* dst = a.out + (int64_t)m * a.ldout + n;
+            if ((((uintptr_t)a.out & 3) | (uintptr_t)(a.ldout & 1)) == 0) {
+                *reinterpret_cast<uint32_t*>(dst) = packed;
+            } else {   // an output view without 4-byte rows: element stores
+                dst[0] = (uint16_t)packed;
+                dst[1] = (uint16_t)(packed >> 16);
+            }
+        }
+    }
+}
+
+// Sum of the split-K partials of the LDS-tiled rank projection, in split
+// order, and the rank epilogue; one thread per 4 output columns (16-byte loads).
+__global__ __launch_bounds__(256) void rank_splitk_epilogue_kernel(SkinnyKArgs a) {
+#pragma clang fp contract(off)
+    const int64_t quads = (int64_t)a.M * a.ncols / 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= quads) return;
+    const int m = (int)(t / (a.ncols / 4)), n = (int)(t % (a.ncols / 4)) * 4;
+    const int64_t off = (int64_t)m * a.ncols + n;
+    const int64_t zs = (int64_t)a.M * a.ncols;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    for (int z0 = 0; z0 < a.ksplit; z0 += 8) {
+        f32x4 pv[8];
+#pragma unroll
+        for (int zz = 0; zz < 8; ++zz)   // unconditional loads (clamped split), masked in the sum
+            pv[zz] = *reinterpret_cast<const f32x4*>(a.partial + min(z0 + zz, a.ksplit - 1) * zs + off);
+#pragma unroll
+        for (int zz = 0; zz < 8; ++zz) {
+            const bool ok = z0 + zz < a.ksplit;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = ok ? v[q] + pv[zz][q] : v[q];
+        }
+    }
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float x = v[q];
+        if (a.col_scale) x = x * a.col_scale[n + q];
+        if (a.bias) x = x + bf16_bits_to_f32(a.bias[n + q]);
+        x = round_bf16(x);
+        if (a.act == 1) x = round_bf16(silu_f32(x));
+        packed[q >> 1] |= (uint32_t)f32_to_bf16_bits(x) << (16 * (q & 1));
+    }
+    uint16_t* dst = a.out + (int64_t)m * a.ldout + n;
+    if ((((uintptr_t)a.out & 7) | (uintptr_t)(a.ldout & 3)) == 0) {
+        *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
+    } else {   // an output view without 8-byte rows: element stores
+        dst[0] = (uint16_t)packed[0]; dst[1] = (uint16_t)(packed[0] >> 16);
+        dst[2] = (uint16_t)packed[1]; dst[3] = (uint16_t)(packed[1] >> 16);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 
@@ -309,6 +563,23 @@ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
     SkinnyPlan p{};
+    if (!gru && rows >= kRankTiledMinRows && K % kRgChunk == 0 && cols % 8 == 0) {
+        // LDS-tiled kernel: 64 x 64 tiles, K split so that about 256 workgroups run.
+        p.tiled = true;
+        p.wm = p.wn = 0;
+        p.m_wg = (int)cdiv(rows, kRgTile);
+        p.n_wg = (int)cdiv(cols, kRgTile);
+        p.ksteps = (int)cdiv(K, 32);
+        const int nchunks = (int)(K / kRgChunk);
+        const int tiles = p.m_wg * p.n_wg;
+        // 8 K splits (one K slice per XCD) unless the tiles alone fill the
+        // device; never below two chunks per split.
+        int ks = tiles >= 512 ? 1 : 8;
+        ks = std::min(ks, std::max(1, nchunks / 2));
+        p.ksplit = std::min(ks, kMaxKSplit);
+        p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * rows * cols * sizeof(float) : 0;
+        return p;
+    }
     if (gru) {
         p.wn = 3;
         p.wm = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
@@ -367,6 +638,20 @@ hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, si
     ka.out = a.rank; ka.ldout = a.ldrank;
     fill_ws(ka, p, ws, data_off);
     const int wmode = a.a_scale ? W_PACKED_E4M3 : (a.a_packed ? W_PACKED : W_ROWMAJOR);
+    if (p.tiled) {
+        const dim3 grid(p.ksplit, p.n_wg, p.m_wg);
+        if (wmode == W_PACKED)
+            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED>), grid, dim3(256), 0, s, ka);
+        else if (wmode == W_PACKED_E4M3)
+            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED_E4M3>), grid, dim3(256), 0, s, ka);
+        else
+            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_ROWMAJOR>), grid, dim3(256), 0, s, ka);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || p.ksplit == 1) return e;
+        const int64_t quads = (int64_t)ka.M * ka.ncols / 4;
+        hipLaunchKernelGGL(rank_splitk_epilogue_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ka);
+        return hipGetLastError();
+    }
     if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, wmode, s);
     return launch_skinny<2, 2, EPI_RANK>(ka, p, wmode, s);
 }

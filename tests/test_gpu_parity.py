@@ -343,7 +343,8 @@ def test_packed_gru_equals_rowmajor(pkg, dev):
 
 @pytest.mark.parametrize("M,d,r,act,bias", [(16, 4096, 512, "identity", False), (16, 2560, 256, "silu", False),
                                             (5, 1024, 64, "silu", True), (40, 512, 136, "identity", True),
-                                            (512, 4096, 512, "silu", False)])
+                                            (512, 4096, 512, "silu", False), (100, 1000, 136, "identity", True),
+                                            (64, 4096, 256, "silu", True)])
 def test_rank_proj(pkg, dev, M, d, r, act, bias):
     print(f"case rank_proj M={M} d={d} r={r} act={act} bias={bias}", flush=True)
     g = torch.Generator().manual_seed(M + d + r)
@@ -369,6 +370,39 @@ def test_rank_proj(pkg, dev, M, d, r, act, bias):
         raise AssertionError(f"{int(bad.sum())} rank elements out of tolerance, e.g. (row, col, got, ref, mag) "
                              f"{detail}")
     assert (bf16_ulps(got, ref) > 0).mean() < 2e-3
+
+
+def test_rank_proj_tiled_packed_equals_rowmajor(pkg, dev):
+    """Many rows (the LDS-tiled rank GEMM): the MFMA-16 blocked A gives the same
+    rank as row-major A (same kernel, same K order), ragged rows, columns and K."""
+    M, d, r = 300, 1000, 200
+    g = torch.Generator().manual_seed(21)
+    h = torch.randn(M, d, generator=g).to(torch.bfloat16).to(dev)
+    A = (torch.randn(r, d, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    b = (torch.randn(r, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    row = pkg.rank_proj(h, A, b, "silu").clone()
+    pk = pkg.rank_proj(h, pkg.pack_operand(A), b, "silu")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(pk, row, rtol=0, atol=0)
+    ref = oracle.rank_proj(f(h), f(A), f(b), "silu")
+    assert (bf16_ulps(f(row), ref) > 0).mean() < 2e-3
+
+
+def test_rank_proj_tiled_into_unaligned_view(pkg, dev):
+    """The LDS-tiled rank GEMM (split K + epilogue kernel) writing into an
+    output view whose rows are not 4- or 8-byte aligned gives the same rank as
+    into a contiguous tensor."""
+    M, d, r = 128, 1024, 64
+    g = torch.Generator().manual_seed(5)
+    h = torch.randn(M, d, generator=g).to(torch.bfloat16).to(dev)
+    A = (torch.randn(r, d, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    want = pkg.rank_proj(h, A, None, "silu").clone()
+    big = torch.zeros(M, r + 3, dtype=torch.bfloat16, device=dev)
+    view = big[:, 1:r + 1]                     # row stride r + 3 (odd), start offset 2 bytes
+    got = pkg.rank_proj(h, A, None, "silu", out=view)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got, want, rtol=0, atol=0)
+    assert big[:, 0].abs().sum().item() == 0 and big[:, r + 1:].abs().sum().item() == 0
 
 
 # ------------------------------------------------------------------ end-to-end draft step
