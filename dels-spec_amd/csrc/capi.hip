@@ -14,6 +14,12 @@
 
 namespace dels {
 
+// The rollout's rank projection reads only G x r weights: below this hidden
+// size two launches (rank GEMM with K whole, then the argmax GEMV) finish
+// sooner than the one-launch decode step, whose device-wide rank hand-off
+// costs a fixed few microseconds.
+constexpr int kRolloutDecodeMinG = 2048;
+
 static thread_local std::string g_last_error;
 
 static int fail(int code, const char* fmt, ...) {
@@ -258,7 +264,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
 
-        if (decode_eligible(B, G, r, ra.a_packed, aa.b_packed)) {
+        if (G >= kRolloutDecodeMinG && decode_eligible(B, G, r, ra.a_packed, aa.b_packed)) {
             // rank projection and argmax in one launch
             e = launch_lowrank_decode(ra, aa, ws, L.decode_off, s);
             if (e != hipSuccess) return hip_fail(e, "fused decode step launch");

@@ -594,9 +594,13 @@ SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
     p.n_wg = (int)cdiv(cols, gru ? 16 : 16 * p.wn);
     p.ksteps = (int)cdiv(K, 32);
     const int tiles = p.m_wg * p.n_wg;
-    // Aim for about 256 workgroups with at least one K step per wave.
+    // Aim for about 256 workgroups with at least one K step per wave -- but
+    // keep K whole while a wave has at most 16 K steps: the split-K hand-off
+    // (device-coherent partials, a counter, the last workgroup's reads) costs
+    // more than the longer K loop at these sizes.
     int ks = (int)std::max<int64_t>(1, 256 / std::max(tiles, 1));
     ks = std::min(ks, std::max(1, p.ksteps / 4));
+    if (p.ksteps <= 64) ks = 1;
     p.ksplit = std::min(ks, kMaxKSplit);
     p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * tiles * p.wm * p.wn * 256 * sizeof(float) : 0;
     return p;
