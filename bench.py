@@ -38,6 +38,7 @@ sys.path.insert(0, REPO_DIR)
 METRIC = "argmax rows/s + % HBM/MFMA roofline, Qwen3-8B low-rank LM head, M=16 & 512"
 HBM_PEAK_GBS = 8000.0
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+FP8_MFMA_PEAK_TFLOPS = 5000.0
 
 
 def parse_args():
@@ -334,16 +335,22 @@ def bench_fp8(pkg, name, args, dev, torch):
     sb = x0.base.element_size()
     sp = x0.prior.element_size()
     nbytes = r * V + r * d + 2 * M * d + sb * M * V + sp * V + 4 * (V + r) + 12 * M
+    arg_bytes = nbytes - r * d - 2 * M * d - 4 * r + 2 * M * r
+    flops, arg_flops = 2 * M * r * (d + V), 2 * M * r * V
+    tiled = M >= 64
     return {"workload": name, "M": M, "d": d, "r": r, "V": V, "weights": "e4m3 (A K32, B K128 blocks)",
             "kernel": "lowrank_decode8_kernel" if M <= 16 else
-            "skinny_gemm_kernel (e4m3 A) + fused_argmax_gemv8_kernel",
+            ("rank_gemm_tiled_kernel (e4m3 A) + quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel"
+             if tiled else "skinny_gemm_kernel (e4m3 A) + fused_argmax_gemv8_kernel"),
             "rows_per_s": M / (us * 1e-6), "us_per_step": us, "algorithmic_bytes": nbytes,
             "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "mfma_frac": flops / (us * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
             "sets": nsets,
-            "fused_argmax_only": {"kernel": "fused_argmax_gemv8_kernel", "us_per_launch": us_arg,
-                                  "algorithmic_bytes": nbytes - r * d - 2 * M * d - 4 * r + 2 * M * r,
-                                  "hbm_frac": (nbytes - r * d - 2 * M * d - 4 * r + 2 * M * r) / (us_arg * 1e-6)
-                                  / 1e9 / HBM_PEAK_GBS}}
+            "fused_argmax_only": {"kernel": "quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel + "
+                                            "argmax_partials_reduce_kernel" if tiled else "fused_argmax_gemv8_kernel",
+                                  "us_per_launch": us_arg, "algorithmic_bytes": arg_bytes,
+                                  "hbm_frac": arg_bytes / (us_arg * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                  "mfma_frac": arg_flops / (us_arg * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS}}
 
 
 
@@ -544,6 +551,11 @@ def main():
             out["fp8"] = bench_fp8(pkg, args.workload, args, dev, torch)
         except Exception as e:  # informative record only
             out["fp8"] = {"error": repr(e)}
+        if args.also_m512:
+            try:
+                out["fp8_m512"] = bench_fp8(pkg, "qwen3_8b_m512", args, dev, torch)
+            except Exception as e:  # informative record only
+                out["fp8_m512"] = {"error": repr(e)}
     if args.cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.workload, x0, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -103,7 +103,8 @@ static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) 
     L.rank_off = kCtrlBytes;
     L.part_off = L.rank_off + align256((size_t)M * r * 2);
     L.argmax_off = L.part_off + skinny_data_bytes(L.plan);
-    L.decode_off = L.argmax_off + align256(argmax_data_bytes(M, r, V));
+    // room for the bf16 argmax and for the e4m3 one (which also keeps the quantised rank)
+    L.decode_off = L.argmax_off + align256(std::max(argmax_data_bytes(M, r, V), argmax_fp8_data_bytes(M, r, V)));
     L.total = L.decode_off + decode_data_bytes(M, d, r);
     return L;
 }
@@ -495,7 +496,9 @@ int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t col
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 pack launch");
 }
 
-size_t dels_fused_argmax_fp8_ws_bytes(int64_t, int64_t, int64_t) { return kCtrlBytes; }
+size_t dels_fused_argmax_fp8_ws_bytes(int64_t M, int64_t r, int64_t V) {
+    return kCtrlBytes + align256(argmax_fp8_data_bytes(M, r, V));
+}
 
 static void fill_argmax_fp8(ArgmaxArgs& a, const void* Bq, const float* b_scale, const void* base, int64_t ldbase,
                             int base_dtype, const void* prior, int prior_dtype, const float* alpha,
@@ -529,7 +532,7 @@ int dels_fused_argmax_fp8(const void* rank, int64_t ldrank, const void* Bq, cons
     a.rank = static_cast<const uint16_t*>(rank); a.ldrank = ldrank;
     fill_argmax_fp8(a, Bq, b_scale, base, ldbase, base_dtype, prior, prior_dtype, alpha, alpha_stride, beta,
                     beta_stride, M, r, V, out_ids, out_score, ld_out);
-    hipError_t e = launch_fused_argmax_fp8(a, ws, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_fused_argmax_fp8(a, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
 }
 
@@ -582,7 +585,7 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
     }
     e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
     if (e != hipSuccess) return hip_fail(e, "fp8 rank projection launch");
-    e = launch_fused_argmax_fp8(a, ws, s);
+    e = launch_fused_argmax_fp8(a, ws, L.argmax_off, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
 }
 

@@ -90,7 +90,8 @@ hipError_t launch_argmax_rows(const void* x, int64_t ldx, int dtype, int M, int 
 
 // fp8 argmax (b_scale set): r in {128, 256, 512}, any M up to kMaxKeyRows.
 bool argmax_fp8_supported(int64_t M, int64_t r);
-hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, hipStream_t s);
+size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V);
+hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
 // ---- fused decode step: rank projection + argmax in one launch (M <= 16) --------
 

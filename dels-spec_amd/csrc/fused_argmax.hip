@@ -6,6 +6,7 @@
 #include "fused_argmax_fp8.h"
 #include "fused_argmax_gemv.h"
 #include "fused_argmax_tiled.h"
+#include "fused_argmax_tiled8.h"
 #include "lowrank_decode.h"
 
 namespace dels {
@@ -80,6 +81,12 @@ __global__ __launch_bounds__(256) void argmax_partials_reduce_kernel(const unsig
 }  // namespace
 
 size_t argmax_data_bytes(int64_t M, int64_t /*r*/, int64_t V) { return tiled_part_bytes(M, V); }
+
+// The e4m3 argmax also keeps the rank quantised per row (tiled kernel).
+size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V) {
+    if (M < kTiledMinRows) return 0;
+    return align256(tiled_part_bytes(M, V)) + align256((size_t)M * r) + align256((size_t)M * 4);
+}
 
 bool argmax_supported(int64_t M, int64_t r, int64_t /*V*/) { return r >= 8 && r <= 512 && M <= kMaxKeyRows; }
 
@@ -238,9 +245,90 @@ bool argmax_fp8_supported(int64_t M, int64_t r) {
     return (r == 128 || r == 256 || r == 512) && M >= 0 && M <= kMaxKeyRows;
 }
 
-hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, hipStream_t s) {
+namespace {
+
+// Per-row e4m3 quantisation of the rank for the tiled kernel, with the fp8
+// GEMV's rule: amax = max |rank[m, :]|, inv = 448 / amax, q = e4m3(rank * inv),
+// scale = amax / 448 (1 and zeros for an all-zero row).  One wave per row, r <= 512.
+__global__ __launch_bounds__(256) void quantize_rank_e4m3_kernel(const uint16_t* __restrict__ rank, int64_t ldrank,
+                                                                 int M, int r, uint8_t* __restrict__ rank_q,
+                                                                 float* __restrict__ rank_scale) {
+#pragma clang fp contract(off)
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (m >= M) return;
+    const uint16_t* row = rank + (int64_t)m * ldrank;
+    const bool ok = 8 * lane < r;   // lane: values 8 * lane .. + 7
+    const u32x4 v = ok ? *reinterpret_cast<const u32x4*>(row + 8 * lane) : u32x4{0u, 0u, 0u, 0u};
+    float amax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(v[e] << 16)));
+        amax = __builtin_fmaxf(amax, __builtin_fabsf(__uint_as_float(v[e] & 0xffff0000u)));
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off, 64));
+    const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+    uint32_t w[2];
+#pragma unroll
+    for (int hw = 0; hw < 2; ++hw) {
+        const uint32_t x0 = v[2 * hw], x1 = v[2 * hw + 1];
+        w[hw] = f32_to_e4m3(__uint_as_float(x0 << 16) * inv) |
+                (f32_to_e4m3(__uint_as_float(x0 & 0xffff0000u) * inv) << 8) |
+                (f32_to_e4m3(__uint_as_float(x1 << 16) * inv) << 16) |
+                (f32_to_e4m3(__uint_as_float(x1 & 0xffff0000u) * inv) << 24);
+    }
+    if (ok) *reinterpret_cast<u32x2*>(rank_q + (int64_t)m * r + 8 * lane) = u32x2{w[0], w[1]};
+    if (lane == 0) rank_scale[m] = amax > 0.f ? amax / kE4M3Max : 1.f;
+}
+
+}  // namespace
+
+// The e4m3 tiled kernel: the bf16 tiled kernel's conditions, r = 256 or 512
+// (B loads per stage split evenly over 8 waves) and 4-byte aligned B scales.
+static bool tiled8_eligible(const ArgmaxArgs& a) {
+    if (!(a.r == 256 || a.r == 512) || (reinterpret_cast<uintptr_t>(a.b_scale) & 3) != 0) return false;
+    ArgmaxArgs t = a;
+    t.b_packed = true;
+    return tiled_eligible(t);
+}
+
+hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s) {
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     char* w = static_cast<char*>(ws);
+    if (tiled8_eligible(a)) {
+        int gx = 1, gy = 1;
+        tiled_grid(a.M, a.V, kPlanCUs, &gx, &gy);
+        TiledKArgs ka{};
+        ka.rank = a.rank; ka.ldrank = a.ldrank;
+        ka.B = a.B;
+        ka.b_scale = a.b_scale;
+        ka.base = a.base; ka.ldbase = a.ldbase;
+        ka.prior = a.prior;
+        ka.alpha = a.alpha; ka.alpha_stride = a.alpha_stride;
+        ka.beta = a.beta; ka.beta_stride = a.beta_stride;
+        ka.M = a.M; ka.V = a.V;
+        ka.nblk16 = (a.V + 15) / 16;
+        ka.ntiles = (a.V + tiled::kTileCols - 1) / tiled::kTileCols;
+        ka.part = reinterpret_cast<unsigned long long*>(w + data_off);
+        // the rank, quantised per row to e4m3, after the partials
+        uint8_t* rank_q = reinterpret_cast<uint8_t*>(w + data_off + align256(tiled_part_bytes(a.M, a.V)));
+        float* rank_scale = reinterpret_cast<float*>(reinterpret_cast<char*>(rank_q) + align256((size_t)a.M * a.r));
+        hipLaunchKernelGGL(quantize_rank_e4m3_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, a.rank, a.ldrank, a.M,
+                           a.r, rank_q, rank_scale);
+        ka.rank_q = rank_q;
+        ka.ldrank = a.r;
+        ka.rank_scale = rank_scale;
+        const int ks8 = a.r / 128;
+        hipError_t e;
+        if (a.base_dtype == 1) e = launch_tiled8_bf16(ka, ks8, pk, gx, gy, s);
+        else if (a.base_dtype == 2) e = launch_tiled8_f16(ka, ks8, pk, gx, gy, s);
+        else e = launch_tiled8_f32(ka, ks8, pk, gx, gy, s);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, ka.part, gx,
+                           a.M, a.V, a.out_ids, a.out_score, a.ld_out);
+        return hipGetLastError();
+    }
     ArgmaxKArgs ka{};
     ka.rank = a.rank; ka.ldrank = a.ldrank;
     ka.B = a.B; ka.ldb = 0;

@@ -65,7 +65,10 @@ namespace dels {
 
 struct TiledKArgs {
     const uint16_t* rank; int64_t ldrank;
-    const uint16_t* B;          // MFMA-16 blocks, r a multiple of 32
+    const uint16_t* B;          // MFMA-16 blocks, r a multiple of 32 (e4m3 kernel: K128 blocks)
+    const float* b_scale;       // e4m3 kernel only: per-row scale of B
+    const uint8_t* rank_q;      // e4m3 kernel only: the rank quantised per row [M][ldrank bytes]
+    const float* rank_scale;    // e4m3 kernel only: its per-row scale [M]
     const void* base; int64_t ldbase;
     const void* prior;          // nullptr when there is no prior
     const float* alpha; int64_t alpha_stride;

@@ -1,0 +1,392 @@
+// fp8 (e4m3) variant of the MFMA-tiled fused combine + vocabulary argmax, for
+// many rows (M >= 64): B in e4m3 K128 blocks with per-row fp32 scales, the
+// rank quantised per row to e4m3 in the prologue, v_mfma_scale_f32_32x32x64_f8f6f4.
+//
+// Per row m and vocabulary row v (the fp8 GEMV's semantics):
+//     dot      = f32(f32(acc[m, v] * sR[m]) * sB[v])      acc: the e4m3 x e4m3 contraction
+//     s[m, v]  = dot * alpha_m + base[m, v] - beta_m * prior[v]   (two fused multiply-adds)
+// and per row the lowest v attaining the maximum.  The rank quantisation is
+// the GEMV's: amax = max |rank[m, :]|, inv = 448 / amax, q = e4m3(rank * inv),
+// sR = amax / 448 (1 and zeros for an all-zero row).
+//
+// The structure is the bf16 tiled kernel's (fused_argmax_tiled.h): 8 waves of
+// 32 rows, 256 rows and a contiguous chunk of 32-column vocabulary tiles per
+// workgroup, one tile per pipeline stage, stage buffers filled by
+// direct-to-LDS loads, the combine of stage st-1 interleaved between the MFMAs
+// of stage st.  What differs is the operand order: the 32x32x64 MFMA takes, for
+// lane l, 32 consecutive K bytes 32*(l/32) .. of row l%32 of a 64-deep step.
+// The K128 blocks (16 rows x 128 K, lane L: row L%16, K 32*(L/16) .. +31 as two
+// 16-byte halves) hold exactly those runs, so the B tile is gathered into
+// step-major LDS blocks of 2 KiB ([half][lane][16 B]) by the loads themselves;
+// every operand read is then two contiguous KiB.  The rank operand uses the
+// same K order (bytes in natural order within each 32-byte run), so the MFMA,
+// which pairs A and B by (lane group, byte), computes the plain dot product.
+#pragma once
+
+#include "fp8.h"
+#include "fused_argmax_tiled.h"
+
+namespace dels {
+
+namespace tiled8 {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kTileCols = 32;
+constexpr int kLdsBytes = 160 * 1024;
+constexpr int kSideBytes = 256;   // per wave and stage: the prior slice, the B scales
+constexpr int kOperandAhead = 2;
+
+// 64-deep K steps of r = 128 * KS8.
+template <int KS8>
+constexpr int steps() { return 2 * KS8; }
+template <int KS8>
+constexpr int b_bytes() { return steps<KS8>() * 2048; }
+template <typename BaseT>
+constexpr int base_bytes_per_wave() { return 32 * kTileCols * (int)sizeof(BaseT); }
+template <int KS8, typename BaseT>
+constexpr int stage_bytes() {
+    return b_bytes<KS8>() + kWaves * (base_bytes_per_wave<BaseT>() + 2 * kSideBytes);
+}
+template <int KS8, typename BaseT>
+constexpr int num_buffers() {
+    constexpr int n = kLdsBytes / stage_bytes<KS8, BaseT>();
+    return n > 4 ? 4 : n;
+}
+// Direct-to-LDS loads per wave and stage: B (two per step, split over the
+// waves), base, prior, B scales.
+template <int KS8, typename BaseT, bool PRIOR>
+constexpr int loads_per_stage() {
+    return 2 * steps<KS8>() / kWaves + (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0) + 1;
+}
+
+__device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8& b, f32x16 acc) {
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
+}
+
+}  // namespace tiled8
+
+template <int KS8, typename BaseT, typename PriorT>
+__global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(TiledKArgs a) {
+#pragma clang fp contract(off)
+    using namespace tiled8;
+    constexpr int kSteps = steps<KS8>();
+    constexpr int kB = b_bytes<KS8>();
+    constexpr int kBaseW = base_bytes_per_wave<BaseT>();
+    constexpr bool kPrior = !is_no_prior<PriorT>::value;
+    constexpr int NBUF = num_buffers<KS8, BaseT>();
+    constexpr int P = NBUF - 1;                          // stages in flight
+    constexpr int E = loads_per_stage<KS8, BaseT, kPrior>();
+    constexpr int nb = 2 * kSteps / kWaves;              // B loads per wave and stage
+    constexpr int nbase = sizeof(BaseT) == 4 ? 4 : 2;
+    constexpr int kWB = sizeof(BaseT) == 4 ? 16 : 8;
+    constexpr int kWP = sizeof(PriorT) == 4 ? 16 : 8;
+    constexpr int kCands = 16;
+    constexpr int kAhead = kOperandAhead;
+    static_assert(NBUF >= 2, "stage does not fit twice in LDS");
+    static_assert((2 * kSteps) % kWaves == 0, "B loads per stage must split over the waves");
+    static_assert(2 * E <= 63, "vmcnt holds the loads of two stages");
+
+    struct __attribute__((aligned(1024))) Stage {
+        char b[kB];                              // [step][half][lane][16 B]
+        char base[kWaves][kBaseW];
+        char prior[kWaves][kSideBytes];
+        char bsc[kWaves][kSideBytes];            // fp32 scales of the tile's 32 vocabulary rows
+    };
+    struct NoStage {};
+    __shared__ Stage lds0, lds1;
+    __shared__ std::conditional_t<(NBUF > 2), Stage, NoStage> lds2;
+    __shared__ std::conditional_t<(NBUF > 3), Stage, NoStage> lds3;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rl = lane & 31;
+    const int h = lane >> 5;
+    const int mw = blockIdx.y * 256 + wave * 32;
+    const bool wave_active = mw < a.M;
+    const int T0 = (int)(((int64_t)blockIdx.x * a.ntiles) / gridDim.x);
+    const int nst = (int)(((int64_t)(blockIdx.x + 1) * a.ntiles) / gridDim.x) - T0;
+    auto tile_of = [&](int st) { return T0 + st; };
+
+    // ---- the rank operand: this lane's row, K runs 64s + 32h .. +31, e4m3 ----
+    // (quantised by quantize_rank_e4m3_kernel: rank_q [M][ldrank] bytes, sR [M])
+    const int mrow = min(mw + rl, a.M - 1);
+    const uint8_t* rqp = a.rank_q + (int64_t)mrow * a.ldrank + 32 * h;
+    i32x8 rq[kSteps];
+#pragma unroll
+    for (int s = 0; s < kSteps; ++s) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(rqp + 64 * s);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(rqp + 64 * s + 16);
+        rq[s] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    }
+    const float sR = a.rank_scale[mrow];
+    const float al = a.alpha[(int64_t)mrow * a.alpha_stride];
+    const float be = a.beta[(int64_t)mrow * a.beta_stride];
+    const bool use_prior = kPrior && be != 0.f;
+    float best = -__builtin_inff();
+    int bidx = INT_MAX;
+    const uint32_t row_off = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
+    // Drain the loads above before any direct-to-LDS load (see the bf16 kernel:
+    // otherwise the compiler waits for every stage load before each MFMA).
+    __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));   // vmcnt(0)
+
+    const char* Bg = reinterpret_cast<const char*>(a.B);
+    const char* baseg = static_cast<const char*>(a.base);
+    const char* priorg = static_cast<const char*>(a.prior);
+    const char* bscg = reinterpret_cast<const char*>(a.b_scale);
+
+    // B gather: load (step s, half h2) puts, in MFMA lane l, 16 bytes of the
+    // K128 block (row block 2T + (l%32)/16, K block s/2), lane (l%16) +
+    // 16*(2*(s%2) + l/32), half h2.
+    const uint32_t b_lane = (uint32_t)(lane & 15) * 16;
+    const uint32_t b_hi = ((lane >> 4) & 1) ? (uint32_t)KS8 * kFp8K128Block : 0u;
+    auto issue_piece = [&](Stage& S, int st, int piece) {
+        const int T = tile_of(st);
+        const int vs = T * kTileCols;
+        if (piece < nb) {
+            const int rb0 = min(2 * T, a.nblk16 - 1);
+            const bool two = 2 * T + 1 < a.nblk16;
+            const char* bt = Bg + (int64_t)rb0 * KS8 * kFp8K128Block;
+            const int ii = wave * nb + piece;               // (step, half) of this load
+            const int s = ii >> 1, h2 = ii & 1;
+            const uint32_t off = b_lane + (two ? b_hi : 0u) + (uint32_t)(s >> 1) * kFp8K128Block +
+                                 (uint32_t)(2 * (s & 1) + h) * 256 + (uint32_t)h2 * 1024;
+            dma16(bt, off, S.b + s * 2048 + h2 * 1024);
+        } else if (piece < nb + nbase) {
+            const int g = piece - nb;
+            char* dst = S.base[wave] + g * 1024;
+            if constexpr (sizeof(BaseT) == 4) {
+                const int v = min(vs + 4 * (2 * g + h), a.V - 4);
+                dma16(baseg, row_off + (uint32_t)v * 4u, dst);
+            } else {
+                const int v = min(vs + 8 * (2 * g + h), a.V - 8);
+                dma16(baseg, row_off + (uint32_t)v * 2u, dst);
+            }
+        } else if (piece == nb + nbase) {
+            const int v = min(vs + (lane & 31), a.V - 1);
+            dma4(bscg, (uint32_t)v * 4u, S.bsc[wave]);
+        } else if constexpr (kPrior) {
+            if constexpr (sizeof(PriorT) == 4) {
+                const int v = min(vs + (lane & 31), a.V - 1);
+                dma4(priorg, (uint32_t)v * 4u, S.prior[wave]);
+            } else {
+                const int v = min(vs + 2 * (lane & 15), a.V - 2);
+                dma4(priorg, (uint32_t)v * 2u, S.prior[wave]);
+            }
+        }
+    };
+    auto issue_stage = [&](Stage& S, int st) {
+#pragma unroll
+        for (int piece = 0; piece < E; ++piece) issue_piece(S, st, piece);
+    };
+
+    // Epilogue operands of one stage in registers (candidate j = 4g + q is the
+    // lane's column 8g + 4h + q): base, prior and B scale values; columns past
+    // V carry a -inf base.
+    struct EpiRegs {
+        uint32_t b[kWB];
+        uint32_t p[kWP];
+        float sb[16];
+    };
+    constexpr uint32_t kNegInf = sizeof(BaseT) == 4 ? 0xff800000u : tiled::half_neg_inf<BaseT>();
+    auto load_epi_group = [&](const Stage& S, int st, int g, EpiRegs& e) {
+        const int vs = tile_of(st) * kTileCols;
+        const int v = vs + 8 * g + 4 * h;
+        const bool partial = vs + kTileCols > a.V;
+        if constexpr (sizeof(BaseT) == 4) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(S.base[wave] + g * 1024 + lane * 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) e.b[4 * g + q] = (partial && v + q >= a.V) ? kNegInf : w[q];
+        } else {
+            const uint2 w = *reinterpret_cast<const uint2*>(S.base[wave] + (g >> 1) * 1024 +
+                                                            (rl + 32 * (g & 1)) * 16 + h * 8);
+            uint32_t w0 = w.x, w1 = w.y;
+            if (partial) {
+                w0 = v < a.V ? w0 : ((w0 & 0xffff0000u) | kNegInf);
+                w0 = v + 1 < a.V ? w0 : ((w0 & 0xffffu) | (kNegInf << 16));
+                w1 = v + 2 < a.V ? w1 : ((w1 & 0xffff0000u) | kNegInf);
+                w1 = v + 3 < a.V ? w1 : ((w1 & 0xffffu) | (kNegInf << 16));
+            }
+            e.b[2 * g] = w0;
+            e.b[2 * g + 1] = w1;
+        }
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(S.bsc[wave] + (8 * g + 4 * h) * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) e.sb[4 * g + q] = sv[q];
+        if constexpr (kPrior) {
+            const char* pp = S.prior[wave] + (8 * g + 4 * h) * (int)sizeof(PriorT);
+            if constexpr (sizeof(PriorT) == 4) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(pp);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) e.p[4 * g + q] = w[q];
+            } else {
+                const uint2 w = *reinterpret_cast<const uint2*>(pp);
+                e.p[2 * g] = w.x;
+                e.p[2 * g + 1] = w.y;
+            }
+        }
+    };
+    // Candidate j of stage stp; the empty volatile asm statements pin its work
+    // between the MFMAs (pure arithmetic would otherwise be gathered after the
+    // last MFMA of the stage).
+    auto epi_one = [&](const f32x16& accp, const EpiRegs& e, int stp, int j) {
+        float av = accp[j];
+        float sbv = e.sb[j];
+        uint32_t bw = e.b[sizeof(BaseT) == 4 ? j : (j >> 1)];
+        asm volatile("" : "+v"(av), "+v"(sbv), "+v"(bw));
+        float dot = av * sR;
+        dot = dot * sbv;
+        const float bv = sizeof(BaseT) == 4 ? __uint_as_float(bw) : tiled::half_at<BaseT>(bw, j & 1);
+        float sc = __builtin_fmaf(dot, al, bv);
+        if constexpr (kPrior) {
+            uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
+            asm volatile("" : "+v"(pw));
+            const float pv = sizeof(PriorT) == 4 ? __uint_as_float(pw) : tiled::half_at<PriorT>(pw, j & 1);
+            const float scp = __builtin_fmaf(-be, pv, sc);
+            sc = use_prior ? scp : sc;
+        }
+        const bool take = sc > best;   // candidates arrive in increasing index order
+        best = take ? sc : best;
+        bidx = take ? stp * 16 + j : bidx;
+        asm volatile("" : "+v"(best), "+v"(bidx));
+    };
+    constexpr int kPer = (kCands + kSteps - 1) / kSteps;   // candidates per MFMA slot
+    auto contract = [&](const Stage& S, int st, Stage& next, int st_next, const f32x16& accp, const EpiRegs& ep,
+                        int stp, EpiRegs& ep_next) {
+        f32x16 acc;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+        auto opnd = [&](int s) {
+            const u32x4 lo = *reinterpret_cast<const u32x4*>(S.b + s * 2048 + lane * 16);
+            const u32x4 hi = *reinterpret_cast<const u32x4*>(S.b + s * 2048 + 1024 + lane * 16);
+            return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2],
+                         (int)hi[3]};
+        };
+        const bool issue = st_next >= 0;
+        i32x8 opq[kAhead];
+#pragma unroll
+        for (int i = 0; i < kAhead; ++i) opq[i] = opnd(i < kSteps ? i : 0);
+#pragma unroll
+        for (int s = 0; s < kSteps; ++s) {
+            const i32x8 a0 = opq[s % kAhead];
+            if (s + kAhead < kSteps) opq[s % kAhead] = opnd(s + kAhead);
+            __builtin_amdgcn_sched_barrier(0);
+            acc = mfma_e4m3_32x32x64(a0, rq[s], acc);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = s * kPer; c < (s + 1) * kPer && c < kCands; ++c) {
+                epi_one(accp, ep, stp, c);
+                if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
+            }
+#pragma unroll
+            for (int piece = 0; piece < E; ++piece)
+                if (s == piece * kSteps / E && issue) issue_piece(next, st_next, piece);
+        }
+        // candidates not reached in the loop (fewer slots than 16 / kPer)
+#pragma unroll
+        for (int c = kSteps * kPer; c < kCands; ++c) {
+            epi_one(accp, ep, stp, c);
+            if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
+        }
+        return acc;
+    };
+
+    auto buf = [&](int i) -> Stage& {
+        if constexpr (NBUF > 3) { if (i == 3) return lds3; }
+        if constexpr (NBUF > 2) { if (i == 2) return lds2; }
+        return i == 1 ? lds1 : lds0;
+    };
+    f32x16 acc_prev;
+    EpiRegs ep_prev, ep_cur;
+    int st_prev = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        acc_prev[i] = 0.f;
+        ep_prev.sb[i] = 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kWB; ++i) ep_prev.b[i] = sizeof(BaseT) == 4 ? kNegInf : kNegInf * 0x10001u;
+#pragma unroll
+    for (int i = 0; i < kWP; ++i) ep_prev.p[i] = 0u;
+
+#pragma unroll
+    for (int i = 0; i < P; ++i)
+        if (i < nst) issue_stage(buf(i), i);
+    for (int st0 = 0; st0 < nst; st0 += NBUF) {
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) {
+            const int st = st0 + u;
+            if (st < nst) {
+                const int younger = min(P - 1, nst - 1 - st);
+                if constexpr (P >= 3) {
+                    if (younger >= 2) tiled::stage_barrier<2 * E>();
+                    else if (younger == 1) tiled::stage_barrier<E>();
+                    else tiled::stage_barrier<0>();
+                } else if constexpr (P == 2) {
+                    if (younger >= 1) tiled::stage_barrier<E>();
+                    else tiled::stage_barrier<0>();
+                } else {
+                    tiled::stage_barrier<0>();
+                }
+                const int st_next = st + P < nst ? st + P : -1;
+                if (wave_active) {
+                    acc_prev = contract(buf(u), st, buf((u + P) % NBUF), st_next, acc_prev, ep_prev, st_prev, ep_cur);
+                    ep_prev = ep_cur;
+                    st_prev = st;
+                } else if (st_next >= 0) {
+                    issue_stage(buf((u + P) % NBUF), st_next);
+                }
+            }
+        }
+    }
+    if (wave_active && nst > 0) {
+#pragma unroll
+        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, st_prev, c);
+    }
+
+    // decode the slot, merge the two column quads of the row, one key per row
+    if (bidx != INT_MAX) {
+        const int st = bidx >> 4, c = bidx & 15;
+        bidx = tile_of(st) * kTileCols + 8 * (c >> 2) + 4 * h + (c & 3);
+    }
+    const float ov = __shfl_xor(best, 32, 64);
+    const int oi = __shfl_xor(bidx, 32, 64);
+    if (argmax_better(ov, oi, best, bidx)) {
+        best = ov;
+        bidx = oi;
+    }
+    const int m = mw + rl;
+    if (h == 0 && m < a.M) {
+        const unsigned long long key = bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx);
+        a.part[(int64_t)blockIdx.x * a.M + m] = key;
+    }
+}
+
+template <int KS8, typename BaseT, typename PriorT>
+hipError_t launch_tiled8_inst(const TiledKArgs& ka, int gx, int gy, hipStream_t s) {
+    hipLaunchKernelGGL((fused_argmax_tiled8_kernel<KS8, BaseT, PriorT>), dim3(gx, gy, 1), dim3(tiled8::kThreads),
+                       0, s, ka);
+    return hipGetLastError();
+}
+
+// Dispatch over r / 128 (2 or 4) and the prior type for one base dtype.
+template <typename BaseT>
+hipError_t launch_tiled8_for_base(const TiledKArgs& ka, int ks8, int prior_kind, int gx, int gy, hipStream_t s) {
+    auto by_prior = [&](auto ks_tag) -> hipError_t {
+        constexpr int KS8 = decltype(ks_tag)::value;
+        switch (prior_kind) {
+            case 0: return launch_tiled8_inst<KS8, BaseT, no_prior_t>(ka, gx, gy, s);
+            case 1: return launch_tiled8_inst<KS8, BaseT, float>(ka, gx, gy, s);
+            case 2: return launch_tiled8_inst<KS8, BaseT, bf16_t>(ka, gx, gy, s);
+            default: return launch_tiled8_inst<KS8, BaseT, f16_t>(ka, gx, gy, s);
+        }
+    };
+    if (ks8 == 2) return by_prior(std::integral_constant<int, 2>{});
+    return by_prior(std::integral_constant<int, 4>{});
+}
+
+hipError_t launch_tiled8_f32(const TiledKArgs& ka, int ks8, int prior_kind, int gx, int gy, hipStream_t s);
+hipError_t launch_tiled8_bf16(const TiledKArgs& ka, int ks8, int prior_kind, int gx, int gy, hipStream_t s);
+hipError_t launch_tiled8_f16(const TiledKArgs& ka, int ks8, int prior_kind, int gx, int gy, hipStream_t s);
+
+}  // namespace dels

@@ -1,11 +1,16 @@
-// Instantiations of the batched (MFMA-tiled) fused argmax kernel for float base
+// Instantiations of the batched (MFMA-tiled) fused argmax kernels (bf16 and e4m3 B) for float base
 // logits (one translation unit per base dtype keeps the build parallel).
 #include "fused_argmax_tiled.h"
+#include "fused_argmax_tiled8.h"
 
 namespace dels {
 
 hipError_t launch_tiled_f32(const TiledKArgs& ka, int ksteps, int prior_kind, int gx, int gy, hipStream_t s) {
     return launch_tiled_for_base<float>(ka, ksteps, prior_kind, gx, gy, s);
+}
+
+hipError_t launch_tiled8_f32(const TiledKArgs& ka, int ks8, int prior_kind, int gx, int gy, hipStream_t s) {
+    return launch_tiled8_for_base<float>(ka, ks8, prior_kind, gx, gy, s);
 }
 
 }  // namespace dels

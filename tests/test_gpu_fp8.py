@@ -84,7 +84,8 @@ def test_pack_fp8_layout(pkg, dev, rows, cols, layout):
 
 # ------------------------------------------------------------------ in-kernel e4m3 rounding
 
-def test_rank_quantisation_is_exact_e4m3_rounding(pkg, dev):
+@pytest.mark.parametrize("r", [128, 256])   # r=128: the fp8 GEMV; r=256 (>= 64 rows): the fp8 tiled kernel
+def test_rank_quantisation_is_exact_e4m3_rounding(pkg, dev, r):
     """Each rank row holds +-448 (so its scale is exactly 1) and one probe value;
     B selects the probe column and the base masks every other vocabulary entry,
     so the returned score is the kernel's e4m3 rounding of the probe.  Probes:
@@ -101,7 +102,7 @@ def test_rank_quantisation_is_exact_e4m3_rounding(pkg, dev):
     probes = torch.from_numpy(probes).bfloat16().float().numpy()     # the rank is bf16
     probes = probes[np.abs(probes) <= 448.0]
     P = probes.size
-    r, V = 128, 4
+    V = 4
     rank = np.zeros((P, r), np.float32)
     rank[:, 0] = np.where(np.arange(P) % 2 == 0, 448.0, -448.0)
     rank[:, 1] = probes
@@ -125,6 +126,10 @@ FP8_ARGMAX_CASES = [
     (40, 256, 30000, torch.float16, None),
     (100, 512, 50000, torch.bfloat16, torch.float32),
     (1, 128, 4099, torch.float32, None),
+    # >= 64 rows, r in {256, 512}: the fp8 MFMA-tiled kernel (ragged row groups, every base dtype)
+    (300, 256, 30000, torch.bfloat16, torch.bfloat16),
+    (64, 512, 20008, torch.float32, torch.float32),
+    (512, 512, 151936, torch.bfloat16, torch.bfloat16),
 ]
 
 
