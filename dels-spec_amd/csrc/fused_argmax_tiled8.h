@@ -229,25 +229,25 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     // Candidate j of stage stp; the empty volatile asm statements pin its work
     // between the MFMAs (pure arithmetic would otherwise be gathered after the
     // last MFMA of the stage).
-    auto epi_one = [&](const f32x16& accp, const EpiRegs& e, int stp, int j) {
+    auto epi_one = [&](const f32x16& accp, const EpiRegs& e, int slot0, int j) {
         float av = accp[j];
         float sbv = e.sb[j];
-        uint32_t bw = e.b[sizeof(BaseT) == 4 ? j : (j >> 1)];
-        asm volatile("" : "+v"(av), "+v"(sbv), "+v"(bw));
+        const uint32_t bw = e.b[sizeof(BaseT) == 4 ? j : (j >> 1)];
+        float bv = sizeof(BaseT) == 4 ? __uint_as_float(bw) : tiled::half_at<BaseT>(bw, j & 1);
+        asm volatile("" : "+v"(av), "+v"(sbv), "+v"(bv));
         float dot = av * sR;
         dot = dot * sbv;
-        const float bv = sizeof(BaseT) == 4 ? __uint_as_float(bw) : tiled::half_at<BaseT>(bw, j & 1);
         float sc = __builtin_fmaf(dot, al, bv);
         if constexpr (kPrior) {
-            uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
-            asm volatile("" : "+v"(pw));
-            const float pv = sizeof(PriorT) == 4 ? __uint_as_float(pw) : tiled::half_at<PriorT>(pw, j & 1);
+            const uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
+            float pv = sizeof(PriorT) == 4 ? __uint_as_float(pw) : tiled::half_at<PriorT>(pw, j & 1);
+            asm volatile("" : "+v"(pv));
             const float scp = __builtin_fmaf(-be, pv, sc);
             sc = use_prior ? scp : sc;
         }
         const bool take = sc > best;   // candidates arrive in increasing index order
         best = take ? sc : best;
-        bidx = take ? stp * 16 + j : bidx;
+        bidx = take ? slot0 + j : bidx;   // slot0 = 16 * stage, wave-uniform
         asm volatile("" : "+v"(best), "+v"(bidx));
     };
     constexpr int kPer = (kCands + kSteps - 1) / kSteps;   // candidates per MFMA slot
@@ -263,6 +263,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
                          (int)hi[3]};
         };
         const bool issue = st_next >= 0;
+        const int slot0 = __builtin_amdgcn_readfirstlane(stp * 16);
         i32x8 opq[kAhead];
 #pragma unroll
         for (int i = 0; i < kAhead; ++i) opq[i] = opnd(i < kSteps ? i : 0);
@@ -275,7 +276,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int c = s * kPer; c < (s + 1) * kPer && c < kCands; ++c) {
-                epi_one(accp, ep, stp, c);
+                epi_one(accp, ep, slot0, c);
                 if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
             }
 #pragma unroll
@@ -285,7 +286,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
         // candidates not reached in the loop (fewer slots than 16 / kPer)
 #pragma unroll
         for (int c = kSteps * kPer; c < kCands; ++c) {
-            epi_one(accp, ep, stp, c);
+            epi_one(accp, ep, slot0, c);
             if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
         }
         return acc;
@@ -341,7 +342,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     }
     if (wave_active && nst > 0) {
 #pragma unroll
-        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, st_prev, c);
+        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, __builtin_amdgcn_readfirstlane(st_prev * 16), c);
     }
 
     // decode the slot, merge the two column quads of the row, one key per row
