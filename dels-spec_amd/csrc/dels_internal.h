@@ -11,13 +11,15 @@ namespace dels {
 // ---- workspace layout ---------------------------------------------------------
 // Every entry point uses the same control area at the start of the workspace:
 // cross-workgroup counters at [0, 32 KiB) and argmax keys at [32 KiB, 64 KiB).
-// Kernels return the control area to zero before they finish; data regions
-// (split-K partials, the rank buffer) start at kCtrlBytes and may hold anything
-// between calls.  Calls with different shapes or entry points can therefore
-// share one workspace.
+// Kernels return the control area to zero before they finish, except the last
+// 128-byte line of the counters, which holds words that persist between calls
+// (the fused decode step's launch generation); data regions (split-K partials,
+// rank words) start at kCtrlBytes and may hold anything between calls.  Calls
+// with different shapes or entry points can therefore share one workspace.
 constexpr size_t kCtrlBytes = 65536;
 constexpr size_t kCountersOff = 0;
-constexpr int kMaxCounters = 8192;
+constexpr int kMaxCounters = 8160;             // counters that kernels return to zero
+constexpr int kDecodeGenWord = 8160;           // the decode step's launch generation (persists)
 constexpr size_t kKeysOff = 32768;
 constexpr int kMaxKeyRows = 4096;
 

@@ -352,6 +352,9 @@ hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_of
 
 namespace {
 int g_decode_spin_limit = 1 << 14;
+// K slices of the in-launch rank projection: nct * slices workgroups compute
+// rank partials, the rest go straight to the argmax stream.
+constexpr int kDecodeSlices = 4;
 
 struct DecodePlan {
     int nct, nz, kpz, ksa;
@@ -360,7 +363,7 @@ struct DecodePlan {
 DecodePlan decode_plan(int64_t d, int64_t r) {
     DecodePlan p{};
     p.nct = (int)(r / 16);
-    p.nz = kDecodeWGs / std::max(p.nct, 1);
+    p.nz = std::min(kDecodeSlices, kDecodeWGs / std::max(p.nct, 1));
     p.ksa = (int)(d / 32);
     p.kpz = (p.ksa + p.nz - 1) / std::max(p.nz, 1);
     return p;
@@ -377,8 +380,7 @@ bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_pack
     if (M < 1 || M > 16 || !a_packed || !b_packed) return false;
     if (!(r == 64 || r == 128 || r == 256 || r == 512)) return false;
     if (d < 32 || d % 32 != 0) return false;
-    const DecodePlan p = decode_plan(d, r);
-    return kDecodeWGs % p.nct == 0 && (p.kpz + 3) / 4 <= kDecodeMaxJ;
+    return kDecodeWGs % decode_plan(d, r).nct == 0;
 }
 
 bool decode8_eligible(int64_t M, int64_t d, int64_t r) {
@@ -387,8 +389,9 @@ bool decode8_eligible(int64_t M, int64_t d, int64_t r) {
 
 size_t decode_data_bytes(int64_t M, int64_t d, int64_t r) {
     if (M > 16 || r % 16 != 0 || d % 32 != 0) return 0;
-    const DecodePlan p = decode_plan(d, r);
-    return align256((size_t)p.nct * p.nz * 256 * sizeof(float)) + align256((size_t)16 * r * 2);
+    // tagged partial words of every workgroup, then the tagged rank words
+    return align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)) +
+           align256((size_t)16 * (r / 2) * sizeof(unsigned long long));
 }
 
 hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, size_t data_off,
@@ -410,14 +413,14 @@ hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* 
     ka.counter = counters;                         // argmax arrivals
     ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
     ka.key_stride = 16;                            // M <= 16: one 128-byte line per row
-    k.done = counters + 1;                         // published rank tiles
-    k.tile_cnt = counters + 64;                    // per-tile split arrivals (nct <= 32)
+    k.gen = counters + kDecodeGenWord;             // launch generation (never reset)
     k.h = ra.h; k.ldh = ra.ldh;
     k.A = ra.A;
     k.bias = ra.bias; k.act = ra.act;
     k.ksa = p.ksa; k.nct = p.nct; k.nz = p.nz; k.kpz = p.kpz;
-    k.partial = reinterpret_cast<float*>(w + data_off);
-    k.rank_buf = reinterpret_cast<uint16_t*>(w + data_off + align256((size_t)p.nct * p.nz * 256 * sizeof(float)));
+    k.partial_words = reinterpret_cast<unsigned long long*>(w + data_off);
+    k.rank_words = reinterpret_cast<unsigned long long*>(
+        w + data_off + align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)));
     k.spin_limit = g_decode_spin_limit;
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     if (ra.a_scale != nullptr) {

@@ -2,26 +2,37 @@
 // projection rank = bf16(act(bf16(h . A^T + bias))) (code/kernel/dels.py:437-443)
 // followed by the fused combine + vocabulary argmax (code/kernel/dels.py:15-138).
 //
-// Two kernels back to back leave the rank projection's latency chain (operand
-// round trip, split-K reduction) on the critical path, ~7 us of a ~37 us step,
-// while HBM idles.  Here the grid is 256 workgroups (one per CU, all resident)
-// and the rank projection is split over all of them:
+// Two kernels back to back leave the rank projection's latency chain on the
+// critical path while HBM idles.  Here the grid is 256 workgroups (one per CU,
+// all resident) and the rank is handed over inside the launch:
 //   1. workgroup g computes the fp32 partial of rank column tile c = g % nct
-//      (16 columns) over K slice z = g / nct, sums its four waves in LDS and
-//      publishes the 16x16 partial with device-coherent stores;
-//   2. the workgroup that completes a tile's arrival count (a returning atomic)
-//      sums the tile's nz partials in split order -- deterministic --, applies
-//      bias, bf16 rounding and the activation, publishes the bf16 tile and bumps
-//      a global tile count;
-//   3. every workgroup puts the first two tiles of its argmax stream in flight,
-//      waits (bounded) for the tile count to reach nct, loads the full rank
-//      with device-coherent loads and runs the GEMV-argmax stream of
-//      fused_argmax_gemv.h on the prefetched tiles onwards.
-// Only returning atomics and agent-scope loads/stores cross workgroups; no
-// cache fences.  If the wait times out (the grid is not co-resident, e.g. other
-// work shares the device), the workgroup computes the whole rank itself -- slow
-// but correct -- so the kernel always terminates.  The last workgroup of the
-// argmax reduction returns every counter to zero.
+//      (16 columns, nct = r/16) over K slice z = g / nct; for z > 0 it
+//      publishes the partial as 64-bit words {tag, fp32} with device-coherent
+//      stores.  The z = 0 workgroup of each tile (its "combiner") collects the
+//      other slices' words (re-reading those whose tag is not this launch's),
+//      sums the partials in slice order, applies bias, bf16 rounding and the
+//      activation, and publishes the tile as words {tag, two bf16};
+//   2. every workgroup then puts the first two tiles of its argmax stream in
+//      flight, reads the whole rank (re-reading untagged words, bounded) and
+//      runs the GEMV-argmax stream of fused_argmax_gemv.h on the prefetched
+//      tiles onwards.
+// The order inside a workgroup follows from how a CU serves its loads: in
+// issue order, so anything issued behind the CU's own prefetch waits for it
+// (the prefetch of the whole grid takes about 5 us to drain).  The operand
+// loads and the partial's store therefore go first; a combiner, whose polls
+// are on the critical path, issues its prefetch only after it has published
+// its tile; everybody else's rank read waits behind its own prefetch, which it
+// would do anyway, since those tiles are consumed first.  Data and readiness
+// travel in the same word, so there are no counters, flags or atomics besides
+// the argmax keys.
+//
+// The tag is a function of a launch generation word in the control area that
+// the last workgroup advances at the end of each launch: words left from an
+// earlier launch (or anything a different entry point left in the data region)
+// never carry the current tag.  If the re-reads run out (the grid is not
+// co-resident, e.g. other work shares the device), the workgroup computes the
+// whole rank itself with the same partials in the same order, so the result
+// is the same bit for bit and the kernel always terminates.
 //
 // The fp8 variant (lowrank_decode8_kernel) runs the same phases with the rank
 // projection weight A as e4m3 (K32 blocks, widened to bf16 in registers, its
@@ -35,35 +46,37 @@
 namespace dels {
 
 constexpr int kDecodeWGs = 256;          // grid of the fused decode step
-constexpr int kDecodeMaxJ = 8;           // K steps per wave in the split rank projection
 
 struct DecodeKArgs {
-    ArgmaxKArgs am;                      // argmax part; am.rank is unused (rank_buf)
+    ArgmaxKArgs am;                      // argmax part; am.rank is unused
     const uint16_t* h; int64_t ldh;      // [M, d] bf16
     const void* A;                       // [r, d] in blocks of 16 rows x 32 K: bf16 (1 KiB) or e4m3 (512 B)
     const float* a_scale;                // e4m3 A only: per-rank-column scale [r]
     const uint16_t* bias; int act;
     int ksa;                             // d / 32
-    int nct, nz, kpz;                    // rank column tiles (r/16), K splits, K blocks per split
-    float* partial;                      // [nct][nz][256]
-    unsigned int* tile_cnt;              // [nct]
-    unsigned int* done;                  // published rank tiles
-    uint16_t* rank_buf;                  // [16][r] bf16
-    int spin_limit;                      // polls of `done` before computing the rank locally
+    int nct, nz, kpz;                    // rank column tiles (r/16), K slices (256/nct), K blocks per slice
+    unsigned long long* partial_words;   // [nct][nz][256]: tag << 32 | fp32 partial (slices z > 0)
+    unsigned long long* rank_words;      // [16][r/2]: tag << 32 | bf16 pair
+    unsigned int* gen;                   // launch generation (control area; advanced once per launch)
+    int spin_limit;                      // re-reads of untagged words before computing the rank locally
 };
+
+// Tag of the rank words of the launch that read generation g (never 0 for the
+// first launch on a zeroed workspace; distinct for 2^32 launches in a row).
+__device__ __forceinline__ uint32_t decode_tag(uint32_t g) { return (g + 1u) * 0x9E3779B1u; }
 
 // fp32 dot of rank column tile c over K blocks [kb0, kb1) for the 16 rows,
 // this wave taking every 4th block from kb0 + wave (all loads issued first).
 // A8: A holds e4m3 bytes, widened to bf16 at use.
-template <bool A8>
+template <bool A8, int J>
 __device__ __forceinline__ f32x4 decode_rank_partial(const DecodeKArgs& d, int M, int c, int kb0, int kb1,
                                                      int wave, int lane) {
     const int col = lane & 15, kg = lane >> 4;
     const bool mok = col < M;
     const uint16_t* hp = d.h + (int64_t)(mok ? col : 0) * d.ldh + kg * 8;
-    u32x4 xv[kDecodeMaxJ], wv[kDecodeMaxJ];
+    u32x4 xv[J], wv[J];
 #pragma unroll
-    for (int j = 0; j < kDecodeMaxJ; ++j) {
+    for (int j = 0; j < J; ++j) {
         const int kb = kb0 + wave + 4 * j;
         const int kc = kb < kb1 ? kb : min(kb0, d.ksa - 1);   // a valid block when masked
         xv[j] = *reinterpret_cast<const u32x4*>(hp + kc * 32);
@@ -78,7 +91,7 @@ __device__ __forceinline__ f32x4 decode_rank_partial(const DecodeKArgs& d, int M
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < kDecodeMaxJ; ++j) {
+    for (int j = 0; j < J; ++j) {
         const bool ok = kb0 + wave + 4 * j < kb1;
         u32x4 w = wv[j];
         if constexpr (A8) w = widen_e4m3x8(w[0], w[1]);
@@ -119,102 +132,151 @@ __device__ __forceinline__ float decode_tile_at(const float* red, int m, int n) 
     return red[(((m >> 2) * 16 + n) << 2) + (m & 3)];
 }
 
-// Phases 1 and 2: workgroup g computes the partial of rank tile g % nct over
-// K slice g / nct and publishes it; the tile's last arrival reduces the tile,
-// publishes the bf16 rank tile and counts it in `done`.
+// Partial of rank column tile c over K slice z (K blocks [z*kpz, (z+1)*kpz)),
+// wave-summed into `red`.  Rounds of 4*J blocks, J the smallest of 2/4/8/16
+// that covers the slice in one round where it can (no loads of masked blocks).
+template <bool A8, int J>
+__device__ __forceinline__ f32x4 decode_slice_acc(const DecodeKArgs& d, int M, int c, int k0, int k1, int wave,
+                                                  int lane) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int kb0 = k0; kb0 < k1; kb0 += 4 * J)
+        acc += decode_rank_partial<A8, J>(d, M, c, kb0, min(k1, kb0 + 4 * J), wave, lane);
+    return acc;
+}
 template <bool A8>
-__device__ __forceinline__ void decode_publish_rank(const DecodeKArgs& d, int M, int r, float* red, int& s_last) {
+__device__ __forceinline__ void decode_slice_partial(const DecodeKArgs& d, int M, int c, int z, float* red, int wave,
+                                                     int lane) {
+    const int k0 = z * d.kpz, k1 = min(d.ksa, k0 + d.kpz);
+    f32x4 acc;
+    if (d.kpz <= 8) acc = decode_slice_acc<A8, 2>(d, M, c, k0, k1, wave, lane);
+    else if (d.kpz <= 16) acc = decode_slice_acc<A8, 4>(d, M, c, k0, k1, wave, lane);
+    else if (d.kpz <= 32) acc = decode_slice_acc<A8, 8>(d, M, c, k0, k1, wave, lane);
+    else acc = decode_slice_acc<A8, 16>(d, M, c, k0, k1, wave, lane);
+    decode_wave_sum(red, acc, wave, lane);
+}
+
+// Phase 1 (see the top of the file).  Ends with a barrier; `red` is free after it.
+template <bool A8>
+__device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, int r, float* red, uint32_t tag) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
+    if ((int)blockIdx.x >= d.nct * d.nz) return;   // no rank work: straight to the argmax stream
     const int c = (int)blockIdx.x % d.nct;
     const int z = (int)blockIdx.x / d.nct;
-    {
-        const int kb0 = z * d.kpz;
-        const int kb1 = min(d.ksa, kb0 + d.kpz);
-        const f32x4 acc = decode_rank_partial<A8>(d, M, c, kb0, kb1, wave, lane);
-        decode_wave_sum(red, acc, wave, lane);
+    decode_slice_partial<A8>(d, M, c, z, red, wave, lane);
+    unsigned long long* pw = d.partial_words + (int64_t)c * d.nz * 256 + threadIdx.x;
+    if (z > 0) {
+        __hip_atomic_store(pw + z * 256, ((unsigned long long)tag << 32) | __float_as_uint(red[threadIdx.x]),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        return;
     }
-    float* mine = d.partial + ((int64_t)c * d.nz + z) * 256;
-    __hip_atomic_store(mine + threadIdx.x, red[threadIdx.x], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0);   // the partial has reached device coherence
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(&d.tile_cnt[c], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)(d.nz - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    float p[16];
-    const float* tp = d.partial + (int64_t)c * d.nz * 256 + threadIdx.x;
-    float v = 0.f;
-    for (int z0 = 0; z0 < d.nz; z0 += 16) {
+    // the combiner: slices 1 .. nz-1 in order, eight words in flight per thread
+    float v = red[threadIdx.x];
+    bool ok = d.spin_limit > 0;
+    for (int z0 = 1; ok && z0 < d.nz; z0 += 8) {
+        unsigned long long w[8];
+        uint32_t missing = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            p[i] = z0 + i < d.nz ? __hip_atomic_load(tp + (int64_t)(z0 + i) * 256, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT)
-                                 : 0.f;
+        for (int i = 0; i < 8; ++i) {
+            if (z0 + i < d.nz) {
+                w[i] = __hip_atomic_load(pw + (z0 + i) * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+            }
+        }
+        // re-read the whole group: every load in flight at once (a test right
+        // after each load would wait for it before the next is issued)
+        for (int it = 0; missing != 0 && it < d.spin_limit; ++it) {
+            __builtin_amdgcn_s_sleep(2);
+            missing = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v += p[i];
+            for (int i = 0; i < 8; ++i)
+                if (z0 + i < d.nz) w[i] = __hip_atomic_load(pw + (z0 + i) * 256, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (z0 + i < d.nz) missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+        }
+        ok = missing == 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (ok && z0 + i < d.nz) v = v + __uint_as_float((uint32_t)w[i]);
     }
-    __syncthreads();
+    if (__syncthreads_or(!ok)) return;   // the consumers will time out and compute the rank themselves
     red[threadIdx.x] = v;
     __syncthreads();
     if (threadIdx.x < 128) {
         const int m = threadIdx.x >> 3, n = (threadIdx.x & 7) * 2;
         const uint32_t lo = decode_rank_epilogue(d, decode_tile_at(red, m, n), c * 16 + n);
         const uint32_t hi = decode_rank_epilogue(d, decode_tile_at(red, m, n + 1), c * 16 + n + 1);
-        __hip_atomic_store(reinterpret_cast<uint32_t*>(d.rank_buf + (int64_t)m * r + c * 16 + n), lo | (hi << 16),
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(d.rank_words + (int64_t)m * (r / 2) + c * 8 + (threadIdx.x & 7),
+                           ((unsigned long long)tag << 32) | (lo | (hi << 16)), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
-    __builtin_amdgcn_s_waitcnt(0);   // the rank tile has reached device coherence
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __hip_atomic_exchange(&d.tile_cnt[c], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_fetch_add(d.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
 }
 
-// Phase 3: wait (bounded) until every rank tile is published, then bring the
-// rank ([16][r] bf16) into LDS: read once per workgroup with device-coherent
-// loads, a 64-byte share per thread -- or, if the wait timed out, computed
-// whole by this workgroup.  Ends with a barrier.
+// Phase 2: bring the rank ([16][R] bf16) into LDS.  Each thread reads its R/32
+// words with device-coherent loads and re-reads (at most spin_limit times) the
+// ones whose tag is not `tag`; if any word is still missing the workgroup
+// computes the whole rank itself (the same partials summed in the same order
+// as phase 1).  Ends with a barrier.
 template <int R, bool A8>
-__device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M, float* red, int& s_ready,
+__device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M, float* red, uint32_t tag,
                                                      uint16_t* s_rank) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
-    if (threadIdx.x == 0) {
-        int it = 0;
-        while (__hip_atomic_load(d.done, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)d.nct &&
-               it < d.spin_limit) {
-            __builtin_amdgcn_s_sleep(8);
-            ++it;
+    constexpr int kPer = R / 32;   // words per thread
+    static_assert(kPer <= 32, "one bit per word in a 32-bit mask");
+    unsigned long long w[kPer];
+    uint32_t missing = (1u << (kPer - 1) << 1) - 1u;
+    if (d.spin_limit > 0) {
+        // Wait until one word of every tile carries the tag -- eight bytes per
+        // lane, so waiting adds little traffic -- then read all the words.
+        {
+            const unsigned long long* pr = d.rank_words + (lane % d.nct) * 8;
+            for (int it = 0; it < d.spin_limit; ++it) {
+                const unsigned long long pw = __hip_atomic_load(pr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (__builtin_amdgcn_ballot_w64((uint32_t)(pw >> 32) != tag) == 0) break;
+                __builtin_amdgcn_s_sleep(2);
+            }
         }
-        s_ready = it < d.spin_limit;
-    }
-    __syncthreads();
-    if (s_ready) {
-        constexpr int kPer = R / 64;   // 8-byte words per thread
-        const unsigned long long* src = reinterpret_cast<const unsigned long long*>(d.rank_buf);
-        unsigned long long* dst = reinterpret_cast<unsigned long long*>(s_rank);
-        unsigned long long w[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i)
-            w[i] = __hip_atomic_load(src + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            w[i] = __hip_atomic_load(d.rank_words + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        missing = 0;
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = w[i];
+        for (int i = 0; i < kPer; ++i) missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+        for (int it = 0; missing != 0 && it < d.spin_limit; ++it) {   // all words in flight at once
+            __builtin_amdgcn_s_sleep(2);
+            missing = 0;
+#pragma unroll
+            for (int i = 0; i < kPer; ++i)
+                w[i] = __hip_atomic_load(d.rank_words + threadIdx.x + 256 * i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+        }
+    }
+    if (!__syncthreads_or(missing != 0)) {
+        uint32_t* dst = reinterpret_cast<uint32_t*>(s_rank);
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = (uint32_t)w[i];
     } else {
+#pragma clang fp contract(off)
         for (int cc = 0; cc < d.nct; ++cc) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            for (int kb0 = 0; kb0 < d.ksa; kb0 += 4 * kDecodeMaxJ)
-                acc += decode_rank_partial<A8>(d, M, cc, kb0, min(d.ksa, kb0 + 4 * kDecodeMaxJ), wave, lane);
-            decode_wave_sum(red, acc, wave, lane);
+            float v = 0.f;
+            for (int z = 0; z < d.nz; ++z) {
+                decode_slice_partial<A8>(d, M, cc, z, red, wave, lane);
+                v = z == 0 ? red[threadIdx.x] : v + red[threadIdx.x];
+                __syncthreads();   // red is rewritten by the next partial
+            }
+            red[threadIdx.x] = v;
+            __syncthreads();
             {
                 const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
                 s_rank[m * R + cc * 16 + n] = decode_rank_epilogue(d, decode_tile_at(red, m, n), cc * 16 + n);
             }
-            __syncthreads();   // red is rewritten by the next tile's sum
+            __syncthreads();   // red is rewritten by the next tile
         }
     }
     __syncthreads();
@@ -248,7 +310,6 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     __shared__ float s_val[4][16];
     __shared__ int s_idx[4][16];
     __shared__ int s_last;
-    __shared__ int s_ready;
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
 
     const int lane = threadIdx.x & 63;
@@ -256,7 +317,8 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     const int col = lane & 15;
     const int kg = lane >> 4;
 
-    decode_publish_rank<false>(d, a.M, r, red, s_last);
+    const uint32_t tag = decode_tag(__hip_atomic_load(d.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    decode_rank_phase<false>(d, a.M, r, red, tag);
 
     const int nwaves = gridDim.x * 4;
     int t = blockIdx.x * 4 + wave;
@@ -274,7 +336,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     if (have_a) load_tile<KSTEPS, B_PACKED_EXACT>(a, t, lane, brow, prior, ta);
     if (have_b) load_tile<KSTEPS, B_PACKED_EXACT>(a, t + nwaves, lane, brow, prior, tb);
 
-    decode_rank_into_lds<r, false>(d, a.M, red, s_ready, s_rank);
+    decode_rank_into_lds<r, false>(d, a.M, red, tag, s_rank);
     bf16x8 ra[KSTEPS];
     {
         const bool mok = col < a.M;
@@ -301,32 +363,29 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
             bidx[q] = take ? v : bidx[q];
         }
     };
-    // Invariant at the loop top: ta holds tile t and tb tile t + nwaves.  The
-    // prefetch inside the loop is unconditional on the continuing path, so the
-    // wait before each contraction covers only the older register set.
-    if (have_b) {
-        while (true) {
-            consume(ta, t);
-            if (t + 2 * nwaves >= ntiles) {
-                consume(tb, t + nwaves);
-                break;
-            }
-            load_tile<KSTEPS, B_PACKED_EXACT>(a, t + 2 * nwaves, lane, brow, prior, ta);
-            t += nwaves;
-            consume(tb, t);
-            if (t + 2 * nwaves >= ntiles) {
-                consume(ta, t + nwaves);
-                break;
-            }
-            load_tile<KSTEPS, B_PACKED_EXACT>(a, t + 2 * nwaves, lane, brow, prior, tb);
-            t += nwaves;
-        }
-    } else if (have_a) {
-        consume(ta, t);
+    // Tiles of this wave: t + k * nwaves for k < cnt.  At the loop top ta and tb
+    // hold tiles k and k + 1; the loop runs only while tiles k + 2 and k + 3
+    // exist, so both prefetches inside it are unconditional and every path into
+    // the loop top carries the same outstanding loads: the compiler's wait
+    // before each contraction then covers only the older register set.  (With
+    // a conditional prefetch in the loop it waited for both sets at the top.)
+    const int cnt = have_a ? (ntiles - 1 - t) / nwaves + 1 : 0;
+    int k = 0;
+    for (; k + 3 < cnt; k += 2) {
+        consume(ta, t + k * nwaves);
+        load_tile<KSTEPS, B_PACKED_EXACT>(a, t + (k + 2) * nwaves, lane, brow, prior, ta);
+        consume(tb, t + (k + 1) * nwaves);
+        load_tile<KSTEPS, B_PACKED_EXACT>(a, t + (k + 3) * nwaves, lane, brow, prior, tb);
     }
+    // zero to three tiles left, the first two already in ta and tb
+    if (k < cnt) consume(ta, t + k * nwaves);
+    if (k + 2 < cnt) load_tile<KSTEPS, B_PACKED_EXACT>(a, t + (k + 2) * nwaves, lane, brow, prior, ta);
+    if (k + 1 < cnt) consume(tb, t + (k + 1) * nwaves);
+    if (k + 2 < cnt) consume(ta, t + (k + 2) * nwaves);
 
-    // ---- 5. cross-workgroup argmax --------------------------------------------
-    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, d.done);
+    // ---- cross-workgroup argmax; the last workgroup advances the generation ----
+    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, nullptr);
+    if (s_last == 1 && threadIdx.x == 0) __hip_atomic_fetch_add(d.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // fp8 variant: A e4m3 (K32 blocks) with per-column scales in the rank
@@ -343,7 +402,6 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     __shared__ float s_val[4][16];
     __shared__ int s_idx[4][16];
     __shared__ int s_last;
-    __shared__ int s_ready;
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
     __shared__ __attribute__((aligned(1024))) char s_ring[RING ? 4 : 1][RING ? kDecode8Ring : 1]
                                                         [RING ? Ring8<KS8>::kSlot : 16];
@@ -353,7 +411,8 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     const int col = lane & 15;
     const int kg = lane >> 4;
 
-    decode_publish_rank<true>(d, a.M, r, red, s_last);
+    const uint32_t tag = decode_tag(__hip_atomic_load(d.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    decode_rank_phase<true>(d, a.M, r, red, tag);
 
     const int nwaves = gridDim.x * 4;
     const int t = blockIdx.x * 4 + wave;
@@ -377,7 +436,7 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
         if (t + nwaves < ntiles) load_tile8<KS8>(a, t + nwaves, lane, brow, prior, tb);
     }
 
-    decode_rank_into_lds<r, true>(d, a.M, red, s_ready, s_rank);
+    decode_rank_into_lds<r, true>(d, a.M, red, tag, s_rank);
     __shared__ __attribute__((aligned(16))) uint8_t s_rq[16 * (r + 16)];
     __shared__ float s_rsc[16];
     quantize_rank_coop<r>(s_rank, r, a.M, s_rq, s_rsc);
@@ -391,7 +450,8 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     else
         stream_tiles8<KS8>(a, rq, rsc, t, nwaves, ntiles, lane, brow, prior, al, be, use_prior, best, bidx, ta, tb,
                            true);
-    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, d.done);
+    argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, nullptr);
+    if (s_last == 1 && threadIdx.x == 0) __hip_atomic_fetch_add(d.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Dispatch over K steps of B (r / 32) and the prior type for one base dtype.

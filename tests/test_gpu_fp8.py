@@ -219,6 +219,8 @@ def test_lowrank_argmax_fp8_repeat_and_local_rank_fallback(pkg, dev):
     finally:
         lib.dels_debug_set_decode_spin_limit(prev)
     assert_parity_fp8(ids2, score2, rank, Bq, sB, f(base), f(prior), f(alpha), f(beta), ref=(rid, rsc, rsec))
+    # the local computation sums the same K-slice partials in the same order
+    assert torch.equal(ids2, first[0]) and torch.equal(score2, first[1])
     ids3, score3 = pkg.lowrank_argmax_fp8(*xs)
     torch.cuda.synchronize()
     assert torch.equal(ids3, first[0]) and torch.equal(score3, first[1])

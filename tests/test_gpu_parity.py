@@ -451,9 +451,9 @@ def test_lowrank_decode_step(pkg, dev, M, d, r, act, bias, bdt, pdt, V):
 
 
 def test_lowrank_decode_repeat_and_local_rank_fallback(pkg, dev):
-    """Back-to-back decode steps are bit-identical (the cross-workgroup hand-off
-    of rank tiles and counters resets itself), and with the rank-ready poll
-    limit forced to zero -- every workgroup computes the rank itself, as when the
+    """Back-to-back decode steps are bit-identical (the rank words of one launch
+    never pass for the next one's), and with the rank poll limit forced to
+    zero -- every workgroup computes the rank itself, as when the
     grid is not co-resident -- the results still meet the parity rule."""
     M, d, r, V = 16, 4096, 512, 151936
     x = pkg.synth.config_inputs("qwen3_8b_m16")
@@ -478,6 +478,8 @@ def test_lowrank_decode_repeat_and_local_rank_fallback(pkg, dev):
     finally:
         lib.dels_debug_set_decode_spin_limit(prev)
     assert_parity(ids2, score2, rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta), ref=ref)
+    # the local computation sums the same K-slice partials in the same order
+    assert torch.equal(ids2, first[0]) and torch.equal(score2, first[1])
     # and the normal path again, on the workspace the fallback call used
     ids3, score3 = pkg.lowrank_argmax(xd.h, Ap, Bp, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
     torch.cuda.synchronize()
