@@ -282,6 +282,13 @@ __device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M
     __syncthreads();
 }
 
+// Slot of this workgroup in the wave-strided tile walk.  The first slots get
+// one tile more when the tiles do not divide evenly; they go to the
+// workgroups without rank work, which start streaming first.
+__device__ __forceinline__ int decode_first_tile(const DecodeKArgs& d) {
+    return ((int)blockIdx.x + (int)gridDim.x - d.nct * d.nz) % (int)gridDim.x;
+}
+
 // Per-lane argmax state of rows 4*(lane/16) + q (M <= 16: one row group).
 template <typename BaseT, typename PriorT>
 __device__ __forceinline__ void decode_rows(const ArgmaxKArgs& a, int kg, float (&al)[4], float (&be)[4],
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     decode_rank_phase<false>(d, a.M, r, red, tag);
 
     const int nwaves = gridDim.x * 4;
-    int t = blockIdx.x * 4 + wave;
+    int t = decode_first_tile(d) * 4 + wave;
     float al[4], be[4], best[4];
     int bidx[4];
     bool use_prior[4];
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     decode_rank_phase<true>(d, a.M, r, red, tag);
 
     const int nwaves = gridDim.x * 4;
-    const int t = blockIdx.x * 4 + wave;
+    const int t = decode_first_tile(d) * 4 + wave;
     float al[4], be[4], best[4];
     int bidx[4];
     bool use_prior[4];
