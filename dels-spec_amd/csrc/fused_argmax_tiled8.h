@@ -1,6 +1,8 @@
 // fp8 (e4m3) variant of the MFMA-tiled fused combine + vocabulary argmax, for
 // many rows (M >= 64): B in e4m3 K128 blocks with per-row fp32 scales, the
-// rank quantised per row to e4m3 in the prologue, v_mfma_scale_f32_32x32x64_f8f6f4.
+// rank quantised per row to e4m3 beforehand (quantize_rank_e4m3_kernel: bytes
+// [M][r] and one scale per row, read here as the MFMA operand; quantising in
+// this kernel's prologue spilled), v_mfma_scale_f32_32x32x64_f8f6f4.
 //
 // Per row m and vocabulary row v (the fp8 GEMV's semantics):
 //     dot      = f32(f32(acc[m, v] * sR[m]) * sB[v])      acc: the e4m3 x e4m3 contraction

@@ -21,9 +21,12 @@
  *    point may be captured into a hipGraph.
  *  - Workspace (`ws`): caller-owned device memory of at least the size the
  *    matching *_ws_bytes() function returns, 256-byte aligned, zero-filled
- *    once before first use (dels_workspace_init).  Kernels return it to all
- *    zeros before they finish.  Calls that share one workspace must not
- *    overlap in time (same stream is fine).
+ *    once before first use (dels_workspace_init).  Kernels return its
+ *    control area (the first 64 KiB) to the state they found it in -- zeros,
+ *    apart from one word that the fused decode step advances once per launch
+ *    (a launch generation) -- so no call needs a memset; the rest may hold
+ *    anything between calls.  Calls that share one workspace must not overlap
+ *    in time (same stream is fine).
  *  - Return value: DELS_OK (0) or a negative DELS_ERR_* code; no exception
  *    crosses the ABI.  dels_strerror() names a code, dels_last_error() gives
  *    the detail of the calling thread's last failure.
