@@ -69,10 +69,10 @@ def parse_args():
 # The dominant kernel(s) of one step per workload, with packed weights.  At
 # M <= 16 the whole step (rank projection + fused argmax) is one launch of the
 # decode kernel; at M=512 the step runs the rank projection GEMM, then the tiled
-# argmax and its partials reduce, which dominate.
+# argmax (its cross-workgroup reduce folded in), which dominates.
 ROOFLINE_KERNELS = {"qwen3_8b_m16": ("lowrank_decode_kernel",),
                     "qwen3_4b_m16": ("lowrank_decode_kernel",),
-                    "qwen3_8b_m512": ("fused_argmax_tiled_kernel", "argmax_partials_reduce_kernel")}
+                    "qwen3_8b_m512": ("fused_argmax_tiled_kernel",)}
 # With row-major weights the M=16 step is the rank projection and the GEMV argmax.
 ROWMAJOR_M16_KERNELS = ("fused_argmax_gemv_kernel",)
 
@@ -346,8 +346,8 @@ def bench_fp8(pkg, name, args, dev, torch):
             "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "mfma_frac": flops / (us * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
             "sets": nsets,
-            "fused_argmax_only": {"kernel": "quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel + "
-                                            "argmax_partials_reduce_kernel" if tiled else "fused_argmax_gemv8_kernel",
+            "fused_argmax_only": {"kernel": "quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel"
+                                            if tiled else "fused_argmax_gemv8_kernel",
                                   "us_per_launch": us_arg, "algorithmic_bytes": arg_bytes,
                                   "hbm_frac": arg_bytes / (us_arg * 1e-6) / 1e9 / HBM_PEAK_GBS,
                                   "mfma_frac": arg_flops / (us_arg * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS}}

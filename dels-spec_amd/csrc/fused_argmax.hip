@@ -21,14 +21,6 @@ constexpr int kPlanCUs = 256;
 
 int base_elem_bytes(int dtype) { return dtype == 0 ? 4 : 2; }
 
-// Partials of the tiled kernel: one key per (vocabulary chunk, row).
-size_t tiled_part_bytes(int64_t M, int64_t V) {
-    if (M < kTiledMinRows) return 0;
-    int gx = 1, gy = 1;
-    tiled_grid((int)std::min<int64_t>(M, kMaxKeyRows), (int)V, kPlanCUs, &gx, &gy);
-    return (size_t)gx * (size_t)M * 8;
-}
-
 // The tiled kernel reads B in the packed layout with r a multiple of 32 (up to
 // 512), and moves base/prior rows with 16-byte direct-to-LDS loads.
 bool tiled_eligible(const ArgmaxArgs& a) {
@@ -46,46 +38,14 @@ bool tiled_eligible(const ArgmaxArgs& a) {
     return (reinterpret_cast<uintptr_t>(a.rank) & 15) == 0 && a.ldrank % 8 == 0;
 }
 
-// Unsigned max of the per-chunk keys of each row, decoded into (id, score).
-// One wave per row: the lanes load the chunks' keys in parallel (so the loads'
-// latencies overlap) and reduce with cross-lane shuffles.
-__global__ __launch_bounds__(256) void argmax_partials_reduce_kernel(const unsigned long long* __restrict__ part,
-                                                                     int chunks, int M, int V, int64_t* out_ids,
-                                                                     float* out_score, int64_t ld_out) {
-    const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (m >= M) return;
-    unsigned long long k = 0;
-    for (int x = lane; x < chunks; x += 64) {
-        const unsigned long long p = part[(int64_t)x * M + m];
-        k = p > k ? p : k;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t lo = __shfl_xor((uint32_t)k, off, 64);
-        const uint32_t hi = __shfl_xor((uint32_t)(k >> 32), off, 64);
-        const unsigned long long o = ((unsigned long long)hi << 32) | lo;
-        k = o > k ? o : k;
-    }
-    if (lane != 0) return;
-    uint32_t idx = ~(uint32_t)(k & 0xffffffffull);
-    float val = f32_from_order_key((uint32_t)(k >> 32));
-    if (k == 0ull || idx >= (uint32_t)V) {
-        idx = 0;
-        val = -__builtin_inff();
-    }
-    out_ids[(int64_t)m * ld_out] = (int64_t)idx;
-    if (out_score) out_score[(int64_t)m * ld_out] = val;
-}
-
 }  // namespace
 
-size_t argmax_data_bytes(int64_t M, int64_t /*r*/, int64_t V) { return tiled_part_bytes(M, V); }
+size_t argmax_data_bytes(int64_t /*M*/, int64_t /*r*/, int64_t /*V*/) { return 0; }
 
 // The e4m3 argmax also keeps the rank quantised per row (tiled kernel).
-size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V) {
+size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t /*V*/) {
     if (M < kTiledMinRows) return 0;
-    return align256(tiled_part_bytes(M, V)) + align256((size_t)M * r) + align256((size_t)M * 4);
+    return align256((size_t)M * r) + align256((size_t)M * 4);
 }
 
 bool argmax_supported(int64_t M, int64_t r, int64_t /*V*/) { return r >= 8 && r <= 512 && M <= kMaxKeyRows; }
@@ -107,16 +67,16 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
         ka.M = a.M; ka.V = a.V;
         ka.nblk16 = (a.V + 15) / 16;
         ka.ntiles = (a.V + tiled::kTileCols - 1) / tiled::kTileCols;
-        ka.part = reinterpret_cast<unsigned long long*>(w + data_off);
+        ka.counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
+        ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
+        ka.key_stride = (int64_t)a.M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
+        ka.out_ids = a.out_ids; ka.out_score = a.out_score; ka.ld_out = a.ld_out;
         const int ks = a.r / 32;
         hipError_t e;
         if (a.base_dtype == 1) e = launch_tiled_bf16(ka, ks, pk, gx, gy, s);
         else if (a.base_dtype == 2) e = launch_tiled_f16(ka, ks, pk, gx, gy, s);
         else e = launch_tiled_f32(ka, ks, pk, gx, gy, s);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, ka.part, gx,
-                           a.M, a.V, a.out_ids, a.out_score, a.ld_out);
-        return hipGetLastError();
+        return e;
     }
     ArgmaxKArgs ka{};
     ka.rank = a.rank; ka.ldrank = a.ldrank;
@@ -310,9 +270,12 @@ hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_of
         ka.M = a.M; ka.V = a.V;
         ka.nblk16 = (a.V + 15) / 16;
         ka.ntiles = (a.V + tiled::kTileCols - 1) / tiled::kTileCols;
-        ka.part = reinterpret_cast<unsigned long long*>(w + data_off);
-        // the rank, quantised per row to e4m3, after the partials
-        uint8_t* rank_q = reinterpret_cast<uint8_t*>(w + data_off + align256(tiled_part_bytes(a.M, a.V)));
+        ka.counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
+        ka.keys = reinterpret_cast<unsigned long long*>(w + kKeysOff);
+        ka.key_stride = (int64_t)a.M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
+        ka.out_ids = a.out_ids; ka.out_score = a.out_score; ka.ld_out = a.ld_out;
+        // the rank, quantised per row to e4m3
+        uint8_t* rank_q = reinterpret_cast<uint8_t*>(w + data_off);
         float* rank_scale = reinterpret_cast<float*>(reinterpret_cast<char*>(rank_q) + align256((size_t)a.M * a.r));
         hipLaunchKernelGGL(quantize_rank_e4m3_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, a.rank, a.ldrank, a.M,
                            a.r, rank_q, rank_scale);
@@ -324,10 +287,7 @@ hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_of
         if (a.base_dtype == 1) e = launch_tiled8_bf16(ka, ks8, pk, gx, gy, s);
         else if (a.base_dtype == 2) e = launch_tiled8_f16(ka, ks8, pk, gx, gy, s);
         else e = launch_tiled8_f32(ka, ks8, pk, gx, gy, s);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(argmax_partials_reduce_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, ka.part, gx,
-                           a.M, a.V, a.out_ids, a.out_score, a.ld_out);
-        return hipGetLastError();
+        return e;
     }
     ArgmaxKArgs ka{};
     ka.rank = a.rank; ka.ldrank = a.ldrank;

@@ -47,11 +47,11 @@
 // differ by a multiple of 8, so they run on the same XCD and the second read of
 // each B tile is served by that XCD's L2.
 //
-// Cross-workgroup reduction: each workgroup writes one 64-bit key per row
-// (order(score) << 32 | ~index, 0 = no candidate) to a partials array
-// [chunks, M]; a second small kernel takes the unsigned maximum over chunks
-// -- the argmax with the lowest-index tie rule -- and decodes it.  No atomics,
-// no counters, nothing to reset.
+// Cross-workgroup reduction (tiled_argmax_finish): each workgroup merges one
+// 64-bit key per row (order(score) << 32 | ~index, 0 = no candidate) into the
+// row's key with a device-scope atomic maximum -- the unsigned maximum is the
+// argmax with the lowest-index tie rule --, and the last workgroup to arrive
+// decodes the keys and returns keys and arrival counter to zero.
 #pragma once
 
 #include <algorithm>
@@ -76,8 +76,55 @@ struct TiledKArgs {
     int M, V;
     int nblk16;                 // ceil(V / 16): 16-row block rows of the packed B
     int ntiles;                 // ceil(V / 32): 32-column vocabulary tiles
-    unsigned long long* part;   // [gridDim.x, M]
+    unsigned long long* keys;   // per-row argmax keys (control area), key_stride apart
+    int64_t key_stride;
+    unsigned int* counter;      // workgroup arrivals (control area)
+    int64_t* out_ids; float* out_score; int64_t ld_out;
 };
+
+// Cross-workgroup argmax of the tiled kernels: every workgroup merges its
+// rows' keys (order(score) << 32 | ~index, 0 = no candidate) into the row keys
+// with returning device-scope atomic maxima -- the unsigned maximum is the
+// argmax with the lowest-index tie rule --, then counts itself in; the last
+// workgroup decodes every row and returns keys and counter to zero.  (This
+// replaces a second kernel that reduced per-chunk keys: its launch cost more
+// than the atomics, which are spread over the workgroups' ends.)  `flag` may
+// alias the stage buffers: the first barrier ends every wave's use of them.
+template <int NB>
+__device__ __forceinline__ void tiled_argmax_finish(const TiledKArgs& a, const int (&m)[NB],
+                                                    const unsigned long long (&key)[NB], int* flag) {
+    __syncthreads();
+    unsigned long long seen = 0;
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+        if (m[i] >= 0 && key[i] != 0ull)
+            seen |= __hip_atomic_fetch_max(&a.keys[(int64_t)m[i] * a.key_stride], key[i], __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    // Using the returned values makes the maxima returning atomics: each has
+    // been performed before the barrier below (the write is overwritten).
+    if (seen == ~0ull) *flag = 2;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned total = gridDim.x * gridDim.y;
+        const unsigned prev = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *flag = prev == total - 1;
+    }
+    __syncthreads();
+    if (*flag != 1) return;
+    for (int r = threadIdx.x; r < a.M; r += blockDim.x) {
+        const unsigned long long k = __hip_atomic_exchange(&a.keys[(int64_t)r * a.key_stride], 0ull,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t idx = ~(uint32_t)(k & 0xffffffffull);
+        float val = f32_from_order_key((uint32_t)(k >> 32));
+        if (k == 0ull || idx >= (uint32_t)a.V) {   // no candidate at all (every score NaN)
+            idx = 0;
+            val = -__builtin_inff();
+        }
+        a.out_ids[(int64_t)r * a.ld_out] = (int64_t)idx;
+        if (a.out_score) a.out_score[(int64_t)r * a.ld_out] = val;
+    }
+    if (threadIdx.x == 0) __hip_atomic_exchange(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 namespace tiled {
 
@@ -457,6 +504,8 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
 
     // Decode the candidate slot st*16 + j into the vocabulary index, then merge
     // the two vocabulary quads of each row (lanes l and l^32).
+    int fin_m[kRowBlocks];
+    unsigned long long fin_key[kRowBlocks];
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
         float bv = best[rb];
@@ -472,11 +521,10 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
             bi = oi;
         }
         const int m = mw + 32 * rb + rl;
-        if (h == 0 && m < a.M) {
-            const unsigned long long key = bi == INT_MAX ? 0ull : pack_argmax(bv, (uint32_t)bi);
-            a.part[(int64_t)blockIdx.x * a.M + m] = key;
-        }
+        fin_m[rb] = (h == 0 && m < a.M) ? m : -1;
+        fin_key[rb] = bi == INT_MAX ? 0ull : pack_argmax(bv, (uint32_t)bi);
     }
+    tiled_argmax_finish(a, fin_m, fin_key, reinterpret_cast<int*>(&lds0));
 }
 
 // Grid of the tiled kernel: row groups of 256 rows times vocabulary chunks,

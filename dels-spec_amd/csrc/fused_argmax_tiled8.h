@@ -359,10 +359,9 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
         bidx = oi;
     }
     const int m = mw + rl;
-    if (h == 0 && m < a.M) {
-        const unsigned long long key = bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx);
-        a.part[(int64_t)blockIdx.x * a.M + m] = key;
-    }
+    const int fin_m[1] = {(h == 0 && m < a.M) ? m : -1};
+    const unsigned long long fin_key[1] = {bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx)};
+    tiled_argmax_finish(a, fin_m, fin_key, reinterpret_cast<int*>(&lds0));
 }
 
 template <int KS8, typename BaseT, typename PriorT>
