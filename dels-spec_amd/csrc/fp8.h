@@ -58,13 +58,18 @@ __device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t q) {
     return s | mag;
 }
 
-// Eight e4m3 bytes (little-endian in lo, hi) widened to the bf16x8 operand.
+// Eight e4m3 bytes (little-endian in lo, hi) widened to the bf16x8 operand by
+// gfx950's v_cvt_scalef32_pk_bf16_fp8 (two bytes per instruction, scale 1).
+// Every e4m3 value is exact in bf16; a check of all 256 codes on the MI355X
+// found the instruction bit-identical to e4m3_to_bf16_bits above except the
+// two NaN codes, which the packers never produce (they saturate at 448).
 __device__ __forceinline__ u32x4 widen_e4m3x8(uint32_t lo, uint32_t hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     u32x4 o;
-    o[0] = e4m3_to_bf16_bits(lo & 0xffu) | (e4m3_to_bf16_bits((lo >> 8) & 0xffu) << 16);
-    o[1] = e4m3_to_bf16_bits((lo >> 16) & 0xffu) | (e4m3_to_bf16_bits(lo >> 24) << 16);
-    o[2] = e4m3_to_bf16_bits(hi & 0xffu) | (e4m3_to_bf16_bits((hi >> 8) & 0xffu) << 16);
-    o[3] = e4m3_to_bf16_bits((hi >> 16) & 0xffu) | (e4m3_to_bf16_bits(hi >> 24) << 16);
+    o[0] = __builtin_bit_cast(uint32_t, (bf16x2_t)__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false));
+    o[1] = __builtin_bit_cast(uint32_t, (bf16x2_t)__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true));
+    o[2] = __builtin_bit_cast(uint32_t, (bf16x2_t)__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false));
+    o[3] = __builtin_bit_cast(uint32_t, (bf16x2_t)__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true));
     return o;
 }
 
