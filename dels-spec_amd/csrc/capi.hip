@@ -17,8 +17,9 @@ namespace dels {
 // The rollout's rank projection reads only G x r weights: below this hidden
 // size two launches (rank GEMM with K whole, then the argmax GEMV) finish
 // sooner than the one-launch decode step, whose device-wide rank hand-off
-// costs a fixed few microseconds.
-constexpr int kRolloutDecodeMinG = 2048;
+// costs a fixed few microseconds.  At G = 1024, r = 256 the decode step is
+// ahead (draft block of batch 8, block 16: 727.9 -> 719.2 us).
+constexpr int kRolloutDecodeMinG = 1024;
 
 static thread_local std::string g_last_error;
 
