@@ -340,12 +340,14 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     // Tiles of this wave: t + k * nwaves, k < cnt, through a ring of ND tile
     // register sets.  The first ND go in flight before the rank is read, so
     // HBM stays busy while the rank is finished: with four sets (64 MB over
-    // the grid at r = 512) the step takes 31.5 us, with two 33.4 us.  The
+    // the grid at r = 512) the step takes 31.5 us, with two 33.4 us; at
+    // r = 256 four sets beat two (a 14-step rollout 406 -> 389 us) and six
+    // lose (439 us).  The
     // loop runs only while the refills exist, so its loads are unconditional
     // and every path into the loop top carries the same outstanding loads:
     // the compiler's wait before each contraction covers only the oldest set
     // (with a conditional refill inside the loop it waited for all of them).
-    constexpr int ND = KSTEPS >= 16 ? 4 : 2;
+    constexpr int ND = KSTEPS >= 8 ? 4 : 2;
     const int cnt = t < ntiles ? (ntiles - 1 - t) / nwaves + 1 : 0;
     TileRegs<KSTEPS> tr[ND];
 #pragma unroll
