@@ -92,26 +92,25 @@ static int check_weight(const void* p, int64_t ld, int64_t cols, int layout, con
 
 // ---- workspace layouts -------------------------------------------------------
 
-// Every layout starts with the shared control area [0, kCtrlBytes).
+// Every layout starts with the control area and the decode words, [0, kDataOff).
 struct LowrankLayout {
-    size_t rank_off, part_off, argmax_off, decode_off, total;
+    size_t rank_off, part_off, argmax_off, total;
     SkinnyPlan plan;
 };
 
 static LowrankLayout lowrank_layout(int64_t M, int64_t d, int64_t r, int64_t V) {
     LowrankLayout L{};
     L.plan = plan_skinny(M, d, r, false);
-    L.rank_off = kCtrlBytes;
+    L.rank_off = kDataOff;
     L.part_off = L.rank_off + align256((size_t)M * r * 2);
     L.argmax_off = L.part_off + skinny_data_bytes(L.plan);
     // room for the bf16 argmax and for the e4m3 one (which also keeps the quantised rank)
-    L.decode_off = L.argmax_off + align256(std::max(argmax_data_bytes(M, r, V), argmax_fp8_data_bytes(M, r, V)));
-    L.total = L.decode_off + decode_data_bytes(M, d, r);
+    L.total = L.argmax_off + align256(std::max(argmax_data_bytes(M, r, V), argmax_fp8_data_bytes(M, r, V)));
     return L;
 }
 
 struct RolloutLayout {
-    size_t part_off, argmax_off, decode_off, total;   // the steps' kernels run in turn and share the partials
+    size_t part_off, argmax_off, total;   // the steps' kernels run in turn and share the partials
     SkinnyPlan rank_plan, gru_plan;
 };
 
@@ -119,10 +118,9 @@ static RolloutLayout rollout_layout(int64_t batch, int64_t G, int64_t r, int64_t
     RolloutLayout L{};
     L.rank_plan = plan_skinny(batch, G, r, false);
     L.gru_plan = plan_skinny(batch, G, G, true);
-    L.part_off = kCtrlBytes;
+    L.part_off = kDataOff;
     L.argmax_off = L.part_off + std::max(skinny_data_bytes(L.rank_plan), skinny_data_bytes(L.gru_plan));
-    L.decode_off = L.argmax_off + align256(argmax_data_bytes(batch, r, V));
-    L.total = L.decode_off + decode_data_bytes(batch, G, r);
+    L.total = L.argmax_off + align256(argmax_data_bytes(batch, r, V));
     return L;
 }
 
@@ -268,7 +266,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
 
         if (G >= kRolloutDecodeMinG && decode_eligible(B, G, r, ra.a_packed, aa.b_packed)) {
             // rank projection and argmax in one launch
-            e = launch_lowrank_decode(ra, aa, ws, L.decode_off, s);
+            e = launch_lowrank_decode(ra, aa, ws, s);
             if (e != hipSuccess) return hip_fail(e, "fused decode step launch");
         } else {
             e = launch_rank_proj(ra, L.rank_plan, ws, L.part_off, s);
@@ -347,7 +345,7 @@ int dels_pack_operand(const void* W, int64_t ldw, int64_t rows, int64_t cols, vo
 }
 
 size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r) {
-    return kCtrlBytes + skinny_data_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1),
+    return kDataOff + skinny_data_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1),
                                                       std::max<int64_t>(r, 1), false));
 }
 
@@ -367,19 +365,19 @@ int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, int a
     if (ldrank < r) return fail(DELS_ERR_INVALID_ARGUMENT, "rank leading dimension < r");
     const SkinnyPlan p = plan_skinny(M, d, r, false);
     if (!skinny_supported(p)) return fail(DELS_ERR_UNSUPPORTED, "rank projection shape needs too many tiles");
-    if ((rc = check_ws(ws, ws_bytes, kCtrlBytes + skinny_data_bytes(p))) != DELS_OK) return rc;
+    if ((rc = check_ws(ws, ws_bytes, kDataOff + skinny_data_bytes(p))) != DELS_OK) return rc;
     RankArgs ra{};
     ra.h = static_cast<const uint16_t*>(h); ra.ldh = ldh;
     ra.A = static_cast<const uint16_t*>(A); ra.lda = lda; ra.a_packed = a_layout == DELS_LAYOUT_MFMA16;
     ra.bias = static_cast<const uint16_t*>(bias); ra.act = act;
     ra.M = (int)M; ra.d = (int)d; ra.r = (int)r;
     ra.rank = static_cast<uint16_t*>(rank); ra.ldrank = ldrank;
-    hipError_t e = launch_rank_proj(ra, p, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_rank_proj(ra, p, ws, kDataOff, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "rank projection launch");
 }
 
 size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) {
-    return kCtrlBytes + align256(argmax_data_bytes(M, r, V));
+    return kDataOff + align256(argmax_data_bytes(M, r, V));
 }
 
 int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t ldb, int b_layout, const void* base,
@@ -401,7 +399,7 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
     a.beta = beta; a.beta_stride = beta_stride;
     a.M = (int)M; a.r = (int)r; a.V = (int)V;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
-    hipError_t e = launch_fused_argmax(a, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_fused_argmax(a, ws, kDataOff, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
 }
 
@@ -453,7 +451,7 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     hipError_t e;
     if (decode_eligible(M, d, r, ra.a_packed, a.b_packed)) {
         // few rows, packed weights: rank projection and argmax in one launch
-        e = launch_lowrank_decode(ra, a, ws, L.decode_off, s);
+        e = launch_lowrank_decode(ra, a, ws, s);
         return e == hipSuccess ? DELS_OK : hip_fail(e, "fused decode step launch");
     }
     e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
@@ -498,7 +496,7 @@ int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t col
 }
 
 size_t dels_fused_argmax_fp8_ws_bytes(int64_t M, int64_t r, int64_t V) {
-    return kCtrlBytes + align256(argmax_fp8_data_bytes(M, r, V));
+    return kDataOff + align256(argmax_fp8_data_bytes(M, r, V));
 }
 
 static void fill_argmax_fp8(ArgmaxArgs& a, const void* Bq, const float* b_scale, const void* base, int64_t ldbase,
@@ -533,7 +531,7 @@ int dels_fused_argmax_fp8(const void* rank, int64_t ldrank, const void* Bq, cons
     a.rank = static_cast<const uint16_t*>(rank); a.ldrank = ldrank;
     fill_argmax_fp8(a, Bq, b_scale, base, ldbase, base_dtype, prior, prior_dtype, alpha, alpha_stride, beta,
                     beta_stride, M, r, V, out_ids, out_score, ld_out);
-    hipError_t e = launch_fused_argmax_fp8(a, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_fused_argmax_fp8(a, ws, kDataOff, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
 }
 
@@ -581,7 +579,7 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
                     beta_stride, M, r, V, out_ids, out_score, ld_out);
     hipError_t e;
     if (decode8_eligible(M, d, r)) {
-        e = launch_lowrank_decode(ra, a, ws, L.decode_off, s);
+        e = launch_lowrank_decode(ra, a, ws, s);
         return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused decode step launch");
     }
     e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
@@ -590,7 +588,7 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused argmax launch");
 }
 
-size_t dels_argmax_rows_ws_bytes(int64_t, int64_t) { return kCtrlBytes; }
+size_t dels_argmax_rows_ws_bytes(int64_t, int64_t) { return kDataOff; }
 
 int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V, int64_t* out_ids, float* out_score,
                      int64_t ld_out, void* ws, size_t ws_bytes, void* stream) {
@@ -604,7 +602,7 @@ int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
                                       (long long)ldx, (long long)V);
     if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
     if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
-    int rc = check_ws(ws, ws_bytes, kCtrlBytes);
+    int rc = check_ws(ws, ws_bytes, kDataOff);
     if (rc != DELS_OK) return rc;
     hipError_t e = launch_argmax_rows(x, ldx, dtype, (int)M, (int)V, out_ids, out_score, ld_out, ws,
                                       static_cast<hipStream_t>(stream));
@@ -612,7 +610,7 @@ int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
 }
 
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {
-    return kCtrlBytes + skinny_data_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1),
+    return kDataOff + skinny_data_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1),
                                                       std::max<int64_t>(G, 1), true));
 }
 
@@ -627,7 +625,7 @@ int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const
     if (batch == 0) return DELS_OK;
     const SkinnyPlan p = plan_skinny(batch, G, G, true);
     if (!skinny_supported(p)) return fail(DELS_ERR_UNSUPPORTED, "GRU shape needs too many tiles");
-    if ((rc = check_ws(ws, ws_bytes, kCtrlBytes + skinny_data_bytes(p))) != DELS_OK) return rc;
+    if ((rc = check_ws(ws, ws_bytes, kDataOff + skinny_data_bytes(p))) != DELS_OK) return rc;
     GruArgs g{};
     g.gi_table = static_cast<const uint16_t*>(gi_table); g.ld_gi = ld_gi; g.table_rows = table_rows;
     g.tokens = tokens; g.tok_stride = tok_stride;
@@ -636,7 +634,7 @@ int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const
     g.b_hh = static_cast<const uint16_t*>(b_hh);
     g.batch = (int)batch; g.G = (int)G;
     g.h_out = static_cast<uint16_t*>(h_out); g.ldh_out = ldh_out;
-    hipError_t e = launch_gru_step(g, p, ws, kCtrlBytes, static_cast<hipStream_t>(stream));
+    hipError_t e = launch_gru_step(g, p, ws, kDataOff, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "GRU step launch");
 }
 

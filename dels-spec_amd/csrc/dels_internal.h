@@ -9,13 +9,21 @@
 namespace dels {
 
 // ---- workspace layout ---------------------------------------------------------
-// Every entry point uses the same control area at the start of the workspace:
-// cross-workgroup counters at [0, 32 KiB) and argmax keys at [32 KiB, 64 KiB).
-// Kernels return the control area to zero before they finish, except the last
-// 128-byte line of the counters, which holds words that persist between calls
-// (the fused decode step's launch generation); data regions (split-K partials,
-// rank words) start at kCtrlBytes and may hold anything between calls.  Calls
-// with different shapes or entry points can therefore share one workspace.
+// Every entry point lays its workspace out the same way:
+//  * [0, kCtrlBytes): the control area -- cross-workgroup counters at
+//    [0, 32 KiB) and argmax keys at [32 KiB, 64 KiB).  Kernels return it to
+//    zero before they finish, except the last 128-byte line of the counters,
+//    whose words persist between calls (the fused decode step's launch
+//    generation).
+//  * [kDecodeOff, kDataOff): the fused decode step's tagged words (rank
+//    partials and the published rank).  Reserved in every layout and written
+//    by the decode kernels only, so each word holds zero or the tag of an
+//    earlier decode launch on this workspace -- never leftover data of another
+//    entry point that could pass for the current launch's tag.
+//  * [kDataOff, ...): data regions of the other kernels (split-K partials, the
+//    rank, quantised operands); they may hold anything between calls.
+// Calls with different shapes or entry points can therefore share one
+// workspace (one at a time).
 constexpr size_t kCtrlBytes = 65536;
 constexpr size_t kCountersOff = 0;
 constexpr int kMaxCounters = 8160;             // counters that kernels return to zero
@@ -23,7 +31,15 @@ constexpr int kDecodeGenWord = 8160;           // the decode step's launch gener
 constexpr size_t kKeysOff = 32768;
 constexpr int kMaxKeyRows = 4096;
 
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline constexpr size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+constexpr int kDecodeWGs = 256;                // grid of the fused decode step (one workgroup per CU)
+constexpr int kDecodeMaxRank = 512;            // largest rank r the decode step takes
+// one 256-word partial per workgroup, then 16 rows x r/2 words of the rank
+constexpr size_t kDecodeWordBytes = align256((size_t)kDecodeWGs * 256 * 8) +
+                                    align256((size_t)16 * (kDecodeMaxRank / 2) * 8);
+constexpr size_t kDecodeOff = kCtrlBytes;
+constexpr size_t kDataOff = kDecodeOff + kDecodeWordBytes;
 
 // ---- skinny GEMM: rank projection and fused GRU step -----------------------
 
@@ -102,11 +118,9 @@ hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_of
 bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed);
 // The fp8 decode step (A e4m3 K32, B e4m3 K128): as above with r in {128, 256, 512}.
 bool decode8_eligible(int64_t M, int64_t d, int64_t r);
-// Data-region bytes of the decode step (rank partials and the shared bf16 rank).
-size_t decode_data_bytes(int64_t M, int64_t d, int64_t r);
 // fp8 when ra.a_scale and aa.b_scale are set (decode8_eligible), bf16 otherwise.
-hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, size_t data_off,
-                                 hipStream_t s);
+// The tagged words go to [kDecodeOff, kDataOff) of `ws`.
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, hipStream_t s);
 // Polls of the rank-ready count before a workgroup computes the rank itself
 // (test hook; returns the previous value).
 int set_decode_spin_limit(int limit);

@@ -100,60 +100,57 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
 // ---- plain row argmax ------------------------------------------------------------
 //
 // sample() at temperature 0 (code/dflash.py:31-33: torch.argmax over the last
-// dimension): the lowest index of each row's maximum.  Rows are split into
-// chunks over workgroups; each folds its best (value, index) into the row's
-// 64-bit key with a device-scope atomic max, and the last workgroup decodes and
-// clears the keys and the counter (as the fused argmax).  NaN entries are
-// skipped and an all -inf row gives index 0 with score -inf, as in the fused
-// argmax.
+// dimension): the lowest index of each row's maximum, where NaN counts as
+// larger than every number (torch.argmax returns the index of the first NaN).
+// Each candidate becomes its 64-bit key order(score) << 32 | ~index (every NaN
+// as the same quiet NaN, whose key lies above +inf's), so an unsigned max is
+// the argmax with both rules.  Rows are split into chunks over workgroups;
+// each folds its best key into the row's key with a device-scope atomic max,
+// and the last workgroup decodes and clears the keys and the counter (as the
+// fused argmax).  An all -inf row gives index 0 with score -inf.
 
 namespace {
+
+__device__ __forceinline__ unsigned long long row_argmax_key(float v, uint32_t idx) {
+    return pack_argmax(v != v ? __uint_as_float(0x7fc00000u) : v, idx);
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long x, int off) {
+    const uint32_t lo = __shfl_xor((uint32_t)x, off, 64);
+    const uint32_t hi = __shfl_xor((uint32_t)(x >> 32), off, 64);
+    return ((unsigned long long)hi << 32) | lo;
+}
 
 template <typename T>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const T* __restrict__ x, int64_t ldx, int M, int V,
                                                           int chunk, unsigned long long* keys, int64_t key_stride,
                                                           unsigned int* counter, int64_t* out_ids, float* out_score,
                                                           int64_t ld_out) {
-    __shared__ float s_val[4];
-    __shared__ int s_idx[4];
+    __shared__ unsigned long long s_key[4];
     __shared__ int s_last;
     const int m = blockIdx.y;
     const int v0 = blockIdx.x * chunk;
     const int v1 = min(V, v0 + chunk);
     const T* row = x + (int64_t)m * ldx;
-    float best = -__builtin_inff();
-    int bi = INT_MAX;
+    unsigned long long best = 0ull;   // below every candidate's key
     for (int v = v0 + (int)threadIdx.x; v < v1; v += 256) {
-        const float sv = load_f32(row + v);
-        const bool take = argmax_better(sv, v, best, bi);
-        best = take ? sv : best;
-        bi = take ? v : bi;
+        const unsigned long long k = row_argmax_key(load_f32(row + v), (uint32_t)v);
+        best = k > best ? k : best;
     }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const float ov = __shfl_xor(best, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (argmax_better(ov, oi, best, bi)) {
-            best = ov;
-            bi = oi;
-        }
+        const unsigned long long o = shfl_xor_u64(best, off);
+        best = o > best ? o : best;
     }
     const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        s_val[wave] = best;
-        s_idx[wave] = bi;
-    }
+    if ((threadIdx.x & 63) == 0) s_key[wave] = best;
     __syncthreads();
     unsigned long long seen = 0;
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
-            if (argmax_better(s_val[w], s_idx[w], best, bi)) {
-                best = s_val[w];
-                bi = s_idx[w];
-            }
-        if (bi != INT_MAX)
-            seen = __hip_atomic_fetch_max(&keys[(int64_t)m * key_stride], pack_argmax(best, (uint32_t)bi),
-                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int w = 1; w < 4; ++w) best = s_key[w] > best ? s_key[w] : best;
+        if (best != 0ull)
+            seen = __hip_atomic_fetch_max(&keys[(int64_t)m * key_stride], best, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
         // the returned value orders the count after the update
         const unsigned prev = __hip_atomic_fetch_add(counter, seen == ~0ull ? 2u : 1u, __ATOMIC_RELAXED,
                                                      __HIP_MEMORY_SCOPE_AGENT);
@@ -341,7 +338,7 @@ int set_decode_spin_limit(int limit) {
 
 bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed) {
     if (M < 1 || M > 16 || !a_packed || !b_packed) return false;
-    if (!(r == 64 || r == 128 || r == 256 || r == 512)) return false;
+    if (!(r == 64 || r == 128 || r == 256 || r == kDecodeMaxRank)) return false;
     if (d < 32 || d % 32 != 0) return false;
     return kDecodeWGs % decode_plan(d, r).nct == 0;
 }
@@ -350,15 +347,11 @@ bool decode8_eligible(int64_t M, int64_t d, int64_t r) {
     return (r == 128 || r == 256 || r == 512) && decode_eligible(M, d, r, true, true);
 }
 
-size_t decode_data_bytes(int64_t M, int64_t d, int64_t r) {
-    if (M > 16 || r % 16 != 0 || d % 32 != 0) return 0;
-    // tagged partial words of every workgroup, then the tagged rank words
-    return align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)) +
-           align256((size_t)16 * (r / 2) * sizeof(unsigned long long));
-}
+static_assert(kDecodeWordBytes >= align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)) +
+                                     (size_t)16 * (kDecodeMaxRank / 2) * sizeof(unsigned long long),
+              "the reserved decode region holds every workgroup's partial words and the rank words");
 
-hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, size_t data_off,
-                                 hipStream_t s) {
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, hipStream_t s) {
     const DecodePlan p = decode_plan(ra.d, ra.r);
     char* w = static_cast<char*>(ws);
     DecodeKArgs k{};
@@ -381,9 +374,9 @@ hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* 
     k.A = ra.A;
     k.bias = ra.bias; k.act = ra.act;
     k.ksa = p.ksa; k.nct = p.nct; k.nz = p.nz; k.kpz = p.kpz;
-    k.partial_words = reinterpret_cast<unsigned long long*>(w + data_off);
+    k.partial_words = reinterpret_cast<unsigned long long*>(w + kDecodeOff);
     k.rank_words = reinterpret_cast<unsigned long long*>(
-        w + data_off + align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)));
+        w + kDecodeOff + align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)));
     k.spin_limit = g_decode_spin_limit;
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     if (ra.a_scale != nullptr) {

@@ -6,7 +6,7 @@
 // weights are bf16): for row m and vocabulary index v,
 //     sR[m] = absmax(rank_m) / 448,  R_q = e4m3(rank_m / sR[m])
 //     dot   = fp32(R_q . B_q[v]) * sR[m] * sB[v]          (two roundings, in that order)
-//     s     = dot * alpha_m + base[m, v] - beta_m * prior[v]
+//     s     = fma(-beta_m, prior[v], fma(dot, alpha_m, base[m, v]))
 // then the same lowest-index argmax as the bf16 kernels.  Layout, streaming and
 // the cross-workgroup reduction are those of fused_argmax_gemv_kernel.
 #pragma once
@@ -61,9 +61,8 @@ __device__ __forceinline__ void consume_tile8(const ArgmaxKArgs& a, const i32x8 
     for (int q = 0; q < 4; ++q) {
         float dot = acc[q] * rsc[q];
         dot = dot * tr.bscale;
-        float sc = dot * al[q];
-        sc = sc + tr.base[q];
-        if (use_prior[q]) sc = sc - be[q] * tr.prior;
+        float sc = __builtin_fmaf(dot, al[q], tr.base[q]);
+        if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
         const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
         best[q] = take ? sc : best[q];
         bidx[q] = take ? v : bidx[q];
@@ -190,9 +189,8 @@ __device__ __forceinline__ void consume_tile8_lds(const ArgmaxKArgs& a, const i3
     for (int q = 0; q < 4; ++q) {
         float dot = acc[q] * rsc[q];
         dot = dot * bsc;
-        float sc = dot * al[q];
-        sc = sc + lds_f32(bl + (4 * kg + q) * 16 + col);
-        if (use_prior[q]) sc = sc - be[q] * pr;
+        float sc = __builtin_fmaf(dot, al[q], lds_f32(bl + (4 * kg + q) * 16 + col));
+        if (use_prior[q]) sc = __builtin_fmaf(-be[q], pr, sc);
         const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);
         best[q] = take ? sc : best[q];
         bidx[q] = take ? v : bidx[q];

@@ -1,8 +1,9 @@
 // Fused low-rank LM-head combine + vocabulary argmax: the small-M GEMV kernel.
 //
 // Semantics (code/kernel/dels.py:42-138): for row m and vocabulary index v,
-//     s[m, v] = fp32(rank_m . B[v]) * alpha_m + base[m, v] - beta_m * prior[v]
-// (prior term only when a prior is given and beta_m != 0); the result per row
+//     s[m, v] = fma(-beta_m, prior[v], fma(fp32(rank_m . B[v]), alpha_m, base[m, v]))
+// (each fma rounded once; the outer one only when a prior is given and
+// beta_m != 0 -- every kernel of the path combines this way); the result per row
 // is the lowest v attaining the maximum, and that maximum.  Logits never leave
 // registers.
 //
@@ -241,9 +242,8 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
         const int v = tile * 16 + col;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            float sc = acc[q] * al[q];
-            sc = sc + tr.base[q];
-            if (use_prior[q]) sc = sc - be[q] * tr.prior;
+            float sc = __builtin_fmaf(acc[q], al[q], tr.base[q]);
+            if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
             const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];

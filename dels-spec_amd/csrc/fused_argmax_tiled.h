@@ -2,9 +2,8 @@
 // kernel for many draft rows (batch x block verification, M >= 64).
 //
 // Semantics as the GEMV kernel (code/kernel/dels.py:42-138):
-//     s[m, v] = fp32(rank_m . B[v]) * alpha_m + base[m, v] - beta_m * prior[v]
-// and per row the lowest v attaining max_v s[m, v]; here the two products are
-// fused multiply-adds (one rounding each, as a compiled Triton kernel does).
+//     s[m, v] = fma(-beta_m, prior[v], fma(fp32(rank_m . B[v]), alpha_m, base[m, v]))
+// and per row the lowest v attaining max_v s[m, v].
 //
 // Here the contraction rank[M, r] x B[V, r]^T is a real dense GEMM, computed
 // transposed with v_mfma_f32_32x32x16_bf16 (on gfx950 the 32x32 bf16 MFMA

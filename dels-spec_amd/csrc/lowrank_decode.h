@@ -27,9 +27,13 @@
 // the argmax keys.
 //
 // The tag is a function of a launch generation word in the control area that
-// the last workgroup advances at the end of each launch: words left from an
-// earlier launch (or anything a different entry point left in the data region)
-// never carry the current tag.  If the re-reads run out (the grid is not
+// the last workgroup advances at the end of each launch, and it is never zero.
+// The words live in a workspace region that only the decode kernels write
+// (every other entry point's data starts past it), so a word holds zero (a
+// fresh workspace) or the tag of an earlier launch: neither passes for the
+// current one.  Tags repeat only after 2^32 - 1 launches on one workspace, so
+// a word would have to go unwritten by every launch of its shape for that long
+// to be mistaken.  If the re-reads run out (the grid is not
 // co-resident, e.g. other work shares the device), the workgroup computes the
 // whole rank itself with the same partials in the same order, so the result
 // is the same bit for bit and the kernel always terminates.
@@ -45,7 +49,6 @@
 
 namespace dels {
 
-constexpr int kDecodeWGs = 256;          // grid of the fused decode step
 
 struct DecodeKArgs {
     ArgmaxKArgs am;                      // argmax part; am.rank is unused
@@ -61,9 +64,13 @@ struct DecodeKArgs {
     int spin_limit;                      // re-reads of untagged words before computing the rank locally
 };
 
-// Tag of the rank words of the launch that read generation g (never 0 for the
-// first launch on a zeroed workspace; distinct for 2^32 launches in a row).
-__device__ __forceinline__ uint32_t decode_tag(uint32_t g) { return (g + 1u) * 0x9E3779B1u; }
+// Tag of the words of the launch that read generation g: an odd multiple of
+// g + 1 (a bijection on 32-bit words), with the one g that would give 0
+// (g = 2^32 - 1) mapped like g = 0 -- so never the zero of a fresh workspace,
+// and distinct for 2^32 - 1 launches in a row.
+__device__ __forceinline__ uint32_t decode_tag(uint32_t g) {
+    return (g + 1u + (g == 0xffffffffu ? 1u : 0u)) * 0x9E3779B1u;
+}
 
 // fp32 dot of rank column tile c over K blocks [kb0, kb1) for the 16 rows,
 // this wave taking every 4th block from kb0 + wave (all loads issued first).
@@ -373,9 +380,8 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
         const int v = tile * 16 + col;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            float sc = acc[q] * al[q];
-            sc = sc + tr.base[q];
-            if (use_prior[q]) sc = sc - be[q] * tr.prior;
+            float sc = __builtin_fmaf(acc[q], al[q], tr.base[q]);
+            if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
             const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];

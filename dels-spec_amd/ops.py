@@ -109,9 +109,12 @@ def _weight(w: Weight, name: str, cols: Optional[int] = None, rows: Optional[int
 class _Workspaces:
     """Zero-initialised scratch buffers, one per (device, stream), grown on demand.
 
-    The kernels return every workspace byte to zero before they finish, so a
-    buffer is cleared only when it is (re)allocated.  Calls on one stream are
-    ordered and may share it; each stream gets its own buffer.
+    Every entry point lays a workspace out alike (include/dels.h): a control
+    area that the kernels return to its previous state, a region only the
+    fused decode step writes (tagged words), and data regions that may hold
+    anything between calls.  No call needs the buffer cleared, so it is zeroed
+    only when it is (re)allocated.  Calls on one stream are ordered and may
+    share it; each stream gets its own buffer.
     """
 
     def __init__(self):
@@ -328,8 +331,9 @@ def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,
                 out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
     """``sample()`` at temperature 0 (code/dflash.py:31-33): the lowest index of
     each row's maximum over the last dimension.  ``logits`` [M, V] (any row
-    stride, unit column stride) fp32/bf16/fp16.  NaN entries are skipped; an all
-    -inf row gives id 0.  Returns ``(ids int64[M], score fp32[M])``."""
+    stride, unit column stride) fp32/bf16/fp16.  As ``torch.argmax``, the first
+    NaN of a row wins (score NaN); an all -inf row gives id 0.  Returns
+    ``(ids int64[M], score fp32[M])``."""
     if logits.dim() == 1:
         logits = logits.unsqueeze(0)
     _require_cuda(logits, "logits")

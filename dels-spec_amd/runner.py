@@ -53,9 +53,16 @@ class DeLSGraphRunner:
             device = torch.device("cuda", torch.cuda.current_device())
         self.device = device
 
+        # The reference keeps every static buffer in the local head's dtype
+        # (code/kernel/dels.py:252).  Here base logits and the prior keep that
+        # dtype (the kernels read fp32, bf16 and fp16), while the weights the
+        # rollout streams are held in bf16: an fp16 or fp32 head is converted
+        # once, so it runs at bf16 weight precision.
         dtype = local_head.rank_proj.weight.dtype
-        if dtype != torch.bfloat16:
-            raise ValueError(f"DeLS native graph runner requires bfloat16 local-head weights, got {dtype}.")
+        if dtype not in _DTYPES:
+            raise ValueError(f"DeLS graph runner supports float32, bfloat16 and float16 local heads, got {dtype}.")
+        self.dtype = dtype
+        wdt = torch.bfloat16
         self.rank_dim = int(local_head.low_rank_lm_head.weight.shape[1])
         self._can_triton_fuse = True
 
@@ -69,17 +76,17 @@ class DeLSGraphRunner:
             raise ValueError("DeLS graph runner supports only a single unidirectional GRU.")
         self.gru_hidden_dim = int(gru.hidden_size)
         with torch.inference_mode():
-            self.gru_w_ih = gru.weight_ih_l0.detach().to(device).contiguous()
-            self.gru_w_hh = gru.weight_hh_l0.detach().to(device).contiguous()
-            self.gru_b_ih = gru.bias_ih_l0.detach().to(device).contiguous() if gru.bias else None
-            self.gru_b_hh = gru.bias_hh_l0.detach().to(device).contiguous() if gru.bias else None
-            embed_weight = local_head.embed_tokens.weight.detach().to(device)
+            self.gru_w_ih = gru.weight_ih_l0.detach().to(device, wdt).contiguous()
+            self.gru_w_hh = gru.weight_hh_l0.detach().to(device, wdt).contiguous()
+            self.gru_b_ih = gru.bias_ih_l0.detach().to(device, wdt).contiguous() if gru.bias else None
+            self.gru_b_hh = gru.bias_hh_l0.detach().to(device, wdt).contiguous() if gru.bias else None
+            embed_weight = local_head.embed_tokens.weight.detach().to(device, wdt)
             # One-off input-projection table gi_table[v] = E[v] . W_ih^T + b_ih (code/kernel/dels.py:265-268).
             self._gru_input_proj_table = F.linear(embed_weight, self.gru_w_ih, self.gru_b_ih).contiguous()
-            self.rank_weight = local_head.rank_proj.weight.detach().to(device).contiguous()
+            self.rank_weight = local_head.rank_proj.weight.detach().to(device, wdt).contiguous()
             rb = local_head.rank_proj.bias
-            self.rank_bias = rb.detach().to(device).contiguous() if rb is not None else None
-            self.lm_head_weight = local_head.low_rank_lm_head.weight.detach().to(device).contiguous()
+            self.rank_bias = rb.detach().to(device, wdt).contiguous() if rb is not None else None
+            self.lm_head_weight = local_head.low_rank_lm_head.weight.detach().to(device, wdt).contiguous()
 
             baseline_flat = torch.zeros(self.vocab_size, dtype=dtype, device=device)
             if baseline_logits is not None:
@@ -108,9 +115,9 @@ class DeLSGraphRunner:
             self.static_base_logits = torch.zeros(B, S, V, dtype=dtype, device=device)
             self.static_out = torch.zeros(B, S, dtype=torch.long, device=device)
             self.static_scores = torch.zeros(B, S, dtype=torch.float32, device=device)
-            self._h_a = torch.zeros(B, G, dtype=dtype, device=device)
-            self._h_b = torch.zeros(B, G, dtype=dtype, device=device)
-            self._rank = torch.zeros(B, r, dtype=dtype, device=device)
+            self._h_a = torch.zeros(B, G, dtype=wdt, device=device)
+            self._h_b = torch.zeros(B, G, dtype=wdt, device=device)
+            self._rank = torch.zeros(B, r, dtype=wdt, device=device)
             self._alpha = torch.tensor(self.alpha_values, dtype=torch.float32, device=device)
             self._beta = torch.tensor(self.beta_values, dtype=torch.float32, device=device)
 
@@ -131,7 +138,7 @@ class DeLSGraphRunner:
         (steps * V for a [B, steps, V] tensor) and writing ``out_ids``/``out_scores`` [B, steps]."""
         B, G, r, V, S = self.batch_size, self.gru_hidden_dim, self.rank_dim, self.vocab_size, self.steps
         prior = self.baseline_logits if self.has_baseline else None
-        dtype = self.rank_weight.dtype
+        dtype = self.baseline_logits.dtype
         p = _lib.RolloutParams()
         p.gi_table = self._gru_input_proj_table.data_ptr()
         p.ld_gi = self._gru_input_proj_table.stride(0)

@@ -129,3 +129,42 @@ class SyntheticLocalHead(torch.nn.Module):
             self.prefix_gru.weight_hh_l0.copy_(torch.randn(3 * G, G, generator=g, device=dev) * std)
             self.rank_proj.weight.copy_(torch.randn(r, G, generator=g, device=dev) * std)
             self.low_rank_lm_head.weight.copy_(torch.randn(V, r, generator=g, device=dev) * std)
+
+
+@dataclass
+class DraftBlockWorkload:
+    """The whole-draft-block workload: batch 8, block 16 unshifted (k_draft 15:
+    one plain argmax and 14 DeLS steps), a target LM head W [V, d] bf16, a
+    local head of hidden size G with rank r, per-step alpha/beta ~ U[0, 0.6]
+    and the Zipf log-prior.  Weights live on the device."""
+
+    head: SyntheticLocalHead
+    W: torch.Tensor            # [V, d] bf16 ~ N(0, 0.02)
+    prior: torch.Tensor        # [V] fp32 log-prior
+    alphas: list
+    betas: list
+    batch: int
+    k_draft: int
+    d: int
+    V: int
+    gen: torch.Generator
+
+    def hiddens(self, n: int) -> list:
+        """``n`` draft blocks of hidden states [batch, k_draft, d] bf16 ~ N(0, 1)."""
+        return [torch.randn(self.batch, self.k_draft, self.d, generator=self.gen, device=self.W.device)
+                .to(torch.bfloat16) for _ in range(n)]
+
+
+def draft_block_workload(device, *, batch: int = 8, k_draft: int = 15, d: int = 4096, V: int = 151936,
+                         E: int = 1024, G: int = 1024, r: int = 256, act: str = "silu") -> DraftBlockWorkload:
+    """Seeded draft-block workload (defaults: the Qwen3-8B head with the reference
+    recipe's local head, E = G = 1024, r = 256, silu)."""
+    dev = torch.device(device)
+    head = SyntheticLocalHead(V, E, G, r, act=act, device=dev, seed=3)
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    W = (torch.randn(V, d, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    prior = zipf_log_prior(V, seed=0).to(torch.float32).to(dev)
+    steps = k_draft - 1
+    ab = torch.rand(2, steps, generator=g, device=dev) * 0.6
+    return DraftBlockWorkload(head, W, prior, ab[0].tolist(), ab[1].tolist(), batch, k_draft, d, V, g)

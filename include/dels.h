@@ -4,6 +4,7 @@
  * The path: for each draft row m,
  *     rank_m  = bf16(act(bf16(h_m . A^T + bias)))
  *     s[m, v] = fp32(rank_m . B[v]) * alpha_m + base[m, v] - beta_m * prior[v]
+ *               (evaluated as two fused multiply-adds, each rounded once)
  *     id_m    = lowest v attaining max_v s[m, v];  score_m = s[m, id_m]
  * without writing the [M, V] logits to memory, plus the GRU local-head step
  * that feeds the next draft position and a hipGraph of the whole suffix
@@ -21,12 +22,15 @@
  *    point may be captured into a hipGraph.
  *  - Workspace (`ws`): caller-owned device memory of at least the size the
  *    matching *_ws_bytes() function returns, 256-byte aligned, zero-filled
- *    once before first use (dels_workspace_init).  Kernels return its
- *    control area (the first 64 KiB) to the state they found it in -- zeros,
- *    apart from one word that the fused decode step advances once per launch
- *    (a launch generation) -- so no call needs a memset; the rest may hold
- *    anything between calls.  Calls that share one workspace must not overlap
- *    in time (same stream is fine).
+ *    once before first use (dels_workspace_init).  Every entry point lays it
+ *    out alike: a 64 KiB control area that kernels return to the state they
+ *    found it in -- zeros, apart from one word that the fused decode step
+ *    advances once per launch (a launch generation) -- so no call needs a
+ *    memset; then 544 KiB that only the fused decode step writes (its rank
+ *    hand-off words, each tagged with a launch generation); then data regions
+ *    that may hold anything between calls.  One workspace may therefore serve
+ *    every entry point and shape in turn; calls that share it must not
+ *    overlap in time (same stream is fine).
  *  - Return value: DELS_OK (0) or a negative DELS_ERR_* code; no exception
  *    crosses the ABI.  dels_strerror() names a code, dels_last_error() gives
  *    the detail of the calling thread's last failure.
@@ -170,8 +174,9 @@ int dels_debug_set_decode_spin_limit(int limit);
  * (code/dflash.py:31-33; torch.argmax over the vocabulary), as used for the
  * first draft position (code/dflash.py:473).  x [M, V] with row stride ldx,
  * dtype DELS_DTYPE_*; out_ids[m*ld_out] int64, out_score[m*ld_out] fp32 (or
- * NULL).  Ties go to the lowest index; NaN entries are skipped; a row of -inf
- * gives id 0 and score -inf.
+ * NULL).  Ties go to the lowest index; NaN ranks above every number, so a
+ * row holding NaN gives the index of its first NaN (score NaN), as
+ * torch.argmax does; a row of -inf gives id 0 and score -inf.
  */
 size_t dels_argmax_rows_ws_bytes(int64_t M, int64_t V);
 int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V,

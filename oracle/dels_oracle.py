@@ -16,8 +16,14 @@ Arithmetic contract restated here (the "Triton semantics" of the fused path,
 
 The dot product is evaluated in float64 and rounded once to float32 (the
 reference's fp32 accumulation order is compiler-defined, so no fixed order can
-be "the" reference; the exact dot is the common target).  The combine is
-evaluated in float32 with one rounding per operation, as the reference does.
+be "the" reference; the exact dot is the common target).  The combine is two
+fused multiply-adds, each rounded once to float32:
+
+    s = fma(dot, alpha_m, base[m, v]);   s = fma(-beta_m, prior[v], s)
+
+which is how the reference's Triton kernel computes ``acc *= ALPHA; acc +=
+base`` and ``acc -= BETA * baseline`` (Triton compiles with floating-point
+contraction enabled by default, so a multiply feeding an add becomes one fma).
 
 Pinning (see tests/test_oracle_*.py): bf16/e4m3 rounding against torch's own
 casts; rank projection against torch.nn.functional.linear/silu; the fused
@@ -38,6 +44,7 @@ __all__ = [
     "e4m3_round",
     "quantize_rows_e4m3",
     "quantize_rank_e4m3",
+    "fma_f32",
     "sigmoid_f32",
     "silu_f32",
     "rank_proj",
@@ -137,6 +144,32 @@ def silu_f32(x) -> np.ndarray:
         return (x / (_F32(1.0) + np.exp(-x))).astype(_F32)
 
 
+def fma_f32(a, b, c) -> np.ndarray:
+    """``a * b + c`` for float32 operands, rounded once to float32 (round to nearest even).
+
+    The product of two float32 values is exact in float64; the sum is rounded
+    to float64 *to odd* (the TwoSum residual says whether it was exact, and an
+    inexact even result steps one float64 ulp towards the residual), and the
+    odd-rounded float64 is then rounded to float32.  Rounding to odd in a format
+    with at least two more bits makes the second rounding correct (Boldo and
+    Melquiond, "When double rounding is odd", 2005).  inf/NaN operands follow
+    IEEE arithmetic.
+    """
+    a = np.asarray(a, _F32).astype(_F64)
+    b = np.asarray(b, _F32).astype(_F64)
+    c = np.asarray(c, _F32).astype(_F64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        p = a * b
+        s = p + c
+        bb = s - p
+        err = (p - (s - bb)) + (c - bb)          # exact residual of s = fl64(p + c)
+        finite = np.isfinite(s) & np.isfinite(err)
+        even = (s.view(np.uint64) & np.uint64(1)) == 0
+        bump = finite & (err != 0) & even
+        s = np.where(bump, np.nextafter(s, np.where(err > 0, np.inf, -np.inf)), s)
+    return s.astype(_F32)
+
+
 def _dot_f32(a, b) -> np.ndarray:
     """``a @ b.T`` evaluated in float64, rounded once to float32."""
     return (np.asarray(a, _F64) @ np.asarray(b, _F64).T).astype(_F32)
@@ -169,15 +202,13 @@ def rank_proj(h, A, bias=None, act: str = "identity") -> np.ndarray:
 # --------------------------------------------------------------------------
 
 def _combine(dot, base, prior, alpha, beta):
-    """fp32 combine of one [M, C] chunk (code/kernel/dels.py:68-90)."""
-    s = (dot * alpha[:, None]).astype(_F32)                 # acc *= ALPHA        (68)
-    s = (s + base).astype(_F32)                             # acc += base          (70-79)
-    if prior is not None:                                   # if HAS_BASELINE      (81-88)
+    """fp32 combine of one [M, C] chunk (code/kernel/dels.py:68-90), as two fmas."""
+    s = fma_f32(dot, alpha[:, None], base)                  # acc *= ALPHA; acc += base   (68-79)
+    if prior is not None:                                   # if HAS_BASELINE             (81-88)
         use = beta != 0
         if use.any():
-            with np.errstate(invalid="ignore"):
-                pb = (beta[:, None] * prior[None, :]).astype(_F32)
-            s = np.where(use[:, None], (s - pb).astype(_F32), s)
+            sp = fma_f32(-beta[:, None], prior[None, :], s)  # acc -= BETA * baseline
+            s = np.where(use[:, None], sp, s)
     return s
 
 
@@ -236,11 +267,10 @@ def score_at(rank, B, base, prior, alpha, beta, ids) -> np.ndarray:
     beta = _rowvec(beta, M)
     Bv = np.asarray(B, _F32)[ids]
     dot = np.einsum("mk,mk->m", rank.astype(_F64), Bv.astype(_F64)).astype(_F32)
-    s = (dot * alpha).astype(_F32)
-    s = (s + base[np.arange(M), ids]).astype(_F32)
+    s = fma_f32(dot, alpha, base[np.arange(M), ids])
     if prior is not None:
         p = np.asarray(prior, _F32).reshape(-1)[ids]
-        s = np.where(beta != 0, (s - (beta * p).astype(_F32)).astype(_F32), s)
+        s = np.where(beta != 0, fma_f32(-beta, p, s), s)
     return s.astype(_F32)
 
 
@@ -469,11 +499,10 @@ def score_at_fp8(rank, B_q, B_scale, base, prior, alpha, beta, ids) -> np.ndarra
     Bv = np.asarray(B_q, _F32)[ids]
     raw = np.einsum("mk,mk->m", R_q.astype(_F64), Bv.astype(_F64)).astype(_F32)
     dot = ((raw * R_scale).astype(_F32) * np.asarray(B_scale, _F32)[ids]).astype(_F32)
-    s = (dot * alpha).astype(_F32)
-    s = (s + base[np.arange(M), ids]).astype(_F32)
+    s = fma_f32(dot, alpha, base[np.arange(M), ids])
     if prior is not None:
         p = np.asarray(prior, _F32).reshape(-1)[ids]
-        s = np.where(beta != 0, (s - (beta * p).astype(_F32)).astype(_F32), s)
+        s = np.where(beta != 0, fma_f32(-beta, p, s), s)
     return s.astype(_F32)
 
 
@@ -507,23 +536,23 @@ def check_parity(dev_ids, dev_scores, ref_ids, ref_scores, ref_second, dev_pick_
     ref_scores = np.asarray(ref_scores, _F64).reshape(-1)
     ref_second = np.asarray(ref_second, _F64).reshape(-1)
     scale = np.maximum(np.abs(ref_scores), 1e-30)
-    with np.errstate(invalid="ignore"):
+    with np.errstate(invalid="ignore"):               # inf - inf on all -inf rows
         margin = (ref_scores - ref_second) / scale
-    pinned = margin > rel_margin
-    id_bad = pinned & (dev_ids != ref_ids)
-    res = {"rows": int(dev_ids.size), "pinned": int(pinned.sum()),
-           "id_mismatch_pinned": int(id_bad.sum()), "bad_rows": np.nonzero(id_bad)[0].tolist()}
-    if dev_scores is not None:
-        ds = np.asarray(dev_scores, _F64).reshape(-1)
-        both_inf = np.isinf(ds) & np.isinf(ref_scores) & (np.sign(ds) == np.sign(ref_scores))
-        sc_bad = ~both_inf & ~(np.abs(ds - ref_scores) <= score_atol)
-        res["score_bad"] = int(sc_bad.sum())
-        res["score_bad_rows"] = np.nonzero(sc_bad)[0].tolist()
-        finite = ~both_inf
-        res["max_score_err"] = float(np.max(np.abs(ds - ref_scores)[finite])) if finite.any() else 0.0
-    if dev_pick_scores is not None:
-        ps = np.asarray(dev_pick_scores, _F64).reshape(-1)
-        slack = rel_margin * scale + 1e-6
-        near_bad = ~pinned & ~(ps >= ref_scores - slack) & ~np.isinf(ref_scores)
-        res["unpinned_far_pick"] = int(near_bad.sum())
+        pinned = margin > rel_margin
+        id_bad = pinned & (dev_ids != ref_ids)
+        res = {"rows": int(dev_ids.size), "pinned": int(pinned.sum()),
+               "id_mismatch_pinned": int(id_bad.sum()), "bad_rows": np.nonzero(id_bad)[0].tolist()}
+        if dev_scores is not None:
+            ds = np.asarray(dev_scores, _F64).reshape(-1)
+            both_inf = np.isinf(ds) & np.isinf(ref_scores) & (np.sign(ds) == np.sign(ref_scores))
+            sc_bad = ~both_inf & ~(np.abs(ds - ref_scores) <= score_atol)
+            res["score_bad"] = int(sc_bad.sum())
+            res["score_bad_rows"] = np.nonzero(sc_bad)[0].tolist()
+            finite = ~both_inf
+            res["max_score_err"] = float(np.max(np.abs(ds - ref_scores)[finite])) if finite.any() else 0.0
+        if dev_pick_scores is not None:
+            ps = np.asarray(dev_pick_scores, _F64).reshape(-1)
+            slack = rel_margin * scale + 1e-6
+            near_bad = ~pinned & ~(ps >= ref_scores - slack) & ~np.isinf(ref_scores)
+            res["unpinned_far_pick"] = int(near_bad.sum())
     return res

@@ -22,29 +22,30 @@ def f(t):
     return t.detach().float().cpu().numpy()
 
 
-def np_first_argmax(x):
-    """Lowest index of each row's maximum, NaN skipped, all -inf -> 0."""
-    x = np.where(np.isnan(x), -np.inf, x)
-    return np.argmax(x, axis=1)
-
-
 @pytest.mark.parametrize("M,V,dtype,stride_pad", [(8, 151936, torch.bfloat16, 0), (5, 4099, torch.float32, 7),
                                                   (33, 20011, torch.float16, 0), (1, 1, torch.float32, 0)])
 def test_argmax_rows(pkg, dev, M, V, dtype, stride_pad):
+    """Ids as torch.argmax on the CPU (code/dflash.py:31-33): lowest index of the
+    maximum, the first NaN of a row wins, an all -inf row gives 0."""
     print(f"case argmax_rows M={M} V={V} {dtype}", flush=True)
     g = torch.Generator().manual_seed(M + V)
     full = (torch.randn(M, V + stride_pad, generator=g) * 3).to(dtype)
     x = full[:, :V]
-    if M > 2 and V > 10:
+    if M > 4 and V > 10:
         x[0, 3] = x[0, V - 2] = 100.0                   # equal maxima: the lower index wins
         x[1].fill_(-float("inf"))                        # all -inf -> 0
-        x[2, 5] = float("nan")                           # NaN is skipped
+        x[2, 7] = x[2, V - 1] = float("nan")             # the first NaN wins over the maximum
+        x[2, 1] = 1000.0
+        x[3, V - 1] = float("nan")                       # a NaN in the vocabulary tail
+        x[4, 0] = -float("nan")                          # a NaN with the sign bit set counts the same
     ids, score = pkg.argmax_rows(x.to(dev))
     torch.cuda.synchronize()
-    xn = f(x)
-    ref = np_first_argmax(xn)
+    ref = torch.argmax(x, dim=-1).numpy()
     np.testing.assert_array_equal(ids.cpu().numpy(), ref)
-    np.testing.assert_array_equal(score.cpu().numpy(), np.where(np.isnan(xn), -np.inf, xn)[np.arange(M), ref])
+    want = f(x)[np.arange(M), ref]
+    got = score.cpu().numpy()
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want))
+    np.testing.assert_array_equal(got[~np.isnan(want)], want[~np.isnan(want)])
 
 
 @pytest.mark.parametrize("B,k,d,V,E,G,r,act,with_prior", [(3, 6, 256, 5003, 32, 64, 64, "silu", True),
@@ -76,7 +77,7 @@ def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
     np.testing.assert_allclose(f(base), ref_base, rtol=2e-2, atol=2e-2)
     # first position: plain argmax of the device's base logits
     bn = f(base)
-    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), np_first_argmax(bn[:, 0, :]))
+    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(base[:, 0, :].cpu(), dim=-1).numpy())
     # the rollout on base[:, 1:], teacher-forced on the device's own ids
     prior_np = f(prior.to(torch.bfloat16)) if with_prior else None
     dev_ids = out[:, 1:].cpu().numpy()
@@ -89,3 +90,50 @@ def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
     assert res["id_mismatch_pinned"] == 0, res
     assert res["max_score_err"] < 2e-2, res
     step.close()
+
+
+def test_draft_step_full_size(pkg, dev):
+    """The whole draft block at the size the bench times: batch 8, block 16 (k_draft 15,
+    14 DeLS steps), W [151936, 4096], local head E = G = 1024, r = 256, silu, bf16 base,
+    the Zipf prior and per-step alpha/beta (synth.draft_block_workload).  The LM-head
+    GEMM against a float32 CPU product on a sample of rows, the first position against
+    torch.argmax, and the 14-step rollout teacher-forced against the oracle."""
+    print("case draft_step full size B=8 k=15 d=4096 V=151936 G=1024 r=256", flush=True)
+    wl = pkg.synth.draft_block_workload(dev)
+    B, k, d, V = wl.batch, wl.k_draft, wl.d, wl.V
+    head = wl.head
+    step = pkg.DeLSDraftStep(local_head=head, lm_head_weight=wl.W, batch_size=B, k_draft=k, vocab_size=V,
+                             alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior, device=dev)
+    hid = wl.hiddens(1)[0]
+    out = step(hid)
+    torch.cuda.synchronize()
+    base = step.static_base.clone()
+    out2 = step(hid)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out2, out, rtol=0, atol=0)
+    # LM head on a row sample (rows (b, position) of the [B*k, V] product)
+    rows = [0, 17, 45, 77, 119]
+    hid_rows = f(hid).reshape(B * k, d)[rows]
+    W_np = f(wl.W)
+    ref_rows = hid_rows @ W_np.T
+    got_rows = f(base).reshape(B * k, V)[rows]
+    np.testing.assert_allclose(got_rows, ref_rows, rtol=1e-2, atol=2e-3)      # bf16 output rounding
+    del W_np
+    # first draft position: torch.argmax of the device's bf16 base logits
+    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(base[:, 0, :].cpu(), dim=-1).numpy())
+    # the rollout over base[:, 1:], teacher-forced on the device's own ids
+    bn = f(base)
+    dev_ids = out[:, 1:].cpu().numpy()
+    prior_np = f(wl.prior.to(torch.bfloat16))
+    rid, rsc, rsec = oracle.rollout(
+        out[:, 0].cpu().numpy(), bn[:, 1:, :], embed=f(head.embed_tokens.weight),
+        W_ih=f(head.prefix_gru.weight_ih_l0), W_hh=f(head.prefix_gru.weight_hh_l0), b_hh=None,
+        A=f(head.rank_proj.weight), rank_bias=None, act=head.rank_activation, B=f(head.low_rank_lm_head.weight),
+        prior=prior_np, alphas=wl.alphas, betas=wl.betas, forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(step.static_rest_scores).reshape(-1), rid.reshape(-1),
+                              rsc.reshape(-1), rsec.reshape(-1))
+    assert res["rows"] == B * (k - 1) and res["pinned"] >= 0.9 * res["rows"], res
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["score_bad"] == 0, res
+    step.close()
+

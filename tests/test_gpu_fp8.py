@@ -163,6 +163,8 @@ FP8_STEP_CASES = [
     (9, 2560, 256, "silu", False, torch.float16, torch.float16, 30000),
     (40, 512, 256, "identity", True, torch.float32, torch.float32, 30000),   # rank GEMM + fp8 argmax
     (96, 1000, 128, "silu", True, torch.bfloat16, torch.bfloat16, 20011),    # LDS-tiled rank GEMM, e4m3 A
+    # the batched-verification shape: e4m3 rank GEMM, row quantisation, fp8 MFMA-tiled argmax
+    (512, 4096, 512, "identity", False, torch.bfloat16, torch.bfloat16, 151936),
 ]
 
 

@@ -7,6 +7,7 @@ differ from the oracle by one bf16 ulp only where fp32 accumulation order
 straddles a rounding boundary.
 """
 
+import ctypes
 import os
 
 import numpy as np
@@ -258,12 +259,24 @@ def test_fused_argmax_vocab_of_one_and_empty_batch(pkg, dev):
     assert ids.numel() == 0
 
 
-def test_shared_workspace_across_entry_points_and_shapes(pkg, dev):
-    """Entry points with different workspace layouts interleaved on one stream's workspace."""
+@pytest.mark.parametrize("layout", ["rowmajor", "packed"])
+def test_shared_workspace_across_entry_points_and_shapes(pkg, dev, layout):
+    """Entry points with different workspace layouts interleaved on one stream's workspace.
+
+    With packed weights the draft step is the one-launch decode kernel, whose
+    tagged words live in a region of the workspace that no other entry point
+    writes: the region is checked unchanged across the other calls."""
+    print(f"case shared workspace {layout}", flush=True)
     x = pkg.synth.lowrank_inputs(16, 1024, 128, 20000, seed=21)
     xd = x.to(dev)
+    if layout == "packed":
+        xd.A, xd.B = pkg.pack_operand(xd.A), pkg.pack_operand(xd.B)
     want = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta)
     want = (want[0].clone(), want[1].clone())
+    ref = oracle.lowrank_argmax(f(x.h), f(x.A), None, x.act, f(x.B), f(x.base), f(x.prior), f(x.alpha),
+                                f(x.beta))
+    assert_parity(want[0], want[1], ref[0], f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta), ref=ref[1:])
+    reserved = slice(65536, 65536 + 544 * 1024)   # the decode step's tagged words
     g = torch.Generator().manual_seed(22)
     big_h = torch.randn(512, 2048, generator=g).to(torch.bfloat16).to(dev)
     big_A = (torch.randn(384, 2048, generator=g) * 0.02).to(torch.bfloat16).to(dev)
@@ -271,9 +284,24 @@ def test_shared_workspace_across_entry_points_and_shapes(pkg, dev):
     w_hh = (torch.randn(3 * 256, 256, generator=g) * 0.05).to(torch.bfloat16).to(dev)
     tok = torch.arange(40, dtype=torch.int64, device=dev) % 50
     h40 = torch.randn(40, 256, generator=g).to(torch.bfloat16).to(dev)
-    for _ in range(2):
-        pkg.rank_proj(big_h, big_A, None, "silu")            # large split-K partial region
+    big_B = pkg.pack_operand((torch.randn(3000, 384, generator=g) * 0.02).to(torch.bfloat16).to(dev))
+    big_base = torch.randn(512, 3000, generator=g).to(dev)
+
+    def others():
+        rk = pkg.rank_proj(big_h, big_A, None, "silu")        # large split-K partial region
         pkg.gru_step(table, tok, h40, w_hh)                   # different tile count
+        pkg.fused_argmax(rk, big_B, big_base, None, 0.5, 0.0)  # tiled argmax, M=512
+
+    others()                                                  # grows the stream's workspace to its final size
+    for _ in range(2):
+        got = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta)
+        ws = pkg.ops.workspace(dev, 0)
+        torch.cuda.synchronize()
+        before = ws[reserved].clone()
+        others()
+        torch.cuda.synchronize()
+        assert pkg.ops.workspace(dev, 0).data_ptr() == ws.data_ptr()
+        assert torch.equal(ws[reserved], before)
         got = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta)
         torch.testing.assert_close(got[0], want[0], rtol=0, atol=0)
         torch.testing.assert_close(got[1], want[1], rtol=0, atol=0)
@@ -486,15 +514,79 @@ def test_lowrank_decode_repeat_and_local_rank_fallback(pkg, dev):
     assert torch.equal(ids3, first[0]) and torch.equal(score3, first[1])
 
 
-def test_lowrank_argmax_m512_rows(pkg, dev):
+@pytest.mark.parametrize("layout", ["rowmajor", "packed"])
+def test_lowrank_argmax_m512_rows(pkg, dev, layout):
+    """The batched-verification shape (M=512, d=4096, r=512, V=151936, bf16 base and prior):
+    every one of the 512 rows against the oracle, with row-major and packed weights."""
+    print(f"case lowrank_argmax M=512 {layout}", flush=True)
     x = pkg.synth.config_inputs("qwen3_8b_m512")
     xd = x.to(dev)
-    ids, score = pkg.lowrank_argmax(xd.h, xd.A, xd.B, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
+    A, B = (xd.A, xd.B) if layout == "rowmajor" else (pkg.pack_operand(xd.A), pkg.pack_operand(xd.B))
+    ids, score = pkg.lowrank_argmax(xd.h, A, B, xd.base, xd.prior, xd.alpha, xd.beta, act=x.act)
     torch.cuda.synchronize()
-    rows = np.r_[0:24, 250:262, 488:512]           # a sample of the 512 rows (oracle cost)
-    rank = oracle.rank_proj(f(x.h[rows]), f(x.A), None, x.act)
-    assert_parity(ids[rows], score[rows], rank, f(x.B), f(x.base[rows]), f(x.prior), f(x.alpha[rows]),
-                  f(x.beta[rows]))
+    rank = oracle.rank_proj(f(x.h), f(x.A), None, x.act)
+    res = assert_parity(ids, score, rank, f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
+    assert res["rows"] == 512 and res["pinned"] >= 500
+
+
+def _exact_dot_case(M, d, r, V, seed):
+    """Inputs whose rank and dot products are exact in fp32 under any summation order.
+
+    h and A in {-1, 0, 1} (A sparse) give an integer rank of magnitude <= 256
+    (exact in bf16); B holds multiples of 1/64 in [-1, 1]; every partial sum of
+    rank . B[v] is then a multiple of 1/64 below 2**15, i.e. within fp32's 24
+    bits, so MFMA accumulation order cannot change it.  The combine's roundings
+    are then the only ones left.
+    """
+    rng = np.random.default_rng(seed)
+    h = rng.integers(-1, 2, (M, d)).astype(np.float32)
+    A = (rng.integers(-1, 2, (r, d)) * (rng.random((r, d)) < 1 / 32)).astype(np.float32)
+    B = (rng.integers(-64, 65, (V, r)) / 64).astype(np.float32)
+    base = (rng.standard_normal((M, V)) * 3).astype(np.float32)
+    prior = np.log(rng.dirichlet(np.ones(V))).astype(np.float32)
+    alpha = rng.uniform(0.05, 0.6, M).astype(np.float32)
+    beta = rng.uniform(0.05, 0.6, M).astype(np.float32)
+    beta[::5] = 0.0                                      # rows without the prior term
+    return h, A, B, base, prior, alpha, beta
+
+
+def test_combine_rounding_is_the_same_on_every_path(pkg, dev):
+    """The combine s = fma(-beta, prior, fma(dot, alpha, base)) is rounded the same way by the
+    one-launch decode step (M <= 16), the GEMV kernel (M < 64) and the MFMA-tiled kernel
+    (M >= 64) as by the oracle: with exact dot products the scores agree bit for bit, on rows
+    where rounding the products separately would give different scores."""
+    M, d, r, V = 64, 256, 128, 20011
+    h, A, B, base, prior, alpha, beta = _exact_dot_case(M, d, r, V, seed=31)
+    rank = oracle.rank_proj(h, A)
+    assert np.array_equal(rank, h @ A.T)                 # the integer rank is exact
+    ids, best, _ = oracle.fused_argmax(rank, B, base, prior, alpha, beta)
+    # the same winners rounded as two separate products and sums
+    dot = (rank.astype(np.float64) * B[ids].astype(np.float64)).sum(1).astype(np.float32)
+    two = ((dot * alpha).astype(np.float32) + base[np.arange(M), ids]).astype(np.float32)
+    two = np.where(beta != 0, (two - (beta * prior[ids]).astype(np.float32)).astype(np.float32), two)
+    differs = two != best
+    assert differs[:16].sum() >= 2 and differs[:40].sum() >= 4 and differs.sum() >= 8, differs.sum()
+
+    hd = torch.from_numpy(h).to(torch.bfloat16).to(dev)
+    Ap = pkg.pack_operand(torch.from_numpy(A).to(torch.bfloat16).to(dev))
+    Bd = torch.from_numpy(B).to(torch.bfloat16).to(dev)
+    Bp = pkg.pack_operand(Bd)
+    rd = torch.from_numpy(rank).to(torch.bfloat16).to(dev)
+    based = torch.from_numpy(base).to(dev)
+    priord = torch.from_numpy(prior).to(dev)
+    al = torch.from_numpy(alpha).to(dev)
+    be = torch.from_numpy(beta).to(dev)
+    runs = {
+        "decode M=16": pkg.lowrank_argmax(hd[:16], Ap, Bp, based[:16], priord, al[:16], be[:16]),
+        "gemv M=40": pkg.fused_argmax(rd[:40], Bp, based[:40], priord, al[:40], be[:40]),
+        "gemv row-major M=40": pkg.fused_argmax(rd[:40], Bd, based[:40], priord, al[:40], be[:40]),
+        "tiled M=64": pkg.fused_argmax(rd, Bp, based, priord, al, be),
+    }
+    torch.cuda.synchronize()
+    for name, (gi, gs) in runs.items():
+        n = gi.numel()
+        np.testing.assert_array_equal(gi.cpu().numpy(), ids[:n], err_msg=name)
+        np.testing.assert_array_equal(gs.cpu().numpy(), best[:n], err_msg=name)
 
 
 # ------------------------------------------------------------------ golden fixtures
@@ -616,6 +708,101 @@ def test_graph_runner_rollout(pkg, dev, nb, steps, V, E, G, r, act, rank_bias, w
                               rsec.reshape(-1))
     # the device's bf16 GRU state may differ from the oracle's by an ulp: allow score drift of 2e-2
     assert res["id_mismatch_pinned"] == 0, res
+    assert res["max_score_err"] < 2e-2, res
+    runner.close()
+
+
+@pytest.mark.parametrize("head_dtype", [torch.float32, torch.float16])
+def test_graph_runner_accepts_fp32_and_fp16_heads(pkg, dev, head_dtype):
+    """A float32 or float16 local head runs as the same head converted once to bf16: base
+    logits and prior stay in the head's dtype, the streamed weights are bf16."""
+    print(f"case runner head dtype {head_dtype}", flush=True)
+    V, E, G, r, nb, steps = 3001, 32, 64, 64, 2, 5
+    head = _Head(V, E, G, r, "silu", False, seed=5).to(dev)           # bf16 weights
+    other = _Head(V, E, G, r, "silu", False, seed=5).to(dev).to(head_dtype)
+    with torch.no_grad():                                              # the same values in the wider dtype
+        for p, q in zip(head.parameters(), other.parameters()):
+            q.copy_(p.to(head_dtype))
+    g = torch.Generator().manual_seed(3)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0).to(head_dtype)
+    kw = dict(batch_size=nb, steps=steps, vocab_size=V, alpha_values=[0.3] * steps, beta_values=[0.2] * steps,
+              device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g).to(dev)
+    base = (torch.randn(nb, steps, V, generator=g) * 3).to(head_dtype).to(dev)
+    r_other = pkg.DeLSGraphRunner(local_head=other, baseline_logits=prior, **kw)
+    assert r_other.static_base_logits.dtype == head_dtype
+    out = r_other(prefix, base)
+    sc = r_other.static_scores.clone()
+    # the bf16 head's rollout over the same base logits and prior, kept in head_dtype
+    r_bf16 = pkg.DeLSGraphRunner(local_head=head, baseline_logits=prior, **kw)
+    with torch.inference_mode():
+        r_bf16.static_base_logits = base.clone()
+        r_bf16.baseline_logits = prior.to(dev).contiguous()
+        r_bf16.static_prefix_ids.copy_(prefix)
+        p = r_bf16._rollout_params(r_bf16.static_base_logits, steps * V, r_bf16.static_prefix_ids,
+                                   r_bf16.static_out, r_bf16.static_scores, r_bf16._ws)
+        pkg._lib.check(pkg._lib.load().dels_rollout_enqueue(ctypes.byref(p), torch.cuda.current_stream().cuda_stream),
+                       "dels_rollout_enqueue")
+    torch.cuda.synchronize()
+    torch.testing.assert_close(r_bf16.static_out, out, rtol=0, atol=0)
+    torch.testing.assert_close(r_bf16.static_scores, sc, rtol=0, atol=0)
+    r_other.close()
+    r_bf16.close()
+
+
+def test_runner_driven_by_position_mix_head(pkg, dev, tmp_path):
+    """A block-prefix position-mix joint checkpoint drives the runner as the reference's
+    benchmark wires it (code/benchmark.py:356-387, 471-480): its gates are the alpha/beta
+    schedules (alpha_beta_schedules), its baseline_logits buffer the prior.  Teacher-forced
+    rollout against the oracle."""
+    print("case runner from a position-mix joint head", flush=True)
+    V, E, G, r, nb, block = 6007, 48, 128, 64, 3, 16
+    steps = block - 2
+    g = torch.Generator().manual_seed(41)
+
+    class Inner(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.embed_tokens = torch.nn.Embedding.from_pretrained(torch.randn(V, E, generator=g), freeze=True)
+
+    class Target(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = Inner()
+            self.lm_head = torch.nn.Linear(E, V, bias=False)
+
+    gates = torch.rand(steps, 2, generator=g) * 0.6
+    gates[3, 1] = 0.0                                       # a position without the prior term
+    pre = "local_head_model."
+    state = {pre + "prefix_gru.weight_ih_l0": torch.randn(3 * G, E, generator=g) * 0.2,
+             pre + "prefix_gru.weight_hh_l0": torch.randn(3 * G, G, generator=g) * 0.2,
+             pre + "rank_proj.weight": torch.randn(r, G, generator=g) * 0.2,
+             pre + "low_rank_lm_head.weight": torch.randn(V, r, generator=g) * 0.2,
+             "position_gates": gates,
+             "baseline_logits": torch.log_softmax(torch.randn(V, generator=g), 0)}
+    cfg = {"method": "block_prefix_position_mix_joint",
+           "local_head_config": dict(vocab_size=V, embed_dim=E, gru_hidden_dim=G, low_rank_dim=r,
+                                     rank_activation="silu")}
+    path = str(tmp_path / "block_prefix_position_mix_joint.pt")
+    torch.save({"model_config": cfg, "model_state_dict": state}, path)
+    head = pkg.PositionMixJointHead.from_checkpoint(checkpoint_path=path, target_model=Target(), block_size=block,
+                                                    dtype=torch.bfloat16, device=dev)
+    alphas, betas = head.alpha_beta_schedules()
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V, alpha_values=alphas,
+                                 beta_values=betas, baseline_logits=head.baseline_logits, device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    base = (torch.randn(nb, steps, V, generator=g) * 3).to(torch.bfloat16)
+    out = runner(prefix.to(dev), base.to(dev))
+    torch.cuda.synchronize()
+    dev_ids = out.cpu().numpy()
+    rid, rsc, rsec = oracle.rollout(
+        prefix.numpy().reshape(-1), f(base), embed=f(head.embed_tokens.weight), W_ih=f(head.prefix_gru.weight_ih_l0),
+        W_hh=f(head.prefix_gru.weight_hh_l0), b_hh=None, A=f(head.rank_proj.weight), rank_bias=None, act="silu",
+        B=f(head.low_rank_lm_head.weight), prior=f(head.baseline_logits).reshape(-1),
+        alphas=np.array(alphas, np.float32), betas=np.array(betas, np.float32), forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(runner.static_scores).reshape(-1), rid.reshape(-1),
+                              rsc.reshape(-1), rsec.reshape(-1))
+    assert res["id_mismatch_pinned"] == 0 and res["pinned"] >= 0.9 * res["rows"], res
     assert res["max_score_err"] < 2e-2, res
     runner.close()
 

@@ -5,6 +5,8 @@ torch.argmax), closed forms that remove one term at a time, a pure-Python
 brute force on tiny shapes, planted maxima/ties, and permutation invariance.
 """
 
+from fractions import Fraction
+
 import numpy as np
 import pytest
 import torch
@@ -99,24 +101,73 @@ def test_prior_skipped_when_beta_zero_or_absent():
 
 # ---------------------------------------------------------------- brute force
 
+def _round_f32_exact(x: Fraction) -> np.float32:
+    """A rational rounded to the nearest float32 (ties to even), by integer arithmetic."""
+    if x == 0:
+        return np.float32(0.0)
+    sign = -1 if x < 0 else 1
+    ax = abs(x)
+    e = ax.numerator.bit_length() - ax.denominator.bit_length()   # 2**e <= ax < 2**(e+2)
+    if Fraction(2) ** e > ax:
+        e -= 1
+    elif Fraction(2) ** (e + 1) <= ax:
+        e += 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)
+    q = ax / quantum
+    n = q.numerator // q.denominator
+    rem = q - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return np.float32(sign * float(n * quantum))
+
+
+def _fma_exact(a, b, c) -> np.float32:
+    """``a * b + c`` of float32 values in exact rational arithmetic, rounded once to float32."""
+    return _round_f32_exact(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
 def _brute_force(rank, B, base, prior, alpha, beta):
-    """Element-by-element fp32 evaluation with Python loops (tiny shapes only)."""
+    """Element-by-element evaluation with Python loops (tiny shapes only): the dot in
+    exact rational arithmetic rounded once to fp32, the combine as two exact fmas."""
     f32 = np.float32
     M, V = base.shape
     ids, best = [], []
     for m in range(M):
         bv, bi = None, None
         for v in range(V):
-            dot = sum(float(rank[m, k]) * float(B[v, k]) for k in range(rank.shape[1]))
-            s = f32(f32(dot) * f32(alpha[m]))
-            s = f32(s + f32(base[m, v]))
+            dot = _round_f32_exact(sum(Fraction(float(rank[m, k])) * Fraction(float(B[v, k]))
+                                       for k in range(rank.shape[1])))
+            s = _fma_exact(dot, f32(alpha[m]), f32(base[m, v]))
             if prior is not None and beta[m] != 0:
-                s = f32(s - f32(f32(beta[m]) * f32(prior[v])))
+                s = _fma_exact(-f32(beta[m]), f32(prior[v]), s)
             if bv is None or s > bv:
                 bv, bi = s, v
         ids.append(bi)
         best.append(bv)
     return np.array(ids), np.array(best, np.float32)
+
+
+def test_fma_f32_is_correctly_rounded():
+    """oracle.fma_f32 against exact rational arithmetic, on random operands with
+    cancellation and on a constructed case that only a correct second rounding
+    gets right: 1 + (2**-24 + 2**-60) lies just above the float32 midpoint
+    between 1 and 1 + 2**-23 but rounds to the midpoint in float64."""
+    rng = np.random.default_rng(5)
+    n = 4000
+    a = (rng.uniform(1, 2, n) * 2.0 ** rng.integers(-8, 8, n)).astype(np.float32)
+    b = (rng.uniform(-2, 2, n) * 2.0 ** rng.integers(-8, 8, n)).astype(np.float32)
+    c = (-(a.astype(np.float64) * b) * rng.uniform(0.5, 1.5, n)).astype(np.float32)   # cancellation
+    a[:4] = [1 + 2.0 ** -12, 1.0, 3.0, np.float32(np.inf)]
+    b[:4] = [np.float32(2.0 ** -24 * (1 - 2.0 ** -12 + 2.0 ** -24)), 1.0, 0.5, 1.0]
+    c[:4] = [1.0, -1.0, 0.25, 1.0]
+    got = oracle.fma_f32(a, b, c)
+    exact = np.array([_fma_exact(x, y, z) if np.isfinite(x) else np.float32(np.inf) for x, y, z in zip(a, b, c)],
+                     np.float32)
+    np.testing.assert_array_equal(got, exact)
+    assert got[0] == np.float32(1 + 2.0 ** -23)
+    two_step = ((a * b).astype(np.float32) + c).astype(np.float32)
+    assert two_step[0] == np.float32(1.0)              # separate roundings land on the other neighbour
+    assert np.count_nonzero(two_step[4:] != exact[4:]) > 50   # the cases distinguish fma from two roundings
 
 
 @pytest.mark.parametrize("seed", [10, 11, 12])
