@@ -4,7 +4,9 @@ Public surface (mirrors the reference's interface for this path):
   * ``DeLSGraphRunner``          -- drop-in hipGraph suffix-rollout runner
   * ``DeLSDraftStep``            -- a whole draft block (target LM head, first
     argmax, rollout) as one graph
-  * ``DeLSLocalHead``            -- local-head module the runner consumes
+  * ``DeLSLocalHead``, ``MarkovDeLSLocalHead``, ``PositionMixJointHead`` --
+    the local-head modules the runners consume, with their checkpoint
+    loaders (``from_checkpoint``), and ``detect_local_head_checkpoint_kind``
   * ``parse_scalar_schedule``, ``load_unigram_log_prior``
   * ``fused_argmax``, ``lowrank_argmax``, ``rank_proj``, ``gru_step`` -- the
     per-step operators, each a thin wrapper over the C ABI in include/dels.h
@@ -14,8 +16,9 @@ Public surface (mirrors the reference's interface for this path):
     fp8 (e4m3 weights, per-channel scales) variant of the same step
 """
 
-from .local_head import (DeLSLocalHead, load_unigram_log_prior, parse_scalar_schedule,
-                         unigram_log_prior_from_counts)
+from .checkpoints import detect_local_head_checkpoint_kind
+from .local_head import (DeLSLocalHead, MarkovDeLSLocalHead, PositionMixJointHead, load_unigram_log_prior,
+                         parse_scalar_schedule, unigram_log_prior_from_counts)
 from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gru_step, lowrank_argmax,
                   lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows, quantize_pack_fp8,
                   rank_proj)
@@ -28,6 +31,9 @@ __all__ = [
     "DeLSDraftStep",
     "argmax_rows",
     "DeLSLocalHead",
+    "MarkovDeLSLocalHead",
+    "PositionMixJointHead",
+    "detect_local_head_checkpoint_kind",
     "parse_scalar_schedule",
     "load_unigram_log_prior",
     "unigram_log_prior_from_counts",
