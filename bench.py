@@ -17,8 +17,10 @@ kernel directly; at M=512 the dominant kernel, the fused argmax, is timed by a
 second graph of K argmax launches only (rank precomputed), the same way.  The
 argmax-only graph is reported at M=16 too, as a secondary figure.
 
-CPU baseline: the oracle (a numpy port of the reference semantics) on a
-bounded number of full calls of the same workload, on this host's cores.
+CPU baseline: the reference's eager CPU PyTorch step (F.linear, bf16 combine,
+torch.argmax; restated in oracle/torch_eager.py) on the same inputs, median of
+at least 20 calls on the host's CPU share, with its id agreement with the GPU.
+``--cpu-configs`` times it at every configuration instead and prints a table.
 
 Prints one JSON line.
 """
@@ -55,6 +57,9 @@ def parse_args():
                     help="add the fp8 variant (e4m3 A and B with per-channel scales) of the workload's shape")
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-configs", action="store_true",
+                    help="only time the reference's CPU torch step at every configuration (no GPU use); "
+                         "one JSON line per configuration")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 512 MiB buffer 8 times (scale reference for HBM byte counters)")
     ap.add_argument("--layout", default="packed", choices=["packed", "rowmajor"],
@@ -245,6 +250,7 @@ def bench_workload(pkg, name, args, dev, torch):
         step(i)
     torch.cuda.synchronize(dev)
     eager = [(o[0].clone(), o[1].clone()) for o in outs]
+    ids_set0 = eager[0][0].cpu()          # set 0 holds the seeded CPU inputs
     for i in range(nsets):
         pkg.rank_proj(sets[i].h, weights[i][0], None, sets[i].act, out=ranks[i])
     torch.cuda.synchronize(dev)
@@ -275,6 +281,7 @@ def bench_workload(pkg, name, args, dev, torch):
         "step_TFLOPs": flops_step / (ms_step * 1e-3) / 1e12,
         "sets": nsets,
         "set_MB": per / 2**20,
+        "ids_set0": ids_set0,
     }
     rec["hbm_frac_step"] = rec["step_GBs"] / HBM_PEAK_GBS
     rec["mfma_frac_step"] = rec["step_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS
@@ -411,43 +418,93 @@ def bench_draft_step(pkg, args, dev, torch):
             "hbm_frac": total / (us_block * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
-def cpu_baseline(name, x0, seconds):
-    """The oracle on full calls of the workload, repeated for about `seconds`."""
-    import numpy as np
-
-    import oracle
-
+def cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
-    except Exception:
-        threads = os.cpu_count() or 1
-    f = lambda t: t.float().numpy()  # noqa: E731
-    h, A, B, base, prior, alpha, beta = (f(x0.h), f(x0.A), f(x0.B), f(x0.base), f(x0.prior), f(x0.alpha),
-                                         f(x0.beta))
-    M = h.shape[0]
-    calls = 0
-    t0 = time.perf_counter()
-    while True:
-        oracle.lowrank_argmax(h, A, None, x0.act, B, base, prior, alpha, beta)
-        calls += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return {
-        "value": M * calls / el,
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def time_cpu_path(fn, args, seconds, min_runs=20, warmup=3):
+    """Median wall time (s) of ``fn(*args)`` after ``warmup`` calls: at least ``min_runs``
+    timed calls, more while the time budget lasts (at most 200)."""
+    for _ in range(warmup):
+        fn(*args)
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        fn(*args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_threads() -> int:
+    """Threads for the CPU baseline: the share OMP_NUM_THREADS grants (16 per GPU on the
+    GPU hosts), else every core."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    return int(env) if env and env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
+
+
+def cpu_baseline(name, x0, seconds, gpu_ids=None):
+    """The reference's CPU PyTorch path for one draft step of the workload, timed on this host.
+
+    Timed: ``oracle.torch_eager.eager_step_bf16`` (the reference's eager bf16
+    step: F.linear, bf16 combine, torch.argmax) and ``step_fp32`` (the same in
+    fp32), median of >= 20 calls after 3 warm-ups with torch on ``cpu_threads()``
+    threads.  ``value`` is the eager bf16 path's rows/s.  With ``gpu_ids`` (the
+    device's ids for the same inputs) the agreement of each CPU path with them
+    is reported too.
+    """
+    import torch
+
+    from oracle import torch_eager
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    M = x0.shape["M"]
+    args = (x0.h, x0.A, x0.B, x0.base, x0.prior, x0.alpha, x0.beta, x0.act)
+    with torch.inference_mode():
+        t_bf16, n_bf16 = time_cpu_path(torch_eager.eager_step_bf16, args, seconds / 2)
+        t_f32, n_f32 = time_cpu_path(torch_eager.step_fp32, args, seconds / 2)
+        ids_bf16 = torch_eager.eager_step_bf16(*args)
+        ids_f32 = torch_eager.step_fp32(*args)
+    out = {
+        "value": M / t_bf16,
         "unit": "rows/s",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{calls} full calls of {name} (M={M}) through the numpy oracle (fp64 dot, fp32 combine), "
-                  f"{el:.1f} s on {platform.processor() or platform.machine()}",
+        "sample": f"median of {n_bf16} calls of one {name} draft step (M={M}: rank projection, low-rank logits, "
+                  f"bf16 combine, argmax) through the reference's eager torch path restated in "
+                  f"oracle/torch_eager.py; torch on {threads} threads of {os.cpu_count()} "
+                  f"({cpu_model()})",
+        "ms_per_step": t_bf16 * 1e3,
+        "fp32_path": {"rows_per_s": M / t_f32, "ms_per_step": t_f32 * 1e3, "runs": n_f32},
     }
+    if gpu_ids is not None:
+        g = gpu_ids.cpu()
+        out["gpu_id_agreement"] = {"vs_eager_bf16": float((g == ids_bf16).float().mean()),
+                                   "vs_fp32": float((g == ids_f32).float().mean()), "rows": M}
+    return out
 
 
 def main():
     args = parse_args()
     if args.traffic_from:
         traffic_from(args)
+        return
+    if args.cpu_configs:
+        import __graft_entry__
+
+        pkg = __graft_entry__.load_package()
+        for name in ("qwen3_4b_m16", "qwen3_8b_m16", "qwen3_8b_m512"):
+            res = cpu_baseline(name, pkg.synth.config_inputs(name), args.cpu_seconds)
+            print(json.dumps({"config": name, **res}), flush=True)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this build targets one GPU: the fused argmax shards by rows or by "
@@ -552,7 +609,7 @@ def main():
             except Exception as e:  # informative record only
                 out["fp8_m512"] = {"error": repr(e)}
     if args.cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(args.workload, x0, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(args.workload, x0, args.cpu_seconds, rec.get("ids_set0"))
     print(json.dumps(out), flush=True)
 
 
