@@ -22,6 +22,7 @@ DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_IDENTITY, ACT_SILU = 0, 1
 LAYOUT_ROWMAJOR, LAYOUT_MFMA16 = 0, 1
 LAYOUT_FP8_K128, LAYOUT_FP8_K32 = 2, 3
+NOALLOC_SCRATCH_BYTES = 16 << 20      # DELS_NOALLOC_SCRATCH_BYTES
 
 _i64 = ctypes.c_int64
 _int = ctypes.c_int
@@ -71,6 +72,9 @@ SIGNATURES = {
                                    _int,
                                    _fptr, _i64, _fptr, _i64, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz,
                                    _ptr]),
+    "dels_lowrank_argmax_noalloc": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _int, _ptr, _i64, _int, _ptr, _i64,
+                                           _int, _ptr, _int, _fptr, _i64, _fptr, _i64, _i64, _i64, _i64, _i64, _ptr,
+                                           _ptr, _i64, _ptr]),
     "dels_gru_step_ws_bytes": (_sz, [_i64, _i64]),
     "dels_gru_step": (_int, [_ptr, _i64, _i64, _ptr, _i64, _ptr, _i64, _ptr, _int, _ptr, _i64, _i64, _ptr, _i64, _ptr,
                              _sz, _ptr]),

@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/dels.h"
@@ -293,6 +294,52 @@ struct GraphHandle {
     hipGraphExec_t exec;
 };
 
+// ---- scratch of the allocation-free draft step ------------------------------------
+//
+// dels_lowrank_argmax_noalloc runs dels_lowrank_argmax with its workspace in
+// this file-scope device array instead of caller memory.  Every GPU the
+// library runs on holds its own copy until the process ends.  In host code the
+// name `scratch` is only a host-side stand-in: the device address of each
+// GPU's copy comes from hipGetSymbolAddress (with that GPU current) and is
+// kept per device; only that address is ever passed to kernels.
+static __device__ __align__(256) unsigned char scratch[DELS_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices];   // device address of `scratch` per device; null until set up
+}  // namespace
+
+// The current device's scratch address.  On the device's first call: look the
+// address up, then zero the array once with the fill kernel on `s`, ahead of
+// the call's own kernels (the workspace contract: zeroed before first use).
+// That fill must not be captured -- a graph would replay it and reset the
+// decode step's launch generation on every replay -- so a first call under
+// stream capture is refused.
+static int scratch_address(hipStream_t s, void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= kMaxScratchDevices) return fail(DELS_ERR_UNSUPPORTED, "device id %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[dev]) {
+        hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+        if ((e = hipStreamIsCapturing(s, &status)) != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (status != hipStreamCaptureStatusNone)
+            return fail(DELS_ERR_INVALID_ARGUMENT,
+                        "the first dels_lowrank_argmax_noalloc call on a device clears its scratch array and "
+                        "must not be captured: make one call outside stream capture first");
+        void* addr = nullptr;
+        if ((e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch))) != hipSuccess)
+            return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if ((e = launch_fill_zero(addr, DELS_NOALLOC_SCRATCH_BYTES, s)) != hipSuccess)
+            return hip_fail(e, "scratch zero fill launch");
+        g_scratch_addr[dev] = addr;
+    }
+    *out = g_scratch_addr[dev];
+    return DELS_OK;
+}
+
 }  // namespace dels
 
 using namespace dels;
@@ -458,6 +505,27 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     if (e != hipSuccess) return hip_fail(e, "rank projection launch");
     e = launch_fused_argmax(a, ws, L.argmax_off, s);
     return e == hipSuccess ? DELS_OK : hip_fail(e, "fused argmax launch");
+}
+
+int dels_lowrank_argmax_noalloc(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout,
+                                const void* bias, int act, const void* B, int64_t ldb, int b_layout,
+                                const void* base, int64_t ldbase, int base_dtype, const void* prior,
+                                int prior_dtype, const float* alpha, int64_t alpha_stride, const float* beta,
+                                int64_t beta_stride, int64_t M, int64_t d, int64_t r, int64_t V, int64_t* out_ids,
+                                float* out_score, int64_t ld_out, void* stream) {
+    const size_t need = dels_lowrank_argmax_ws_bytes(M, d, r, V);
+    if (need > DELS_NOALLOC_SCRATCH_BYTES)
+        return fail(DELS_ERR_WORKSPACE,
+                    "dels_lowrank_argmax_noalloc: M=%lld d=%lld r=%lld V=%lld needs %zu bytes of scratch, more "
+                    "than the %zu-byte array; call dels_lowrank_argmax with a workspace instead",
+                    (long long)M, (long long)d, (long long)r, (long long)V, need,
+                    (size_t)DELS_NOALLOC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    const int rc = scratch_address(static_cast<hipStream_t>(stream), &ws);
+    if (rc != DELS_OK) return rc;
+    return dels_lowrank_argmax(h, ldh, A, lda, a_layout, bias, act, B, ldb, b_layout, base, ldbase, base_dtype,
+                               prior, prior_dtype, alpha, alpha_stride, beta, beta_stride, M, d, r, V, out_ids,
+                               out_score, ld_out, ws, DELS_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 // ---- fp8 variant ---------------------------------------------------------------

@@ -160,6 +160,30 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
                         void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * dels_lowrank_argmax without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * workspace is a file-scope device array of DELS_NOALLOC_SCRATCH_BYTES that
+ * every GPU the library runs on holds until the process ends; the call
+ * allocates nothing.  Shapes whose dels_lowrank_argmax_ws_bytes() exceeds the
+ * array are refused with DELS_ERR_WORKSPACE (16 MiB covers M <= 512 at
+ * d = 4096, r = 512).  All calls on one GPU share its array: calls that
+ * overlap in time on one GPU race (serialise them, e.g. on one stream).  The
+ * first call on a device clears the array once on `stream` and must not be
+ * made under stream capture; later calls may be captured.
+ */
+#define DELS_NOALLOC_SCRATCH_BYTES (16u << 20)
+int dels_lowrank_argmax_noalloc(const void* h, int64_t ldh, const void* A, int64_t lda, int a_layout,
+                                const void* bias, int act,
+                                const void* B, int64_t ldb, int b_layout,
+                                const void* base, int64_t ldbase, int base_dtype,
+                                const void* prior, int prior_dtype,
+                                const float* alpha, int64_t alpha_stride,
+                                const float* beta, int64_t beta_stride,
+                                int64_t M, int64_t d, int64_t r, int64_t V,
+                                int64_t* out_ids, float* out_score, int64_t ld_out, void* stream);
+
+/*
  * Test hook (no counterpart in the reference).  With M <= 16 rows and both
  * weights in the MFMA-16 layout, dels_lowrank_argmax runs the rank projection
  * and the argmax in one launch whose workgroups wait (bounded) for each other's
