@@ -2,6 +2,7 @@
 
 Public surface (mirrors the reference's interface for this path):
   * ``DeLSGraphRunner``          -- drop-in hipGraph suffix-rollout runner
+  * ``MarkovDeLSGraphRunner``    -- the same for the Markov local head
   * ``DeLSDraftStep``            -- a whole draft block (target LM head, first
     argmax, rollout) as one graph
   * ``DeLSLocalHead``, ``MarkovDeLSLocalHead``, ``PositionMixJointHead`` --
@@ -19,15 +20,18 @@ Public surface (mirrors the reference's interface for this path):
 from .checkpoints import detect_local_head_checkpoint_kind
 from .local_head import (DeLSLocalHead, MarkovDeLSLocalHead, PositionMixJointHead, load_unigram_log_prior,
                          parse_scalar_schedule, unigram_log_prior_from_counts)
-from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gru_step, lowrank_argmax,
-                  lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows, quantize_pack_fp8,
-                  rank_proj)
+from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gather_argmax, gru_step,
+                  lowrank_argmax, lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows,
+                  quantize_pack_fp8, rank_proj)
 from .draft_step import DeLSDraftStep
 from .runner import DeLSGraphRunner
+from .markov_runner import MarkovDeLSGraphRunner
 from . import synth
 
 __all__ = [
     "DeLSGraphRunner",
+    "MarkovDeLSGraphRunner",
+    "gather_argmax",
     "DeLSDraftStep",
     "argmax_rows",
     "DeLSLocalHead",

@@ -52,6 +52,22 @@ class RolloutParams(ctypes.Structure):
     ]
 
 
+class MarkovRolloutParams(ctypes.Structure):
+    """Mirror of ``struct dels_markov_rollout`` in include/dels.h."""
+
+    _fields_ = [
+        ("embedding", _ptr), ("ld_embedding", _i64), ("table_rows", _i64),
+        ("lm_w", _ptr), ("lm_layout", _int),
+        ("prior", _ptr), ("prior_dtype", _int),
+        ("alpha", _fptr), ("beta", _fptr),
+        ("batch", _i64), ("steps", _i64), ("r", _i64), ("V", _i64),
+        ("prev_ids", _ptr),
+        ("base", _ptr), ("base_dtype", _int), ("ld_base", _i64),
+        ("out_ids", _ptr), ("out_scores", _ptr),
+        ("ws", _ptr), ("ws_bytes", _sz),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/dels.h declares.
 SIGNATURES = {
     "dels_abi_version": (_int, []),
@@ -83,6 +99,12 @@ SIGNATURES = {
     "dels_graph_create": (_int, [ctypes.POINTER(RolloutParams), ctypes.POINTER(_ptr)]),
     "dels_graph_launch": (_int, [_ptr, _ptr]),
     "dels_graph_destroy": (_int, [_ptr]),
+    "dels_gather_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_gather_argmax": (_int, [_ptr, _i64, _ptr, _i64, _i64, _ptr, _i64, _int, _ptr, _i64, _int, _ptr, _int, _fptr,
+                                  _i64, _fptr, _i64, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_markov_rollout_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_markov_rollout_enqueue": (_int, [ctypes.POINTER(MarkovRolloutParams), _ptr]),
+    "dels_markov_graph_create": (_int, [ctypes.POINTER(MarkovRolloutParams), ctypes.POINTER(_ptr)]),
     "dels_argmax_rows_ws_bytes": (_sz, [_i64, _i64]),
     "dels_argmax_rows": (_int, [_ptr, _i64, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_packed_fp8_bytes": (_sz, [_i64, _i64, _int]),

@@ -294,6 +294,94 @@ struct GraphHandle {
     hipGraphExec_t exec;
 };
 
+// One eager run of `enqueue` on a private stream (resolves per-kernel launch
+// configuration outside capture), then the same work captured into a graph.
+template <typename Enqueue>
+static int capture_graph(Enqueue enqueue, void** graph_out) {
+    hipStream_t cs = nullptr;
+    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail(e, "capture stream creation");
+    int rc = enqueue(cs);
+    if (rc == DELS_OK && (e = hipStreamSynchronize(cs)) != hipSuccess) rc = hip_fail(e, "warm-up run");
+    hipGraph_t graph = nullptr;
+    if (rc == DELS_OK) {
+        e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+        if (e != hipSuccess) {
+            rc = hip_fail(e, "hipStreamBeginCapture");
+        } else {
+            rc = enqueue(cs);
+            hipError_t e2 = hipStreamEndCapture(cs, &graph);
+            if (rc == DELS_OK && e2 != hipSuccess) rc = hip_fail(e2, "hipStreamEndCapture");
+        }
+    }
+    hipGraphExec_t exec = nullptr;
+    if (rc == DELS_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
+        rc = hip_fail(e, "hipGraphInstantiate");
+    (void)hipStreamDestroy(cs);
+    if (rc != DELS_OK) {
+        if (graph) (void)hipGraphDestroy(graph);
+        return rc;
+    }
+    *graph_out = new GraphHandle{graph, exec};
+    return DELS_OK;
+}
+
+// ---- Markov rollout ----------------------------------------------------------------
+
+static int check_markov(const dels_markov_rollout* p) {
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout parameters are NULL");
+    if (p->steps <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout requires steps > 0, got %lld",
+                                   (long long)p->steps);
+    if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout requires batch > 0");
+    if (!p->prev_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "prev_ids is NULL");
+    if (p->table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "embedding table is empty");
+    int rc = check_bf16_matrix(p->embedding, p->ld_embedding, p->r, "embedding");
+    if (rc != DELS_OK) return rc;
+    if (p->ld_base != 0 && p->ld_base < p->steps * p->V)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout ld_base %lld < steps * V", (long long)p->ld_base);
+    if ((rc = check_argmax_args(nullptr, p->r, p->lm_w, p->r, p->lm_layout, p->base,
+                                p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->prior, p->prior_dtype,
+                                p->alpha, 0, p->beta, 0, p->batch, p->r, p->V, p->out_ids, p->steps, false)) != DELS_OK)
+        return rc;
+    return check_ws(p->ws, p->ws_bytes, kDataOff + align256(argmax_data_bytes(p->batch, p->r, p->V)));
+}
+
+static ArgmaxArgs gather_args(const int64_t* tokens, int64_t tok_stride, const void* E, int64_t lde,
+                              int64_t table_rows, const void* B, int64_t ldb, int b_layout, const void* base,
+                              int64_t ldbase, int base_dtype, const void* prior, int prior_dtype, const float* alpha,
+                              int64_t alpha_stride, const float* beta, int64_t beta_stride, int64_t M, int64_t r,
+                              int64_t V, int64_t* out_ids, float* out_score, int64_t ld_out) {
+    ArgmaxArgs a{};
+    a.rank = static_cast<const uint16_t*>(E); a.ldrank = lde;
+    a.rank_rows = tokens; a.rank_rows_stride = tok_stride; a.rank_rows_count = table_rows;
+    a.B = static_cast<const uint16_t*>(B); a.ldb = ldb; a.b_packed = b_layout == DELS_LAYOUT_MFMA16;
+    a.base = base; a.ldbase = ldbase; a.base_dtype = base_dtype;
+    a.prior = prior; a.prior_dtype = prior_dtype;
+    a.alpha = alpha; a.alpha_stride = alpha_stride;
+    a.beta = beta; a.beta_stride = beta_stride;
+    a.M = (int)M; a.r = (int)r; a.V = (int)V;
+    a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
+    return a;
+}
+
+static int enqueue_markov(const dels_markov_rollout* p, hipStream_t s) {
+    const size_t esz = dtype_size(p->base_dtype);
+    const int64_t ldbase = p->ld_base ? p->ld_base : p->steps * p->V;
+    for (int64_t step = 0; step < p->steps; ++step) {
+        // token_s: the previous token for the first step, then the step before's pick
+        const int64_t* tok = step == 0 ? p->prev_ids : p->out_ids + (step - 1);
+        const int64_t tok_stride = step == 0 ? 1 : p->steps;
+        ArgmaxArgs a = gather_args(tok, tok_stride, p->embedding, p->ld_embedding, p->table_rows, p->lm_w, p->r,
+                                   p->lm_layout, static_cast<const char*>(p->base) + (size_t)step * p->V * esz,
+                                   ldbase, p->base_dtype, p->prior, p->prior_dtype, p->alpha + step, 0,
+                                   p->beta + step, 0, p->batch, p->r, p->V, p->out_ids + step,
+                                   p->out_scores ? p->out_scores + step : nullptr, p->steps);
+        hipError_t e = launch_fused_argmax(a, p->ws, kDataOff, s);
+        if (e != hipSuccess) return hip_fail(e, "Markov argmax launch");
+    }
+    return DELS_OK;
+}
+
 // ---- scratch of the allocation-free draft step ------------------------------------
 //
 // dels_lowrank_argmax_noalloc runs dels_lowrank_argmax with its workspace in
@@ -722,34 +810,48 @@ int dels_graph_create(const dels_rollout* p, void** graph_out) {
     *graph_out = nullptr;
     int rc = check_rollout(p);
     if (rc != DELS_OK) return rc;
-    hipStream_t cs = nullptr;
-    hipError_t e = hipStreamCreateWithFlags(&cs, hipStreamNonBlocking);
-    if (e != hipSuccess) return hip_fail(e, "capture stream creation");
-    // One eager pass first: resolves per-kernel launch configuration outside capture.
-    rc = enqueue_rollout(p, cs);
-    if (rc == DELS_OK && (e = hipStreamSynchronize(cs)) != hipSuccess) rc = hip_fail(e, "warm-up rollout");
-    hipGraph_t graph = nullptr;
-    if (rc == DELS_OK) {
-        e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
-        if (e != hipSuccess) {
-            rc = hip_fail(e, "hipStreamBeginCapture");
-        } else {
-            rc = enqueue_rollout(p, cs);
-            hipError_t e2 = hipStreamEndCapture(cs, &graph);
-            if (rc == DELS_OK && e2 != hipSuccess) rc = hip_fail(e2, "hipStreamEndCapture");
-        }
-    }
-    hipGraphExec_t exec = nullptr;
-    if (rc == DELS_OK && (e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess)
-        rc = hip_fail(e, "hipGraphInstantiate");
-    (void)hipStreamDestroy(cs);
-    if (rc != DELS_OK) {
-        if (graph) (void)hipGraphDestroy(graph);
-        return rc;
-    }
-    GraphHandle* hdl = new GraphHandle{graph, exec};
-    *graph_out = hdl;
-    return DELS_OK;
+    return capture_graph([p](hipStream_t s) { return enqueue_rollout(p, s); }, graph_out);
+}
+
+size_t dels_gather_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) { return dels_fused_argmax_ws_bytes(M, r, V); }
+
+int dels_gather_argmax(const int64_t* tokens, int64_t tok_stride, const void* E, int64_t lde, int64_t table_rows,
+                       const void* B, int64_t ldb, int b_layout, const void* base, int64_t ldbase, int base_dtype,
+                       const void* prior, int prior_dtype, const float* alpha, int64_t alpha_stride,
+                       const float* beta, int64_t beta_stride, int64_t M, int64_t r, int64_t V, int64_t* out_ids,
+                       float* out_score, int64_t ld_out, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_argmax_args(nullptr, r, B, ldb, b_layout, base, ldbase, base_dtype, prior, prior_dtype, alpha,
+                               alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, false);
+    if (rc != DELS_OK) return rc;
+    if (M == 0) return DELS_OK;
+    if (!tokens) return fail(DELS_ERR_INVALID_ARGUMENT, "token ids pointer is NULL");
+    if (table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "embedding table is empty");
+    if ((rc = check_bf16_matrix(E, lde, r, "E (embedding table)")) != DELS_OK) return rc;
+    if ((rc = check_ws(ws, ws_bytes, dels_gather_argmax_ws_bytes(M, r, V))) != DELS_OK) return rc;
+    ArgmaxArgs a = gather_args(tokens, tok_stride, E, lde, table_rows, B, ldb, b_layout, base, ldbase, base_dtype,
+                               prior, prior_dtype, alpha, alpha_stride, beta, beta_stride, M, r, V, out_ids,
+                               out_score, ld_out);
+    hipError_t e = launch_fused_argmax(a, ws, kDataOff, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "gather argmax launch");
+}
+
+size_t dels_markov_rollout_ws_bytes(int64_t batch, int64_t r, int64_t V) {
+    return kDataOff + align256(argmax_data_bytes(std::max<int64_t>(batch, 1), std::max<int64_t>(r, 1),
+                                                 std::max<int64_t>(V, 1)));
+}
+
+int dels_markov_rollout_enqueue(const dels_markov_rollout* p, void* stream) {
+    int rc = check_markov(p);
+    if (rc != DELS_OK) return rc;
+    return enqueue_markov(p, static_cast<hipStream_t>(stream));
+}
+
+int dels_markov_graph_create(const dels_markov_rollout* p, void** graph_out) {
+    if (!graph_out) return fail(DELS_ERR_INVALID_ARGUMENT, "graph_out is NULL");
+    *graph_out = nullptr;
+    int rc = check_markov(p);
+    if (rc != DELS_OK) return rc;
+    return capture_graph([p](hipStream_t s) { return enqueue_markov(p, s); }, graph_out);
 }
 
 int dels_graph_launch(void* graph, void* stream) {

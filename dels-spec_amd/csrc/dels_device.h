@@ -79,6 +79,16 @@ __device__ __forceinline__ unsigned long long pack_argmax(float v, uint32_t idx)
     return ((unsigned long long)f32_order_key(v) << 32) | (unsigned long long)(~idx);
 }
 
+// Row of the rank matrix that draft row m reads: m itself, or -- when the rank
+// is gathered from a table (the embedding rows of a Markov step) -- the token
+// id rows[m * stride], clamped into [0, count) as an embedding lookup's index
+// must lie.
+__device__ __forceinline__ int64_t rank_row_of(const int64_t* rows, int64_t stride, int64_t count, int m) {
+    if (rows == nullptr) return m;
+    const int64_t t = rows[(int64_t)m * stride];
+    return t < 0 ? 0 : (t >= count ? count - 1 : t);
+}
+
 // Candidate (v, i) beats (bv, bi): larger value, or equal value and lower index.
 __device__ __forceinline__ bool argmax_better(float v, int i, float bv, int bi) {
     return (v > bv) || (v == bv && i < bi);

@@ -86,6 +86,10 @@ hipError_t launch_gru_step(const GruArgs& a, const SkinnyPlan& p, void* ws, size
 
 struct ArgmaxArgs {
     const uint16_t* rank; int64_t ldrank;
+    // non-null: row m of the rank is row rank_rows[m * rank_rows_stride] of the
+    // [rank_rows_count, r] table `rank` (bf16 argmax only)
+    const int64_t* rank_rows = nullptr;
+    int64_t rank_rows_stride = 0, rank_rows_count = 0;
     const uint16_t* B; int64_t ldb; bool b_packed;
     const float* b_scale = nullptr;   // non-null: B is e4m3 in K128 blocks, this its per-row scale [V]
     const void* base; int64_t ldbase; int base_dtype;

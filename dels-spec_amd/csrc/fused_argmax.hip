@@ -59,6 +59,7 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
         tiled_grid(a.M, a.V, kPlanCUs, &gx, &gy);
         TiledKArgs ka{};
         ka.rank = a.rank; ka.ldrank = a.ldrank;
+        ka.rank_rows = a.rank_rows; ka.rank_rows_stride = a.rank_rows_stride; ka.rank_rows_count = a.rank_rows_count;
         ka.B = a.B;
         ka.base = a.base; ka.ldbase = a.ldbase;
         ka.prior = a.prior;
@@ -80,6 +81,7 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
     }
     ArgmaxKArgs ka{};
     ka.rank = a.rank; ka.ldrank = a.ldrank;
+    ka.rank_rows = a.rank_rows; ka.rank_rows_stride = a.rank_rows_stride; ka.rank_rows_count = a.rank_rows_count;
     ka.B = a.B; ka.ldb = a.ldb;
     ka.base = a.base; ka.ldbase = a.ldbase;
     ka.prior = a.prior;

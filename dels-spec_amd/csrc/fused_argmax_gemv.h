@@ -40,6 +40,8 @@ namespace dels {
 
 struct ArgmaxKArgs {
     const uint16_t* rank; int64_t ldrank;
+    const int64_t* rank_rows;   // non-null: row m of the rank is rank[rank_rows[m * rank_rows_stride]]
+    int64_t rank_rows_stride, rank_rows_count;
     const uint16_t* B; int64_t ldb;     // [V, r] row-major, or MFMA-16 blocks
     const void* base; int64_t ldbase;
     const void* prior;
@@ -201,7 +203,8 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
     {
         const int mrow = m0 + col;
         const bool mok = mrow < a.M;
-        const uint16_t* rp = a.rank + (int64_t)(mok ? mrow : 0) * a.ldrank;
+        const uint16_t* rp =
+            a.rank + rank_row_of(a.rank_rows, a.rank_rows_stride, a.rank_rows_count, mok ? mrow : 0) * a.ldrank;
 #pragma unroll
         for (int s = 0; s < KSTEPS; ++s) {
             const int k = s * 32 + kg * 8;

@@ -64,6 +64,8 @@ namespace dels {
 
 struct TiledKArgs {
     const uint16_t* rank; int64_t ldrank;
+    const int64_t* rank_rows;   // non-null: row m of the rank is rank[rank_rows[m * rank_rows_stride]]
+    int64_t rank_rows_stride, rank_rows_count;
     const uint16_t* B;          // MFMA-16 blocks, r a multiple of 32 (e4m3 kernel: K128 blocks)
     const float* b_scale;       // e4m3 kernel only: per-row scale of B
     const uint8_t* rank_q;      // e4m3 kernel only: the rank quantised per row [M][ldrank bytes]
@@ -248,7 +250,8 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
         const int mrow = min(mw + 32 * rb + rl, a.M - 1);
-        const uint16_t* rp = a.rank + (int64_t)mrow * a.ldrank + h * 8;
+        const uint16_t* rp =
+            a.rank + rank_row_of(a.rank_rows, a.rank_rows_stride, a.rank_rows_count, mrow) * a.ldrank + h * 8;
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) ra[rb][s] = load_bf16x8(rp + s * 16);
         al[rb] = a.alpha[(int64_t)mrow * a.alpha_stride];

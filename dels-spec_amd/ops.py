@@ -12,6 +12,8 @@ Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
   * ``lowrank_argmax`` -- the two above, one draft step, code/kernel/dels.py:437-446
   * ``gru_step``       -- _gru_cell / _fused_gru_cell_kernel with the input-table
                           gather, code/kernel/dels.py:140-211, 359-373, 432, 461
+  * ``gather_argmax``  -- a Markov step: F.embedding + _fused_markov_argmax_kernel +
+                          _reduce_argmax_kernel, code/kernel/markov_dels.py:15-138, 216-268
 """
 
 from __future__ import annotations
@@ -325,6 +327,43 @@ def lowrank_argmax(h: torch.Tensor, rank_weight: Weight, lm_head_weight: Weight,
     return out_ids, out_score
 
 
+
+
+def gather_argmax(tokens: torch.Tensor, embedding: torch.Tensor, lm_head_weight: Weight, base_logits: torch.Tensor,
+                  baseline_logits: Optional[torch.Tensor] = None, alpha: Scalars = 1.0, beta: Scalars = 0.0,
+                  *, out_ids: Optional[torch.Tensor] = None,
+                  out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One Markov DeLS step: ``fused_argmax`` with the rank gathered from a table,
+    ``rank = F.embedding(tokens, embedding)`` (code/kernel/markov_dels.py:216-268).
+
+    ``tokens`` [M] int64 (a strided view is fine; ids are clamped to the table);
+    ``embedding`` [rows, r] bf16 row-major; the rest as ``fused_argmax``.
+    """
+    _require_cuda(tokens, "tokens")
+    if tokens.dtype != torch.int64:
+        raise TypeError("tokens must be int64")
+    if tokens.dim() != 1:
+        tokens = tokens.reshape(-1)
+    M = tokens.numel()
+    _require_bf16_matrix(embedding, "embedding")
+    rows, r = embedding.shape
+    b_ptr, ldb, b_lay, V, _ = _weight(lm_head_weight, "lm_head_weight", cols=r)
+    base = _base_view(base_logits, M, V)
+    prior = _prior_view(baseline_logits, V)
+    dev = tokens.device
+    a, a_s = _rows_param(alpha, M, dev, "alpha")
+    b, b_s = _rows_param(beta, M, dev, "beta")
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_gather_argmax_ws_bytes(M, r, V))
+    _lib.check(lib.dels_gather_argmax(
+        tokens.data_ptr(), tokens.stride(0), embedding.data_ptr(), embedding.stride(0), rows, b_ptr, ldb, b_lay,
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype],
+        prior.data_ptr() if prior is not None else None, _DTYPES[prior.dtype] if prior is not None else 0,
+        a.data_ptr(), a_s, b.data_ptr(), b_s, M, r, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out,
+        ws.data_ptr(), ws.numel(), _stream_ptr(dev)), "dels_gather_argmax")
+    return out_ids, out_score
 
 
 def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,

@@ -313,10 +313,65 @@ int dels_rollout_enqueue(const dels_rollout* p, void* stream);
  * hipGraph of the rollout: replaces the torch.cuda.CUDAGraph capture and
  * replay of DeLSGraphRunner (code/kernel/dels.py:320-329, 477).  The graph
  * bakes in the pointers of `p`; the handle owns only the graph objects.
+ * dels_graph_launch and dels_graph_destroy also take the handles of
+ * dels_markov_graph_create.
  */
 int dels_graph_create(const dels_rollout* p, void** graph_out);
 int dels_graph_launch(void* graph, void* stream);
 int dels_graph_destroy(void* graph);
+
+/*
+ * Markov DeLS step: the rank of row m is a row of a table, rank_m =
+ * E[tokens[m]] (F.embedding(current_token, embedding_weight)), followed by the
+ * fused argmax of dels_fused_argmax.  Replaces _fused_markov_argmax_kernel +
+ * _reduce_argmax_kernel with the embedding gather of
+ * MarkovDeLSGraphRunner._forward_impl (code/kernel/markov_dels.py:15-138,
+ * 216-258, 261-268); the gather is the kernels' rank load, no separate launch.
+ *   tokens[m*tok_stride] int64, clamped to [0, table_rows);
+ *   E [table_rows, r] bf16 row-major (lde % 8 == 0, 16-byte aligned);
+ *   the rest as dels_fused_argmax (B [V, r] bf16 in b_layout).
+ */
+size_t dels_gather_argmax_ws_bytes(int64_t M, int64_t r, int64_t V);
+int dels_gather_argmax(const int64_t* tokens, int64_t tok_stride, const void* E, int64_t lde,
+                       int64_t table_rows, const void* B, int64_t ldb, int b_layout,
+                       const void* base, int64_t ldbase, int base_dtype,
+                       const void* prior, int prior_dtype,
+                       const float* alpha, int64_t alpha_stride,
+                       const float* beta, int64_t beta_stride,
+                       int64_t M, int64_t r, int64_t V,
+                       int64_t* out_ids, float* out_score, int64_t ld_out,
+                       void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * The Markov rollout of MarkovDeLSGraphRunner._forward_impl
+ * (code/kernel/markov_dels.py:261-278): token_0 = prev_ids; for each step s,
+ * out_ids[:, s] = dels_gather_argmax(token_s) against base[:, s, :] with
+ * alpha[s]/beta[s], and token_{s+1} = out_ids[:, s].  One launch per step.
+ */
+typedef struct dels_markov_rollout {
+    const void* embedding;  /* [table_rows, r] bf16 row-major */
+    int64_t ld_embedding;
+    int64_t table_rows;
+    const void* lm_w;       /* [V, r] bf16 */
+    int lm_layout;          /* DELS_LAYOUT_ROWMAJOR (ld = r) or DELS_LAYOUT_MFMA16 */
+    const void* prior;      /* [V] or NULL */
+    int prior_dtype;
+    const float* alpha;     /* [steps] fp32 */
+    const float* beta;      /* [steps] fp32 */
+    int64_t batch, steps, r, V;
+    const int64_t* prev_ids; /* [batch] int64 */
+    const void* base;       /* [batch, steps, V]: row b, step s at base + (b * ld_base + s * V) */
+    int base_dtype;
+    int64_t ld_base;        /* elements between batch rows of base (0: steps * V) */
+    int64_t* out_ids;       /* [batch, steps] int64 */
+    float* out_scores;      /* [batch, steps] fp32 or NULL */
+    void* ws;
+    size_t ws_bytes;
+} dels_markov_rollout;
+
+size_t dels_markov_rollout_ws_bytes(int64_t batch, int64_t r, int64_t V);
+int dels_markov_rollout_enqueue(const dels_markov_rollout* p, void* stream);
+int dels_markov_graph_create(const dels_markov_rollout* p, void** graph_out);
 
 #ifdef __cplusplus
 }

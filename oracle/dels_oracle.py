@@ -55,6 +55,7 @@ __all__ = [
     "gru_input_table",
     "gru_cell",
     "rollout",
+    "markov_rollout",
     "unigram_log_prior",
     "rank_proj_fp8",
     "fused_argmax_fp8",
@@ -381,6 +382,31 @@ def rollout(prefix_ids, base, *, gi_table=None, W_hh, b_hh, A, rank_bias, act, B
         tok = i if forced_ids is None else np.asarray(forced_ids, np.int64)[:, s]
         if s + 1 < steps:
             h = gru_cell(gi_rows(tok), h, W_hh, b_hh)
+    return ids, scores, seconds
+
+
+def markov_rollout(prev_ids, base, *, E, B, prior, alphas, betas, forced_ids=None):
+    """The Markov DeLS rollout (code/kernel/markov_dels.py:261-278).
+
+    ``token_0 = prev_ids``; for each step s the rank is the table row
+    ``E[token_s]`` (F.embedding; ids clamped into the table), the fused argmax
+    against ``base[:, s]`` with ``alphas[s]``/``betas[s]`` picks ``out[:, s]``,
+    and ``token_{s+1} = out[:, s]`` (or ``forced_ids[:, s]``, teacher forcing).
+    Returns ``(ids, scores, seconds)``, each ``[batch, steps]``.
+    """
+    tok = np.asarray(prev_ids, np.int64).reshape(-1)
+    base = np.asarray(base, _F32)
+    E = np.asarray(E, _F32)
+    nb, steps, V = base.shape
+    ids = np.zeros((nb, steps), np.int64)
+    scores = np.zeros((nb, steps), _F32)
+    seconds = np.zeros((nb, steps), _F32)
+    for s in range(steps):
+        rank = E[np.clip(tok, 0, E.shape[0] - 1)]
+        i, sc, sec = fused_argmax(rank, B, base[:, s, :], prior, np.full(nb, alphas[s], _F32),
+                                  np.full(nb, betas[s], _F32))
+        ids[:, s], scores[:, s], seconds[:, s] = i, sc, sec
+        tok = i if forced_ids is None else np.asarray(forced_ids, np.int64)[:, s]
     return ids, scores, seconds
 
 

@@ -203,6 +203,28 @@ def test_runner_argument_checks(pkg, kwargs, msg):
         pkg.DeLSGraphRunner(**args)
 
 
+class _MarkovHead:
+    vocab_size = 10
+    embedding_weight = None
+    lm_head_weight = None
+
+
+@pytest.mark.parametrize("kwargs,msg", [
+    (dict(steps=0, alpha_values=[], beta_values=[]), "requires steps > 0"),
+    (dict(alpha_values=[0.1]), "alpha/beta schedules must match steps"),
+    (dict(vocab_size=11), "local-head vocab size mismatch"),
+    (dict(beta_values=[0.0, 0.2, 0.0], baseline_logits=None), "requires baseline_logits when any beta is nonzero"),
+    (dict(device="cpu"), "no CPU fallback"),
+])
+def test_markov_runner_argument_checks(pkg, kwargs, msg):
+    """MarkovDeLSGraphRunner's checks (code/kernel/markov_dels.py:153-173) run before any device use."""
+    args = dict(local_head=_MarkovHead(), batch_size=1, steps=3, vocab_size=10, alpha_values=[0.1] * 3,
+                beta_values=[0.0] * 3, baseline_logits=None, device="cuda")
+    args.update(kwargs)
+    with pytest.raises(ValueError, match=msg):
+        pkg.MarkovDeLSGraphRunner(**args)
+
+
 def test_local_head_mirror_eager_methods(pkg):
     class Target:
         class model:

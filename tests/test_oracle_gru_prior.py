@@ -135,3 +135,37 @@ def test_fp8_oracle_reduces_to_bf16_with_unit_scales():
     raw = oracle.fused_argmax(rank, Bq * np.exp2(k)[:, None], base, None, 1e-6, 0.0)
     # the fp8 path quantises rank per row; with alpha tiny the base term dominates both
     np.testing.assert_array_equal(ids2, raw[0])
+
+
+# ------------------------------------------------------------------ Markov rollout
+
+def test_markov_rollout_follows_the_chain():
+    """Rows of E orthonormal and B[pi(t)] = 10 E[t]: from token t the low-rank logit is 10 at
+    pi(t) and 0 elsewhere, so with a small base every step moves t -> pi(t) and the rollout
+    visits pi^(s+1)(prev) -- a rollout feeding the wrong token (the previous one, or the
+    step's own input) would not."""
+    rng = np.random.default_rng(4)
+    V, r, nb, steps = 50, 64, 3, 6
+    Q, _ = np.linalg.qr(rng.standard_normal((r, r)))
+    E = Q[:V].astype(np.float32)
+    pi = rng.permutation(V)
+    B = np.zeros((V, r), np.float32)
+    B[pi] = 10 * E
+    base = (rng.standard_normal((nb, steps, V)) * 0.1).astype(np.float32)
+    prior = np.log(rng.dirichlet(np.ones(V))).astype(np.float32) * 0.01
+    prev = np.array([0, 7, 49])
+    ids, scores, _ = oracle.markov_rollout(prev, base, E=E, B=B, prior=prior, alphas=[1.0] * steps,
+                                           betas=[0.2] * steps)
+    want = np.zeros((nb, steps), np.int64)
+    t = prev.copy()
+    for s in range(steps):
+        t = pi[t]
+        want[:, s] = t
+    np.testing.assert_array_equal(ids, want)
+    assert np.all(scores > 9.0)
+    # teacher forcing: each step starts from the forced token
+    forced = rng.integers(0, V, (nb, steps))
+    fids, _, _ = oracle.markov_rollout(prev, base, E=E, B=B, prior=prior, alphas=[1.0] * steps,
+                                       betas=[0.2] * steps, forced_ids=forced)
+    np.testing.assert_array_equal(fids[:, 0], pi[prev])
+    np.testing.assert_array_equal(fids[:, 1:], pi[forced[:, :-1]])
