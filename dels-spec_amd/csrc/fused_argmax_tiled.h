@@ -193,7 +193,8 @@ constexpr uint32_t half_neg_inf() { return std::is_same<T, bf16_t>::value ? 0xff
 
 }  // namespace tiled
 
-template <int KS, typename BaseT, typename PriorT>
+// EXACT: V is a multiple of the 32-column tile, so no tile needs masking.
+template <int KS, typename BaseT, typename PriorT, bool EXACT>
 __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(TiledKArgs a) {
 #pragma clang fp contract(off)
     using namespace tiled;
@@ -243,9 +244,11 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     // Rank operand of the wave's rows, resident for the whole kernel; rows past
     // M repeat row M-1 (their results are not written).
     bf16x8 ra[kRowBlocks][kSteps];
-    float al[kRowBlocks], be[kRowBlocks], best[kRowBlocks];
+    float al[kRowBlocks], nbeta[kRowBlocks], best[kRowBlocks];
     int bidx[kRowBlocks];
-    bool use_prior[kRowBlocks];
+    // prior bits kept (the row uses the prior term) or cleared: fp32/f16 mask, the
+    // high half of a 16-bit pair, and the v_perm_b32 selector of the low half
+    uint32_t pmask[kRowBlocks], pmask_hi[kRowBlocks], psel_lo[kRowBlocks];
     uint32_t row_off[kRowBlocks];   // byte offset of the lane's base row (M * ldbase * size < 2^31)
 #pragma unroll
     for (int rb = 0; rb < kRowBlocks; ++rb) {
@@ -255,8 +258,13 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
 #pragma unroll
         for (int s = 0; s < kSteps; ++s) ra[rb][s] = load_bf16x8(rp + s * 16);
         al[rb] = a.alpha[(int64_t)mrow * a.alpha_stride];
-        be[rb] = a.beta[(int64_t)mrow * a.beta_stride];
-        use_prior[rb] = kPrior && be[rb] != 0.f;
+        const float be = a.beta[(int64_t)mrow * a.beta_stride];
+        // beta == 0 skips the prior term: fma(0, +0, sc) == sc, whatever the prior holds
+        const bool use_prior = kPrior && be != 0.f;
+        nbeta[rb] = use_prior ? -be : 0.f;
+        pmask[rb] = use_prior ? 0xffffffffu : 0u;
+        pmask_hi[rb] = use_prior ? 0xffff0000u : 0u;
+        psel_lo[rb] = use_prior ? 0x01000c0cu : 0x0c0c0c0cu;   // bytes 1,0 -> 3,2; zeros below
         best[rb] = -__builtin_inff();
         bidx[rb] = INT_MAX;
         row_off[rb] = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
                 const int v = min(vs + 8 * (2 * g + h), a.V - 8);
                 dma16(baseg, row_off[rb] + (uint32_t)v * 2u, dst);
             }
-        } else if constexpr (kPrior) {
+        } else if (kPrior && piece == nb + kRowBlocks * nbase) {
             if constexpr (sizeof(PriorT) == 4) {
                 const int v = min(vs + (lane & 31), a.V - 1);
                 dma4(priorg, (uint32_t)v * 4u, S.prior[wave]);
@@ -338,7 +346,7 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     auto load_epi_group = [&](const Stage& S, int st, int rb, int g, EpiRegs& e) {
         const int vs = tile_of(st) * kTileCols;
         const int v = vs + 8 * g + 4 * h;   // column of candidate 4g
-        const bool partial = vs + kTileCols > a.V;   // only the last tile of the vocabulary
+        const bool partial = !EXACT && vs + kTileCols > a.V;   // only the last tile of the vocabulary
         if constexpr (sizeof(BaseT) == 4) {
             const u32x4 w = *reinterpret_cast<const u32x4*>(S.base[wave] + rb * kBaseRB + g * 1024 + lane * 16);
 #pragma unroll
@@ -375,29 +383,35 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
         if constexpr (sizeof(BaseT) == 4) return __uint_as_float(w);
         else return half_at<BaseT>(w, j & 1);
     };
-    auto word_to_prior = [&](uint32_t w, int j) -> float {
-        if constexpr (sizeof(PriorT) == 4) return __uint_as_float(w);
-        else return half_at<PriorT>(w, j & 1);
+    // Prior value of candidate j, as +0 for rows without the prior term.
+    auto masked_prior = [&](uint32_t w, int j, int rb) -> float {
+        if constexpr (sizeof(PriorT) == 4) {
+            return __uint_as_float(w & pmask[rb]);
+        } else if constexpr (std::is_same<PriorT, bf16_t>::value) {
+            return __uint_as_float((j & 1) ? (w & pmask_hi[rb]) : __builtin_amdgcn_perm(w, w, psel_lo[rb]));
+        } else {
+            return __uint_as_float(__float_as_uint(half_at<PriorT>(w, j & 1)) & pmask[rb]);
+        }
     };
     // Candidate j of row block rb of stage stp.
     // The empty volatile asm statements pin the candidate's work to its place
     // between the MFMAs: pure arithmetic is otherwise free to be gathered
     // after the last MFMA of the stage, which is where the compiler puts it.
-    auto epi_one = [&](const f32x16 (&accp)[kRowBlocks], const EpiRegs& e, int stp, int rb, int j) {
+    // They pin values just extracted, so that no register is copied for them.
+    auto epi_one = [&](const f32x16 (&accp)[kRowBlocks], const EpiRegs& e, int sidx, int rb, int j) {
         float av = accp[rb][j];
-        uint32_t bw = e.b[rb][sizeof(BaseT) == 4 ? j : (j >> 1)];
-        asm volatile("" : "+v"(av), "+v"(bw));
-        float sc = __builtin_fmaf(av, al[rb], word_to_base(bw, j));
+        float bv = word_to_base(e.b[rb][sizeof(BaseT) == 4 ? j : (j >> 1)], j);
+        asm volatile("" : "+v"(av), "+v"(bv));
+        float sc = __builtin_fmaf(av, al[rb], bv);
         if constexpr (kPrior) {
-            uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
-            asm volatile("" : "+v"(pw));
-            const float scp = __builtin_fmaf(-be[rb], word_to_prior(pw, j), sc);
-            sc = use_prior[rb] ? scp : sc;
+            float pv = masked_prior(e.p[sizeof(PriorT) == 4 ? j : (j >> 1)], j, rb);
+            asm volatile("" : "+v"(pv));
+            sc = __builtin_fmaf(nbeta[rb], pv, sc);
         }
         // candidates arrive in increasing index order: strict ">" keeps the lowest index
         const bool take = sc > best[rb];
         best[rb] = take ? sc : best[rb];
-        bidx[rb] = take ? stp * 16 + j : bidx[rb];
+        bidx[rb] = take ? sidx + j : bidx[rb];
         asm volatile("" : "+v"(best[rb]), "+v"(bidx[rb]));
     };
 
@@ -432,7 +446,7 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
                 // candidates c in [slot * kCands / kSlots, (slot + 1) * kCands / kSlots): row block c / 16, j = c % 16
 #pragma unroll
                 for (int c = slot * kCands / kSlots; c < (slot + 1) * kCands / kSlots; ++c) {
-                    epi_one(accp, ep, stp, c >> 4, c & 15);
+                    epi_one(accp, ep, stp * 16, c >> 4, c & 15);
                     if ((c & 3) == 3) load_epi_group(S, st, c >> 4, (c & 15) >> 2, ep_next);
                 }
 #pragma unroll
@@ -501,7 +515,7 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     if (wave_active && nst > 0) {
         // the epilogue of the last stage
 #pragma unroll
-        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, st_prev, c >> 4, c & 15);
+        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, st_prev * 16, c >> 4, c & 15);
     }
 
     // Decode the candidate slot st*16 + j into the vocabulary index, then merge
@@ -543,8 +557,12 @@ inline void tiled_grid(int M, int V, int cus, int* gx, int* gy) {
 
 template <int KS, typename BaseT, typename PriorT>
 hipError_t launch_tiled_inst(const TiledKArgs& ka, int gx, int gy, hipStream_t s) {
-    hipLaunchKernelGGL((fused_argmax_tiled_kernel<KS, BaseT, PriorT>), dim3(gx, gy, 1), dim3(tiled::kThreads), 0,
-                       s, ka);
+    if (ka.V % tiled::kTileCols == 0)
+        hipLaunchKernelGGL((fused_argmax_tiled_kernel<KS, BaseT, PriorT, true>), dim3(gx, gy, 1),
+                           dim3(tiled::kThreads), 0, s, ka);
+    else
+        hipLaunchKernelGGL((fused_argmax_tiled_kernel<KS, BaseT, PriorT, false>), dim3(gx, gy, 1),
+                           dim3(tiled::kThreads), 0, s, ka);
     return hipGetLastError();
 }
 

@@ -68,7 +68,8 @@ __device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8
 
 }  // namespace tiled8
 
-template <int KS8, typename BaseT, typename PriorT>
+// EXACT: V is a multiple of the 32-column tile, so no tile needs masking.
+template <int KS8, typename BaseT, typename PriorT, bool EXACT>
 __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(TiledKArgs a) {
 #pragma clang fp contract(off)
     using namespace tiled8;
@@ -124,7 +125,11 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     const float sR = a.rank_scale[mrow];
     const float al = a.alpha[(int64_t)mrow * a.alpha_stride];
     const float be = a.beta[(int64_t)mrow * a.beta_stride];
+    // beta == 0 skips the prior term: fma(0, +0, sc) == sc, whatever the prior holds
     const bool use_prior = kPrior && be != 0.f;
+    const float nbeta = use_prior ? -be : 0.f;
+    const uint32_t pmask = use_prior ? 0xffffffffu : 0u, pmask_hi = use_prior ? 0xffff0000u : 0u;
+    const uint32_t psel_lo = use_prior ? 0x01000c0cu : 0x0c0c0c0cu;   // v_perm_b32: bytes 1,0 -> 3,2
     float best = -__builtin_inff();
     int bidx = INT_MAX;
     const uint32_t row_off = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
@@ -194,7 +199,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     auto load_epi_group = [&](const Stage& S, int st, int g, EpiRegs& e) {
         const int vs = tile_of(st) * kTileCols;
         const int v = vs + 8 * g + 4 * h;
-        const bool partial = vs + kTileCols > a.V;
+        const bool partial = !EXACT && vs + kTileCols > a.V;
         if constexpr (sizeof(BaseT) == 4) {
             const u32x4 w = *reinterpret_cast<const u32x4*>(S.base[wave] + g * 1024 + lane * 16);
 #pragma unroll
@@ -242,10 +247,13 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
         float sc = __builtin_fmaf(dot, al, bv);
         if constexpr (kPrior) {
             const uint32_t pw = e.p[sizeof(PriorT) == 4 ? j : (j >> 1)];
-            float pv = sizeof(PriorT) == 4 ? __uint_as_float(pw) : tiled::half_at<PriorT>(pw, j & 1);
+            float pv;   // the prior value, or +0 for a row without the prior term
+            if constexpr (sizeof(PriorT) == 4) pv = __uint_as_float(pw & pmask);
+            else if constexpr (std::is_same<PriorT, bf16_t>::value)
+                pv = __uint_as_float((j & 1) ? (pw & pmask_hi) : __builtin_amdgcn_perm(pw, pw, psel_lo));
+            else pv = __uint_as_float(__float_as_uint(tiled::half_at<PriorT>(pw, j & 1)) & pmask);
             asm volatile("" : "+v"(pv));
-            const float scp = __builtin_fmaf(-be, pv, sc);
-            sc = use_prior ? scp : sc;
+            sc = __builtin_fmaf(nbeta, pv, sc);
         }
         const bool take = sc > best;   // candidates arrive in increasing index order
         best = take ? sc : best;
@@ -366,8 +374,12 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
 
 template <int KS8, typename BaseT, typename PriorT>
 hipError_t launch_tiled8_inst(const TiledKArgs& ka, int gx, int gy, hipStream_t s) {
-    hipLaunchKernelGGL((fused_argmax_tiled8_kernel<KS8, BaseT, PriorT>), dim3(gx, gy, 1), dim3(tiled8::kThreads),
-                       0, s, ka);
+    if (ka.V % tiled8::kTileCols == 0)
+        hipLaunchKernelGGL((fused_argmax_tiled8_kernel<KS8, BaseT, PriorT, true>), dim3(gx, gy, 1), dim3(tiled8::kThreads),
+                           0, s, ka);
+    else
+        hipLaunchKernelGGL((fused_argmax_tiled8_kernel<KS8, BaseT, PriorT, false>), dim3(gx, gy, 1), dim3(tiled8::kThreads),
+                           0, s, ka);
     return hipGetLastError();
 }
 
