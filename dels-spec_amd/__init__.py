@@ -15,6 +15,8 @@ Public surface (mirrors the reference's interface for this path):
     kernels stream at full HBM bandwidth
   * ``quantize_pack_fp8``, ``fused_argmax_fp8``, ``lowrank_argmax_fp8`` -- the
     fp8 (e4m3 weights, per-channel scales) variant of the same step
+  * ``sample`` (and ``argmax_rows``, ``sample_rows``) -- the reference's
+    ``sample(logits, temperature)``: argmax, or one softmax draw per row
 """
 
 from .checkpoints import detect_local_head_checkpoint_kind
@@ -22,7 +24,8 @@ from .local_head import (DeLSLocalHead, MarkovDeLSLocalHead, PositionMixJointHea
                          parse_scalar_schedule, unigram_log_prior_from_counts)
 from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gather_argmax, gru_step,
                   lowrank_argmax, lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows,
-                  quantize_pack_fp8, rank_proj)
+                  quantize_pack_fp8, rank_proj, sample_rows)
+from .sampling import sample
 from .draft_step import DeLSDraftStep
 from .runner import DeLSGraphRunner
 from .markov_runner import MarkovDeLSGraphRunner
@@ -34,6 +37,8 @@ __all__ = [
     "gather_argmax",
     "DeLSDraftStep",
     "argmax_rows",
+    "sample_rows",
+    "sample",
     "DeLSLocalHead",
     "MarkovDeLSLocalHead",
     "PositionMixJointHead",

@@ -107,6 +107,9 @@ SIGNATURES = {
     "dels_markov_graph_create": (_int, [ctypes.POINTER(MarkovRolloutParams), ctypes.POINTER(_ptr)]),
     "dels_argmax_rows_ws_bytes": (_sz, [_i64, _i64]),
     "dels_argmax_rows": (_int, [_ptr, _i64, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_sample_rows_ws_bytes": (_sz, [_i64, _i64]),
+    "dels_sample_rows": (_int, [_ptr, _i64, _int, _i64, _i64, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, _ptr,
+                                _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_packed_fp8_bytes": (_sz, [_i64, _i64, _int]),
     "dels_pack_operand_fp8": (_int, [_ptr, _i64, _i64, _i64, _int, _ptr, _sz, _ptr]),
     "dels_fused_argmax_fp8_ws_bytes": (_sz, [_i64, _i64, _i64]),

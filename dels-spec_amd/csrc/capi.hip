@@ -765,6 +765,33 @@ int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
     return e == hipSuccess ? DELS_OK : hip_fail(e, "argmax rows launch");
 }
 
+size_t dels_sample_rows_ws_bytes(int64_t, int64_t) { return kDataOff; }
+
+int dels_sample_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V, float temperature, uint64_t seed,
+                     uint64_t offset, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws, size_t ws_bytes,
+                     void* stream) {
+    if (!(temperature == temperature) || temperature == __builtin_inff())
+        return fail(DELS_ERR_INVALID_ARGUMENT, "temperature must be finite");
+    // sample() takes the argmax below 1e-5 (code/dflash.py:32-33)
+    if (temperature < 1e-5f)
+        return dels_argmax_rows(x, ldx, dtype, M, V, out_ids, out_score, ld_out, ws, ws_bytes, stream);
+    if (M < 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape M=%lld V=%lld", (long long)M, (long long)V);
+    if (M > kMaxKeyRows || V >= INT32_MAX) return fail(DELS_ERR_UNSUPPORTED, "sample rows: M <= %d and V < 2^31-1",
+                                                       kMaxKeyRows);
+    if (M == 0) return DELS_OK;
+    if (!x) return fail(DELS_ERR_INVALID_ARGUMENT, "logits pointer is NULL");
+    if (!valid_dtype(dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown logits dtype %d", dtype);
+    if (M > 1 && ldx < V) return fail(DELS_ERR_INVALID_ARGUMENT, "logits leading dimension %lld < V %lld",
+                                      (long long)ldx, (long long)V);
+    if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+    if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    int rc = check_ws(ws, ws_bytes, kDataOff);
+    if (rc != DELS_OK) return rc;
+    hipError_t e = launch_sample_rows(x, ldx, dtype, (int)M, (int)V, temperature, seed, offset, out_ids, out_score,
+                                      ld_out, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "sample rows launch");
+}
+
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {
     return kDataOff + skinny_data_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1),
                                                       std::max<int64_t>(G, 1), true));

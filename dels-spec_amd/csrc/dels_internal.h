@@ -110,6 +110,12 @@ hipError_t launch_fused_argmax(const ArgmaxArgs& a, void* ws, size_t data_off, h
 hipError_t launch_argmax_rows(const void* x, int64_t ldx, int dtype, int M, int V, int64_t* out_ids,
                               float* out_score, int64_t ld_out, void* ws, hipStream_t s);
 
+// Temperature sampling of logits [M, V] (dtype as launch_argmax_rows): Gumbel-max
+// over Philox4x32-10 bits at counter (v/4, m, offset) and key seed; M <= kMaxKeyRows.
+hipError_t launch_sample_rows(const void* x, int64_t ldx, int dtype, int M, int V, float temperature, uint64_t seed,
+                              uint64_t offset, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws,
+                              hipStream_t s);
+
 // fp8 argmax (b_scale set): r in {128, 256, 512}, any M up to kMaxKeyRows.
 bool argmax_fp8_supported(int64_t M, int64_t r);
 size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V);

@@ -14,6 +14,8 @@ Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
                           gather, code/kernel/dels.py:140-211, 359-373, 432, 461
   * ``gather_argmax``  -- a Markov step: F.embedding + _fused_markov_argmax_kernel +
                           _reduce_argmax_kernel, code/kernel/markov_dels.py:15-138, 216-268
+  * ``argmax_rows`` / ``sample_rows`` -- sample() at temperature 0 / above 0,
+                          code/dflash.py:31-38
 """
 
 from __future__ import annotations
@@ -387,6 +389,35 @@ def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,
     _lib.check(lib.dels_argmax_rows(logits.data_ptr(), logits.stride(0), _DTYPES[logits.dtype], M, V,
                                     out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(),
                                     _stream_ptr(logits.device)), "dels_argmax_rows")
+    return out_ids, out_score
+
+
+def sample_rows(logits: torch.Tensor, temperature: float, seed: int, offset: int = 0, *,
+                out_ids: Optional[torch.Tensor] = None,
+                out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One draw per row from ``softmax(logits / temperature)`` (code/dflash.py:31-38).
+
+    A Gumbel-max over Philox4x32-10 noise keyed by ``seed`` (64 bits) at counter
+    ``(v // 4, row, offset)``: the ids depend only on ``(seed, offset, row,
+    logits)``.  ``temperature < 1e-5`` is ``argmax_rows``, as in the reference.
+    ``logits`` [M, V] (unit column stride) fp32/bf16/fp16.  Returns
+    ``(ids int64[M], score fp32[M])``, the score being the winning
+    ``logits / temperature + gumbel`` value."""
+    if logits.dim() == 1:
+        logits = logits.unsqueeze(0)
+    _require_cuda(logits, "logits")
+    if logits.dtype not in _DTYPES:
+        raise TypeError(f"logits must be float32, bfloat16 or float16, got {logits.dtype}")
+    if logits.dim() != 2 or (logits.shape[1] > 1 and logits.stride(1) != 1):
+        raise ValueError("logits must be an [M, V] matrix with unit column stride")
+    M, V = logits.shape
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, logits.device)
+    lib = _lib.load()
+    ws = workspace(logits.device, lib.dels_sample_rows_ws_bytes(M, V))
+    _lib.check(lib.dels_sample_rows(logits.data_ptr(), logits.stride(0), _DTYPES[logits.dtype], M, V,
+                                    float(temperature), int(seed) & (2**64 - 1), int(offset) & (2**64 - 1),
+                                    out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(),
+                                    _stream_ptr(logits.device)), "dels_sample_rows")
     return out_ids, out_score
 
 

@@ -208,6 +208,25 @@ int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
                      void* ws, size_t ws_bytes, void* stream);
 
 /*
+ * dels_sample_rows: sample() at temperature > 0 (code/dflash.py:31-38:
+ * softmax(logits / T) then torch.multinomial, one draw per row), for logits
+ * [M, V] (dtype and layout as dels_argmax_rows).  Computed as a Gumbel-max:
+ *   y = round_dtype(fp32(x) / T),  u = ((bits >> 9) + 0.5) * 2^-23,
+ *   id = argmax_v (y[v] - log(-log(u[v]))),  score = that maximum,
+ * where bits is word v%4 of Philox4x32-10 at counter (v/4, m, offset low,
+ * offset high) and key (seed low, seed high).  The ids are distributed as
+ * softmax(y) draws and depend only on (seed, offset, row, logits).
+ * temperature < 1e-5 is dels_argmax_rows, as in the reference; NaN or inf
+ * temperatures are rejected.  Where torch.multinomial raises (a row with NaN
+ * or +inf, or of -inf only) this returns the argmax rule's id instead.
+ */
+size_t dels_sample_rows_ws_bytes(int64_t M, int64_t V);
+int dels_sample_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V,
+                     float temperature, uint64_t seed, uint64_t offset,
+                     int64_t* out_ids, float* out_score, int64_t ld_out,
+                     void* ws, size_t ws_bytes, void* stream);
+
+/*
  * fp8 variant (no counterpart in the reference: the fp8 configuration of the
  * same draft step, with e4m3 weights and per-output-channel fp32 scales).
  *

@@ -7,3 +7,4 @@ baseline), never as a fallback for the HIP path.
 """
 
 from .dels_oracle import *  # noqa: F401,F403
+from . import sampling  # noqa: F401
