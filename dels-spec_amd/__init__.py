@@ -3,6 +3,7 @@
 Public surface (mirrors the reference's interface for this path):
   * ``DeLSGraphRunner``          -- drop-in hipGraph suffix-rollout runner
   * ``MarkovDeLSGraphRunner``    -- the same for the Markov local head
+  * ``DraftCorrectionGraphRunner`` -- the Domino correction rollout (hipGraph)
   * ``DeLSDraftStep``            -- a whole draft block (target LM head, first
     argmax, rollout) as one graph
   * ``DeLSLocalHead``, ``MarkovDeLSLocalHead``, ``PositionMixJointHead`` --
@@ -24,16 +25,20 @@ from .local_head import (DeLSLocalHead, MarkovDeLSLocalHead, PositionMixJointHea
                          parse_scalar_schedule, unigram_log_prior_from_counts)
 from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gather_argmax, gru_step,
                   lowrank_argmax, lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows,
-                  quantize_pack_fp8, rank_proj, sample_rows)
+                  quantize_pack_fp8, rank_proj, sample_rows, domino_argmax)
 from .sampling import sample
 from .draft_step import DeLSDraftStep
 from .runner import DeLSGraphRunner
 from .markov_runner import MarkovDeLSGraphRunner
+from .domino_runner import DraftCorrectionGraphRunner, unwrap_correction_mlp
 from . import synth
 
 __all__ = [
     "DeLSGraphRunner",
     "MarkovDeLSGraphRunner",
+    "DraftCorrectionGraphRunner",
+    "unwrap_correction_mlp",
+    "domino_argmax",
     "gather_argmax",
     "DeLSDraftStep",
     "argmax_rows",

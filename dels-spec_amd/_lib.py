@@ -52,6 +52,28 @@ class RolloutParams(ctypes.Structure):
     ]
 
 
+class DominoRolloutParams(ctypes.Structure):
+    """Mirror of ``struct dels_domino_rollout`` in include/dels.h."""
+
+    _fields_ = [
+        ("gi_table", _ptr), ("ld_gi", _i64), ("table_rows", _i64),
+        ("w_hh", _ptr), ("b_hh", _ptr),
+        ("w_z", _ptr), ("fc1_bias", _ptr), ("w_s", _ptr),
+        ("fc2_w", _ptr), ("fc2_bias", _ptr), ("fc2_bias_dtype", _int),
+        ("alpha", ctypes.c_float),
+        ("batch", _i64), ("steps", _i64), ("prefix_len", _i64), ("D", _i64), ("G", _i64), ("E", _i64),
+        ("V", _i64),
+        ("weights_layout", _int),
+        ("prefix_ids", _ptr),
+        ("hiddens", _ptr),
+        ("base", _ptr), ("base_dtype", _int), ("ld_base", _i64),
+        ("out_ids", _ptr), ("out_scores", _ptr),
+        ("h_a", _ptr), ("h_b", _ptr),
+        ("z", _ptr), ("s", _ptr),
+        ("ws", _ptr), ("ws_bytes", _sz),
+    ]
+
+
 class MarkovRolloutParams(ctypes.Structure):
     """Mirror of ``struct dels_markov_rollout`` in include/dels.h."""
 
@@ -107,6 +129,12 @@ SIGNATURES = {
     "dels_markov_graph_create": (_int, [ctypes.POINTER(MarkovRolloutParams), ctypes.POINTER(_ptr)]),
     "dels_argmax_rows_ws_bytes": (_sz, [_i64, _i64]),
     "dels_argmax_rows": (_int, [_ptr, _i64, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_domino_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_domino_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _int, _ptr, _i64, _int, ctypes.c_float,
+                                  _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_domino_rollout_ws_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "dels_domino_rollout_enqueue": (_int, [ctypes.POINTER(DominoRolloutParams), _ptr]),
+    "dels_domino_graph_create": (_int, [ctypes.POINTER(DominoRolloutParams), ctypes.POINTER(_ptr)]),
     "dels_sample_rows_ws_bytes": (_sz, [_i64, _i64]),
     "dels_sample_rows": (_int, [_ptr, _i64, _int, _i64, _i64, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64, _ptr,
                                 _ptr, _i64, _ptr, _sz, _ptr]),

@@ -428,6 +428,172 @@ static int scratch_address(hipStream_t s, void** out) {
     return DELS_OK;
 }
 
+// ---- Domino correction rollout ---------------------------------------------------
+
+struct DominoLayout {
+    size_t part_off, total;   // the projections and GRU steps run in turn and share the partials
+    SkinnyPlan z_plan, s_plan, gru_plan;
+};
+
+static DominoLayout domino_layout(int64_t batch, int64_t steps, int64_t D, int64_t G, int64_t E) {
+    DominoLayout L{};
+    L.z_plan = plan_skinny(batch * steps, D, E, false);
+    L.s_plan = plan_skinny(batch, G, E, false);
+    L.gru_plan = plan_skinny(batch, G, G, true);
+    L.part_off = kDataOff;
+    L.total = L.part_off + std::max(skinny_data_bytes(L.z_plan),
+                                    std::max(skinny_data_bytes(L.s_plan), skinny_data_bytes(L.gru_plan)));
+    return L;
+}
+
+static int check_domino_step(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
+                             const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase,
+                             int base_dtype, float alpha, int64_t M, int64_t E, int64_t V, const int64_t* out_ids,
+                             int64_t ld_out) {
+    if (M < 0 || E <= 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape M=%lld E=%lld V=%lld",
+                                                (long long)M, (long long)E, (long long)V);
+    if (V >= INT32_MAX || M > kMaxKeyRows) return fail(DELS_ERR_UNSUPPORTED, "Domino step: M <= %d, V < 2^31-1",
+                                                       kMaxKeyRows);
+    if (E % 32 != 0 || E > kDominoMaxE)
+        return fail(DELS_ERR_UNSUPPORTED, "Domino step: E=%lld must be a multiple of 32 and at most %d",
+                    (long long)E, kDominoMaxE);
+    if (!(alpha == alpha)) return fail(DELS_ERR_INVALID_ARGUMENT, "guidance alpha is NaN");
+    if (M == 0) return DELS_OK;
+    if (!z || !sv) return fail(DELS_ERR_INVALID_ARGUMENT, "z or s is NULL");
+    if ((M > 1 && (ldz < E || lds < E)) || ldz < 0 || lds < 0)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "z/s leading dimension < E");
+    if (!fc2_w) return fail(DELS_ERR_INVALID_ARGUMENT, "fc2 weight is NULL");
+    if (!aligned16(fc2_w)) return fail(DELS_ERR_ALIGNMENT, "packed fc2 weight must be 16-byte aligned");
+    if (fc2_bias && !valid_dtype(fc2_bias_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown fc2 bias dtype %d",
+                                                               fc2_bias_dtype);
+    if (!base) return fail(DELS_ERR_INVALID_ARGUMENT, "base logits pointer is NULL");
+    if (!valid_dtype(base_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown base dtype %d", base_dtype);
+    if (M > 1 && ldbase < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
+                                         (long long)ldbase, (long long)V);
+    if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+    if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    return DELS_OK;
+}
+
+static DominoArgs domino_args(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
+                              const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase,
+                              int base_dtype, float alpha, int64_t M, int64_t E, int64_t V, int64_t* out_ids,
+                              float* out_score, int64_t ld_out) {
+    DominoArgs d{};
+    d.z = static_cast<const uint16_t*>(z); d.ldz = ldz;
+    d.s = static_cast<const uint16_t*>(sv); d.lds = lds;
+    d.W = static_cast<const uint16_t*>(fc2_w);
+    d.bias = fc2_bias; d.bias_dtype = fc2_bias_dtype;
+    d.base = base; d.ldbase = ldbase; d.base_dtype = base_dtype;
+    d.alpha = alpha;
+    d.M = (int)M; d.E = (int)E; d.V = (int)V;
+    d.out_ids = out_ids; d.out_score = out_score; d.ld_out = ld_out;
+    return d;
+}
+
+static int check_domino_rollout(const dels_domino_rollout* p) {
+    if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "Domino rollout parameters are NULL");
+    if (p->steps <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires steps > 0, got %lld",
+                                   (long long)p->steps);
+    if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires batch > 0");
+    if (p->prefix_len <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Domino rollout requires prefix_len > 0");
+    if (p->D <= 0 || p->D % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size D must be a positive multiple of 8");
+    int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
+                            p->weights_layout, p->batch, p->G, p->h_b, p->G);
+    if (rc != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->h_b, p->G, p->G, "h_b")) != DELS_OK) return rc;
+    if ((rc = check_weight(p->w_z, p->D, p->D, p->weights_layout, "w_z")) != DELS_OK) return rc;
+    if ((rc = check_weight(p->w_s, p->G, p->G, p->weights_layout, "w_s")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->hiddens, p->D, p->D, "hiddens")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->z, p->E, p->E, "z scratch")) != DELS_OK) return rc;
+    if ((rc = check_bf16_matrix(p->s, p->E, p->E, "s scratch")) != DELS_OK) return rc;
+    if (p->ld_base != 0 && p->ld_base < p->steps * p->V)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "rollout ld_base %lld < steps * V", (long long)p->ld_base);
+    if ((rc = check_domino_step(p->z, p->steps * p->E, p->s, p->E, p->fc2_w, p->fc2_bias, p->fc2_bias_dtype, p->base,
+                                p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->alpha, p->batch, p->E,
+                                p->V, p->out_ids, p->steps)) != DELS_OK)
+        return rc;
+    const DominoLayout L = domino_layout(p->batch, p->steps, p->D, p->G, p->E);
+    if (!skinny_supported(L.z_plan) || !skinny_supported(L.s_plan) || !skinny_supported(L.gru_plan))
+        return fail(DELS_ERR_UNSUPPORTED, "Domino rollout shape needs too many workgroup tiles");
+    return check_ws(p->ws, p->ws_bytes, L.total);
+}
+
+static int enqueue_domino(const dels_domino_rollout* p, hipStream_t s) {
+    const DominoLayout L = domino_layout(p->batch, p->steps, p->D, p->G, p->E);
+    char* ws = static_cast<char*>(p->ws);
+    const int B = (int)p->batch, S = (int)p->steps, G = (int)p->G, E = (int)p->E, V = (int)p->V;
+    const bool packed = p->weights_layout == DELS_LAYOUT_MFMA16;
+
+    // z = F.linear(parallel_hiddens, w_z, fc1_bias) for every step at once  (code/kernel/domino.py:386-390)
+    RankArgs rz{};
+    rz.h = static_cast<const uint16_t*>(p->hiddens); rz.ldh = p->D;
+    rz.A = static_cast<const uint16_t*>(p->w_z); rz.lda = p->D; rz.a_packed = packed;
+    rz.bias = static_cast<const uint16_t*>(p->fc1_bias); rz.act = DELS_ACT_IDENTITY;
+    rz.M = B * S; rz.d = (int)p->D; rz.r = E;
+    rz.rank = static_cast<uint16_t*>(p->z); rz.ldrank = E;
+    hipError_t e = launch_rank_proj(rz, L.z_plan, ws, L.part_off, s);
+    if (e != hipSuccess) return hip_fail(e, "z projection launch");
+
+    GruArgs g{};
+    g.gi_table = static_cast<const uint16_t*>(p->gi_table);
+    g.ld_gi = p->ld_gi;
+    g.table_rows = p->table_rows;
+    g.w_hh = static_cast<const uint16_t*>(p->w_hh);
+    g.w_packed = packed;
+    g.b_hh = static_cast<const uint16_t*>(p->b_hh);
+    g.batch = B;
+    g.G = G;
+    g.ldh_in = G;
+    g.ldh_out = G;
+
+    // h = prefix_gru(embed_tokens(prefix_ids)) from h = 0, one cell per prefix id  (392-396)
+    uint16_t* h_cur = static_cast<uint16_t*>(p->h_a);
+    uint16_t* h_next = static_cast<uint16_t*>(p->h_b);
+    for (int64_t j = 0; j < p->prefix_len; ++j) {
+        g.tokens = p->prefix_ids + j;
+        g.tok_stride = p->prefix_len;
+        g.h_in = j == 0 ? nullptr : h_cur;
+        g.h_out = j == 0 ? h_cur : h_next;
+        e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
+        if (e != hipSuccess) return hip_fail(e, "GRU step launch");
+        if (j > 0) std::swap(h_cur, h_next);
+    }
+
+    const size_t esz = dtype_size(p->base_dtype);
+    for (int t = 0; t < S; ++t) {
+        // s = F.linear(h, w_s)   (400-402)
+        RankArgs rs{};
+        rs.h = h_cur; rs.ldh = G;
+        rs.A = static_cast<const uint16_t*>(p->w_s); rs.lda = G; rs.a_packed = packed;
+        rs.bias = nullptr; rs.act = DELS_ACT_IDENTITY;
+        rs.M = B; rs.d = G; rs.r = E;
+        rs.rank = static_cast<uint16_t*>(p->s); rs.ldrank = E;
+        e = launch_rank_proj(rs, L.s_plan, ws, L.part_off, s);
+        if (e != hipSuccess) return hip_fail(e, "s projection launch");
+
+        // the fused correction step on z[:, t], s and base[:, t]   (404-410, 419)
+        const DominoArgs d = domino_args(static_cast<const char*>(p->z) + (size_t)t * E * 2, (int64_t)S * E, p->s, E,
+                                         p->fc2_w, p->fc2_bias, p->fc2_bias_dtype,
+                                         static_cast<const char*>(p->base) + (size_t)t * V * esz,
+                                         p->ld_base ? p->ld_base : (int64_t)S * V, p->base_dtype, p->alpha, B, E, V,
+                                         p->out_ids + t, p->out_scores ? p->out_scores + t : nullptr, S);
+        e = launch_domino_argmax(d, ws, s);
+        if (e != hipSuccess) return hip_fail(e, "Domino step launch");
+
+        if (t + 1 < S) {   // GRU step on the chosen ids   (421-428)
+            g.tokens = p->out_ids + t;
+            g.tok_stride = S;
+            g.h_in = h_cur;
+            g.h_out = h_next;
+            e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
+            if (e != hipSuccess) return hip_fail(e, "GRU step launch");
+            std::swap(h_cur, h_next);
+        }
+    }
+    return DELS_OK;
+}
+
 }  // namespace dels
 
 using namespace dels;
@@ -879,6 +1045,43 @@ int dels_markov_graph_create(const dels_markov_rollout* p, void** graph_out) {
     int rc = check_markov(p);
     if (rc != DELS_OK) return rc;
     return capture_graph([p](hipStream_t s) { return enqueue_markov(p, s); }, graph_out);
+}
+
+size_t dels_domino_argmax_ws_bytes(int64_t, int64_t, int64_t) { return kDataOff; }
+
+int dels_domino_argmax(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
+                       const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase, int base_dtype,
+                       float alpha, int64_t M, int64_t E, int64_t V, int64_t* out_ids, float* out_score,
+                       int64_t ld_out, void* ws, size_t ws_bytes, void* stream) {
+    int rc = check_domino_step(z, ldz, sv, lds, fc2_w, fc2_bias, fc2_bias_dtype, base, ldbase, base_dtype, alpha, M,
+                               E, V, out_ids, ld_out);
+    if (rc != DELS_OK) return rc;
+    if (M == 0) return DELS_OK;
+    if ((rc = check_ws(ws, ws_bytes, kDataOff)) != DELS_OK) return rc;
+    const DominoArgs d = domino_args(z, ldz, sv, lds, fc2_w, fc2_bias, fc2_bias_dtype, base, ldbase, base_dtype, alpha,
+                                     M, E, V, out_ids, out_score, ld_out);
+    hipError_t e = launch_domino_argmax(d, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "Domino step launch");
+}
+
+size_t dels_domino_rollout_ws_bytes(int64_t batch, int64_t steps, int64_t D, int64_t G, int64_t E, int64_t V) {
+    (void)V;
+    return domino_layout(std::max<int64_t>(batch, 1), std::max<int64_t>(steps, 1), std::max<int64_t>(D, 1),
+                         std::max<int64_t>(G, 1), std::max<int64_t>(E, 1)).total;
+}
+
+int dels_domino_rollout_enqueue(const dels_domino_rollout* p, void* stream) {
+    int rc = check_domino_rollout(p);
+    if (rc != DELS_OK) return rc;
+    return enqueue_domino(p, static_cast<hipStream_t>(stream));
+}
+
+int dels_domino_graph_create(const dels_domino_rollout* p, void** graph_out) {
+    if (!graph_out) return fail(DELS_ERR_INVALID_ARGUMENT, "graph_out is NULL");
+    *graph_out = nullptr;
+    int rc = check_domino_rollout(p);
+    if (rc != DELS_OK) return rc;
+    return capture_graph([p](hipStream_t s) { return enqueue_domino(p, s); }, graph_out);
 }
 
 int dels_graph_launch(void* graph, void* stream) {

@@ -121,6 +121,25 @@ bool argmax_fp8_supported(int64_t M, int64_t r);
 size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V);
 hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
+// ---- Domino correction step (SiLU(z + s) . fc2^T (+ bias), alpha, base, argmax) ----
+
+constexpr int kDominoMaxE = 2048;              // largest correction-MLP width (LDS operands)
+
+struct DominoArgs {
+    const uint16_t* z; int64_t ldz;            // [M, E] bf16: fc1's hidden-state part of this step
+    const uint16_t* s; int64_t lds;            // [M, E] bf16: fc1's GRU-state part
+    const uint16_t* W;                         // fc2 weight [V, E], MFMA-16 blocks
+    const void* bias; int bias_dtype;          // fc2 bias [V] (nullptr: none), dtype code as base
+    const void* base; int64_t ldbase; int base_dtype;
+    float alpha;
+    int M, E, V;
+    int64_t* out_ids; float* out_score; int64_t ld_out;
+};
+bool domino_supported(int64_t M, int64_t E, int64_t V);
+size_t domino_lds_bytes(int64_t E);
+// keys and counter in the control area of `ws`
+hipError_t launch_domino_argmax(const DominoArgs& a, void* ws, hipStream_t s);
+
 // ---- fused decode step: rank projection + argmax in one launch (M <= 16) --------
 
 // Both weights packed, r/32 in {2, 4, 8, 16}, d a multiple of 32 and at most

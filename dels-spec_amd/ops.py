@@ -16,6 +16,8 @@ Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
                           _reduce_argmax_kernel, code/kernel/markov_dels.py:15-138, 216-268
   * ``argmax_rows`` / ``sample_rows`` -- sample() at temperature 0 / above 0,
                           code/dflash.py:31-38
+  * ``domino_argmax``  -- a Domino correction step: _fused_mlp_bias_argmax_kernel +
+                          _reduce_argmax_kernel, code/kernel/domino.py:58-173, 438-482
 """
 
 from __future__ import annotations
@@ -389,6 +391,39 @@ def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,
     _lib.check(lib.dels_argmax_rows(logits.data_ptr(), logits.stride(0), _DTYPES[logits.dtype], M, V,
                                     out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(),
                                     _stream_ptr(logits.device)), "dels_argmax_rows")
+    return out_ids, out_score
+
+
+def domino_argmax(z: torch.Tensor, s: torch.Tensor, fc2_weight: Weight, base_logits: torch.Tensor,
+                  guidance_alpha: float, fc2_bias: Optional[torch.Tensor] = None, *,
+                  out_ids: Optional[torch.Tensor] = None,
+                  out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One Domino correction step (code/kernel/domino.py:58-173, 438-482):
+    ``argmax_v fma(SiLU(z + s) . fc2[v] (+ fc2_bias[v]), alpha, base[v])`` per row, with
+    ``SiLU(z + s)`` kept in fp32.  ``z``, ``s`` [M, E] bf16 (any row stride);
+    ``fc2_weight`` [V, E] (a ``PackedWeight``, or a bf16 matrix packed on the fly);
+    ``base_logits`` [M, V].  Returns ``(ids int64[M], score fp32[M])``."""
+    _require_bf16_matrix(z, "z")
+    M, E = z.shape
+    _require_bf16_matrix(s, "s", rows=M, cols=E)
+    if not isinstance(fc2_weight, PackedWeight):
+        fc2_weight = pack_operand(fc2_weight)
+    _require_cuda(fc2_weight.data, "fc2_weight")
+    if fc2_weight.cols != E:
+        raise ValueError(f"fc2_weight has {fc2_weight.cols} columns, expected {E}")
+    V = fc2_weight.rows
+    base = _base_view(base_logits, M, V)
+    bias = _prior_view(fc2_bias, V) if fc2_bias is not None else None
+    dev = z.device
+    out_ids, out_score, ld_out = _outputs(out_ids, out_score, M, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_domino_argmax_ws_bytes(M, E, V))
+    _lib.check(lib.dels_domino_argmax(
+        z.data_ptr(), z.stride(0), s.data_ptr(), s.stride(0), fc2_weight.data.data_ptr(),
+        bias.data_ptr() if bias is not None else None, _DTYPES[bias.dtype] if bias is not None else 0,
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype], float(guidance_alpha), M, E, V,
+        out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(), _stream_ptr(dev)),
+        "dels_domino_argmax")
     return out_ids, out_score
 
 

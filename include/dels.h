@@ -340,6 +340,73 @@ int dels_graph_launch(void* graph, void* stream);
 int dels_graph_destroy(void* graph);
 
 /*
+ * Domino correction step (DraftCorrectionGraphRunner._fused_step_triton,
+ * code/kernel/domino.py:58-173, 438-482): for rows m < M of z and s [M, E]
+ * bf16 (the hidden-state and GRU-state parts of the correction MLP's first
+ * layer),
+ *   mid[m, k] = p * sigmoid(p),  p = fp32(z[m, k]) + fp32(s[m, k])   (fp32)
+ *   dot[m, v] = fp32(mid[m] . fc2[v])   (+ fc2_bias[v] when given)
+ *   id_m = lowest argmax_v fma(dot[m, v], alpha, base[m, v]).
+ * fc2 [V, E] bf16 in the MFMA-16 layout (dels_pack_operand); E a multiple of
+ * 32, at most 2048; fc2_bias [V] of fc2_bias_dtype or NULL; base [M, V] with
+ * leading dimension ldbase.  mid enters the matrix cores as two bf16 parts
+ * (hi + lo, 2^-17 relative).
+ */
+size_t dels_domino_argmax_ws_bytes(int64_t M, int64_t E, int64_t V);
+int dels_domino_argmax(const void* z, int64_t ldz, const void* s, int64_t lds, const void* fc2_w,
+                       const void* fc2_bias, int fc2_bias_dtype,
+                       const void* base, int64_t ldbase, int base_dtype, float alpha,
+                       int64_t M, int64_t E, int64_t V,
+                       int64_t* out_ids, float* out_score, int64_t ld_out,
+                       void* ws, size_t ws_bytes, void* stream);
+
+/*
+ * The Domino correction rollout of DraftCorrectionGraphRunner._forward_impl
+ * (code/kernel/domino.py:379-436):
+ *   z = F.linear(hiddens [batch * steps, D], w_z, fc1_bias)       (bf16)
+ *   h = GRU over the prefix ids from h = 0 (gi_table rows, one cell per id)
+ *   for each step t: s = F.linear(h, w_s); out_ids[:, t] = the correction
+ *   step on z[:, t], s and base[:, t, :]; then a GRU step on that id unless
+ *   t is the last step.
+ * gi_table = F.linear(embed_tokens.weight, W_ih, b_ih) as in the DeLS rollout.
+ */
+typedef struct dels_domino_rollout {
+    const void* gi_table;   /* [table_rows, 3G] bf16 */
+    int64_t ld_gi;
+    int64_t table_rows;
+    const void* w_hh;       /* [3G, G] bf16 (weights_layout) */
+    const void* b_hh;       /* [3G] bf16 or NULL */
+    const void* w_z;        /* [E, D] bf16 (weights_layout): fc1.weight[:, :D] */
+    const void* fc1_bias;   /* [E] bf16 or NULL */
+    const void* w_s;        /* [E, G] bf16 (weights_layout): fc1.weight[:, D:] */
+    const void* fc2_w;      /* [V, E] bf16, MFMA-16 layout */
+    const void* fc2_bias;   /* [V] or NULL */
+    int fc2_bias_dtype;
+    float alpha;            /* guidance alpha */
+    int64_t batch, steps, prefix_len, D, G, E, V;
+    int weights_layout;     /* DELS_LAYOUT_* of w_hh, w_z and w_s */
+    const int64_t* prefix_ids; /* [batch, prefix_len] int64 */
+    const void* hiddens;    /* [batch, steps, D] bf16, contiguous */
+    const void* base;       /* [batch, steps, V]: row b, step t at base + (b * ld_base + t * V) */
+    int base_dtype;
+    int64_t ld_base;        /* 0: steps * V */
+    int64_t* out_ids;       /* [batch, steps] int64 */
+    float* out_scores;      /* [batch, steps] fp32 or NULL */
+    void* h_a;              /* [batch, G] bf16 state buffers (ping-pong) */
+    void* h_b;
+    void* z;                /* [batch * steps, E] bf16 scratch */
+    void* s;                /* [batch, E] bf16 scratch */
+    void* ws;
+    size_t ws_bytes;
+} dels_domino_rollout;
+
+size_t dels_domino_rollout_ws_bytes(int64_t batch, int64_t steps, int64_t D, int64_t G, int64_t E, int64_t V);
+int dels_domino_rollout_enqueue(const dels_domino_rollout* p, void* stream);
+/* hipGraph of the rollout (torch.cuda.graph of code/kernel/domino.py:364-377); launch and
+ * destroy with dels_graph_launch / dels_graph_destroy. */
+int dels_domino_graph_create(const dels_domino_rollout* p, void** graph_out);
+
+/*
  * Markov DeLS step: the rank of row m is a row of a table, rank_m =
  * E[tokens[m]] (F.embedding(current_token, embedding_weight)), followed by the
  * fused argmax of dels_fused_argmax.  Replaces _fused_markov_argmax_kernel +
