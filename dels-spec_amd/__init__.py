@@ -25,7 +25,7 @@ from .local_head import (DeLSLocalHead, MarkovDeLSLocalHead, PositionMixJointHea
                          parse_scalar_schedule, unigram_log_prior_from_counts)
 from .ops import (Fp8Weight, PackedWeight, argmax_rows, fused_argmax, fused_argmax_fp8, gather_argmax, gru_step,
                   lowrank_argmax, lowrank_argmax_fp8, pack_operand, pack_operand_fp8, quantize_e4m3_rows,
-                  quantize_pack_fp8, rank_proj, sample_rows, domino_argmax)
+                  quantize_pack_fp8, rank_proj, sample_rows, domino_argmax, lm_head, pack_lm_head)
 from .sampling import sample
 from .draft_step import DeLSDraftStep
 from .runner import DeLSGraphRunner
@@ -39,6 +39,8 @@ __all__ = [
     "DraftCorrectionGraphRunner",
     "unwrap_correction_mlp",
     "domino_argmax",
+    "lm_head",
+    "pack_lm_head",
     "gather_argmax",
     "DeLSDraftStep",
     "argmax_rows",

@@ -129,6 +129,9 @@ SIGNATURES = {
     "dels_markov_graph_create": (_int, [ctypes.POINTER(MarkovRolloutParams), ctypes.POINTER(_ptr)]),
     "dels_argmax_rows_ws_bytes": (_sz, [_i64, _i64]),
     "dels_argmax_rows": (_int, [_ptr, _i64, _int, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+    "dels_lm_head_ws_bytes": (_sz, [_i64, _i64, _i64]),
+    "dels_pack_lm_head": (_int, [_ptr, _i64, _i64, _i64, _ptr, _sz, _ptr]),
+    "dels_lm_head": (_int, [_ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_domino_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
     "dels_domino_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _int, _ptr, _i64, _int, ctypes.c_float,
                                   _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),

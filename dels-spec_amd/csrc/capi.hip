@@ -1047,6 +1047,52 @@ int dels_markov_graph_create(const dels_markov_rollout* p, void** graph_out) {
     return capture_graph([p](hipStream_t s) { return enqueue_markov(p, s); }, graph_out);
 }
 
+size_t dels_lm_head_ws_bytes(int64_t, int64_t, int64_t) { return kDataOff; }
+
+int dels_pack_lm_head(const void* W, int64_t ldw, int64_t rows, int64_t cols, void* packed, size_t packed_bytes_,
+                      void* stream) {
+    if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
+    if (cols % (32 * kLmHeadKChunk) != 0)
+        return fail(DELS_ERR_UNSUPPORTED, "LM head layout: cols=%lld must be a multiple of %d", (long long)cols,
+                    32 * kLmHeadKChunk);
+    if (rows == 0 || cols == 0) return DELS_OK;
+    int rc = check_bf16_matrix(W, ldw, cols, "W (to pack)");
+    if (rc != DELS_OK) return rc;
+    if (!packed || !aligned16(packed)) return fail(DELS_ERR_ALIGNMENT, "packed output must be 16-byte aligned");
+    if (packed_bytes_ < packed_bytes(rows, cols))
+        return fail(DELS_ERR_INVALID_ARGUMENT, "packed output too small: %zu bytes given, %zu needed", packed_bytes_,
+                    packed_bytes(rows, cols));
+    hipError_t e = launch_pack_mfma16(static_cast<const uint16_t*>(W), ldw, rows, cols, static_cast<uint16_t*>(packed),
+                                      static_cast<hipStream_t>(stream), kLmHeadKChunk);
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "pack launch");
+}
+
+int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int64_t K, int64_t V, void* base,
+                 int64_t ldo, int64_t argmax_period, int64_t* out_ids, float* out_score, int64_t ld_out, void* ws,
+                 size_t ws_bytes, void* stream) {
+    if (M < 0 || K <= 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad LM head shape M=%lld K=%lld V=%lld",
+                                                (long long)M, (long long)K, (long long)V);
+    if (argmax_period < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "argmax_period must be >= 0");
+    if (M == 0) return DELS_OK;
+    if (!lm_head_supported(M, K, V, argmax_period))
+        return fail(DELS_ERR_UNSUPPORTED, "LM head: K=%lld must be a multiple of 256, M <= 8192, V < 2^31-1 and "
+                    "at most %d argmax rows", (long long)K, kMaxKeyRows);
+    int rc;
+    if ((rc = check_bf16_matrix(hidden, ldh, K, "hidden")) != DELS_OK) return rc;
+    if (!W) return fail(DELS_ERR_INVALID_ARGUMENT, "W is NULL");
+    if (!aligned16(W)) return fail(DELS_ERR_ALIGNMENT, "packed W must be 16-byte aligned");
+    if (base && M > 1 && ldo < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
+                                              (long long)ldo, (long long)V);
+    if (argmax_period > 0) {
+        if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
+        if (ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    }
+    if ((rc = check_ws(ws, ws_bytes, kDataOff)) != DELS_OK) return rc;
+    hipError_t e = launch_lm_head(hidden, ldh, W, (int)M, (int)K, (int)V, base, ldo, (int)argmax_period, out_ids,
+                                  out_score, ld_out, ws, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? DELS_OK : hip_fail(e, "LM head launch");
+}
+
 size_t dels_domino_argmax_ws_bytes(int64_t, int64_t, int64_t) { return kDataOff; }
 
 int dels_domino_argmax(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,

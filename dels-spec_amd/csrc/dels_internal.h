@@ -121,6 +121,17 @@ bool argmax_fp8_supported(int64_t M, int64_t r);
 size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V);
 hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
+// ---- target LM head of a draft block: base = bf16(hidden . W^T), argmax rows fused ----
+// K blocks per chunk of the LM head's K-chunk-major W layout (dels_pack_lm_head).
+constexpr int kLmHeadKChunk = 4;
+// W [V, K] in MFMA-16 blocks, K-chunk-major, K a multiple of 256; rows m with argmax_period > 0
+// and m % argmax_period == 0 are argmaxed (ids/scores at row m / argmax_period of
+// out_*) instead of stored.  Keys and counter in the control area of `ws`.
+bool lm_head_supported(int64_t M, int64_t K, int64_t V, int64_t argmax_period);
+hipError_t launch_lm_head(const void* hidden, int64_t ldh, const void* W, int M, int K, int V, void* base,
+                          int64_t ldo, int argmax_period, int64_t* out_ids, float* out_score, int64_t ld_out,
+                          void* ws, hipStream_t s);
+
 // ---- Domino correction step (SiLU(z + s) . fc2^T (+ bias), alpha, base, argmax) ----
 
 constexpr int kDominoMaxE = 2048;              // largest correction-MLP width (LDS operands)
@@ -163,8 +174,9 @@ inline int64_t packed_col_blocks(int64_t cols) { return (cols + 31) / 32; }
 inline size_t packed_bytes(int64_t rows, int64_t cols) {
     return (size_t)packed_row_blocks(rows) * packed_col_blocks(cols) * 1024;
 }
+// kchunk > 0: K-chunk-major block order (the LM head's layout), see pack.hip.
 hipError_t launch_pack_mfma16(const uint16_t* W, int64_t ldw, int64_t rows, int64_t cols, uint16_t* P,
-                              hipStream_t s);
+                              hipStream_t s, int64_t kchunk = 0);
 // e4m3 layouts: K128 (16 x 128 blocks of 2 KiB, the fp8 argmax's B) and K32
 // (16 x 32 blocks of 512 bytes, the fp8 rank projection's A).
 enum : int { FP8_K128 = 2, FP8_K32 = 3 };

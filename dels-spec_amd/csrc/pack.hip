@@ -13,8 +13,13 @@
 
 namespace dels {
 
+// kchunk > 0 (col_blocks a multiple of it): the blocks go K-chunk-major instead,
+// block (bi, bj) at ((bj / kchunk) * row_blocks + bi) * kchunk + bj % kchunk, so
+// that kchunk consecutive K blocks of every row block -- one K chunk of the whole
+// matrix -- are one contiguous run (the LM head's stream order).
 __global__ void pack_mfma16_kernel(const uint16_t* __restrict__ W, int64_t ldw, int64_t rows, int64_t cols,
-                                   int64_t col_blocks, int64_t chunks, uint16_t* __restrict__ P) {
+                                   int64_t col_blocks, int64_t chunks, int64_t kchunk, int64_t row_blocks,
+                                   uint16_t* __restrict__ P) {
     for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < chunks;
          idx += (int64_t)gridDim.x * blockDim.x) {
         const int lane = (int)(idx & 63);
@@ -33,18 +38,20 @@ __global__ void pack_mfma16_kernel(const uint16_t* __restrict__ W, int64_t ldw, 
                 __builtin_memcpy(&v, e, 16);
             }
         }
-        *reinterpret_cast<u32x4*>(P + idx * 8) = v;
+        const int64_t dst = kchunk > 0 ? ((bj / kchunk) * row_blocks + bi) * kchunk + bj % kchunk : blk;
+        *reinterpret_cast<u32x4*>(P + (dst * 64 + lane) * 8) = v;
     }
 }
 
 hipError_t launch_pack_mfma16(const uint16_t* W, int64_t ldw, int64_t rows, int64_t cols, uint16_t* P,
-                              hipStream_t s) {
+                              hipStream_t s, int64_t kchunk) {
     const int64_t col_blocks = packed_col_blocks(cols);
-    const int64_t chunks = packed_row_blocks(rows) * col_blocks * 64;
+    const int64_t row_blocks = packed_row_blocks(rows);
+    const int64_t chunks = row_blocks * col_blocks * 64;
     if (chunks == 0) return hipSuccess;
     const int blocks = (int)std::min<int64_t>(4096, (chunks + 255) / 256);
     hipLaunchKernelGGL(pack_mfma16_kernel, dim3(blocks), dim3(256), 0, s, W, ldw, rows, cols, col_blocks, chunks,
-                       P);
+                       kchunk, row_blocks, P);
     return hipGetLastError();
 }
 

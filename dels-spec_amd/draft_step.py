@@ -6,11 +6,16 @@ The graph path of ``spec_generate`` for one block (code/dflash.py:452-486):
     verify_ids[:, 1] = sample(base_logits[:, :1])             # plain argmax of position 0
     verify_ids[:, 2:k+1] = graph_runner(verify_ids[:, 1:2], base_logits[:, 1:k])
 
-Here the LM-head GEMM is a plain library GEMM (``torch.mm`` -> hipBLASLt, as
-``nn.Linear`` does in the reference), the first-position argmax is
-``dels_argmax_rows`` and the suffix rollout is ``dels_rollout_enqueue`` over the
-runner's packed weights, reading ``base_logits[:, 1:k]`` in place (row stride
-k * V).  All three are captured once into one graph and replayed per block.
+The LM head and the first-position argmax are either (``lm_head="library"``,
+the default) a plain library GEMM (``torch.mm`` -> hipBLASLt, as ``nn.Linear``
+in the reference) followed by ``dels_argmax_rows``, or (``lm_head="fused"``) one
+launch of the hand-written ``dels_lm_head`` (W packed once, streamed from HBM
+once, the position-0 rows argmaxed inside the GEMM and never stored; hidden
+size a multiple of 256).  On the MI355X the library GEMM is faster at this
+shape (batch 8, block 16: 284 us against about 345 us), hence the default.
+The suffix rollout is ``dels_rollout_enqueue`` over the runner's packed
+weights, reading ``base_logits[:, 1:k]`` in place (row stride k * V).  All of
+it is captured once into one graph and replayed per block.
 The drafter that produces ``parallel_hiddens`` is outside this path.
 """
 
@@ -22,7 +27,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from .ops import new_workspace
+from .ops import new_workspace, pack_lm_head
 from .runner import DeLSGraphRunner
 
 
@@ -38,7 +43,9 @@ class DeLSDraftStep:
 
     def __init__(self, *, local_head, lm_head_weight: torch.Tensor, batch_size: int, k_draft: int,
                  vocab_size: int, alpha_values: list[float], beta_values: list[float],
-                 baseline_logits: Optional[torch.Tensor], device: torch.device):
+                 baseline_logits: Optional[torch.Tensor], device: torch.device, lm_head: str = "library"):
+        if lm_head not in ("library", "fused"):
+            raise ValueError(f"lm_head must be 'library' or 'fused', got {lm_head!r}")
         if k_draft < 2:
             raise ValueError(f"DeLSDraftStep needs k_draft >= 2 (at least one DeLS step), got {k_draft}.")
         self.runner = DeLSGraphRunner(local_head=local_head, batch_size=batch_size, steps=k_draft - 1,
@@ -52,6 +59,11 @@ class DeLSDraftStep:
             raise ValueError("lm_head_weight must be a bfloat16 [vocab_size, hidden] matrix")
         self.lm_head_weight = W.contiguous()
         d = int(W.shape[1])
+        lib = _lib.load()
+        self._fused_head = lm_head == "fused"
+        if self._fused_head and (d % 256 != 0 or B * k > 8192):
+            raise ValueError("lm_head='fused' needs a hidden size that is a multiple of 256 and batch * k <= 8192")
+        self._w_p = pack_lm_head(self.lm_head_weight) if self._fused_head else None
         self.batch_size, self.k_draft, self.vocab_size, self.hidden_size = B, k, V, d
         self.static_hidden = torch.zeros(B, k, d, dtype=torch.bfloat16, device=device)
         self.static_base = torch.empty(B, k, V, dtype=torch.bfloat16, device=device)
@@ -60,10 +72,10 @@ class DeLSDraftStep:
         self.static_rest = torch.zeros(B, k - 1, dtype=torch.int64, device=device)
         self.static_rest_scores = torch.zeros(B, k - 1, dtype=torch.float32, device=device)
         self.static_out = torch.zeros(B, k, dtype=torch.int64, device=device)
-        lib = _lib.load()
         self._ws = new_workspace(device, max(lib.dels_rollout_ws_bytes(B, self.runner.gru_hidden_dim,
                                                                         self.runner.rank_dim, V),
-                                             lib.dels_argmax_rows_ws_bytes(B, V)))
+                                             lib.dels_argmax_rows_ws_bytes(B, V),
+                                             lib.dels_lm_head_ws_bytes(B * k, d, V)))
         self._params = self.runner._rollout_params(self.static_base[:, 1:, :], k * V, self.static_first,
                                                    self.static_rest, self.static_rest_scores, self._ws)
         self._graph = None
@@ -72,12 +84,20 @@ class DeLSDraftStep:
     def _enqueue(self, stream: torch.cuda.Stream) -> None:
         B, k, V, d = self.batch_size, self.k_draft, self.vocab_size, self.hidden_size
         lib = _lib.load()
-        # base logits of the whole block: [B*k, d] . W^T, as nn.Linear
-        torch.mm(self.static_hidden.view(B * k, d), self.lm_head_weight.t(), out=self.static_base.view(B * k, V))
-        _lib.check(lib.dels_argmax_rows(self.static_base.data_ptr(), k * V, _lib.DTYPE_BF16, B, V,
-                                        self.static_first.data_ptr(), self.static_first_score.data_ptr(), 1,
-                                        self._ws.data_ptr(), self._ws.numel(), stream.cuda_stream),
-                   "dels_argmax_rows")
+        if self._fused_head:
+            # base logits of positions 1..k-1 and the argmax of position 0 (rows b * k), one launch
+            _lib.check(lib.dels_lm_head(self.static_hidden.data_ptr(), d, self._w_p.data.data_ptr(), B * k, d, V,
+                                        self.static_base.data_ptr(), V, k, self.static_first.data_ptr(),
+                                        self.static_first_score.data_ptr(), 1, self._ws.data_ptr(),
+                                        self._ws.numel(), stream.cuda_stream), "dels_lm_head")
+        else:
+            # base logits of the whole block: [B*k, d] . W^T, as nn.Linear
+            torch.mm(self.static_hidden.view(B * k, d), self.lm_head_weight.t(),
+                     out=self.static_base.view(B * k, V))
+            _lib.check(lib.dels_argmax_rows(self.static_base.data_ptr(), k * V, _lib.DTYPE_BF16, B, V,
+                                            self.static_first.data_ptr(), self.static_first_score.data_ptr(), 1,
+                                            self._ws.data_ptr(), self._ws.numel(), stream.cuda_stream),
+                       "dels_argmax_rows")
         _lib.check(lib.dels_rollout_enqueue(ctypes.byref(self._params), stream.cuda_stream), "dels_rollout_enqueue")
         self.static_out[:, 0].copy_(self.static_first)
         self.static_out[:, 1:].copy_(self.static_rest)

@@ -16,6 +16,8 @@ Reference semantics (paths relative to the dt-3t/DeLS-Spec repository):
                           _reduce_argmax_kernel, code/kernel/markov_dels.py:15-138, 216-268
   * ``argmax_rows`` / ``sample_rows`` -- sample() at temperature 0 / above 0,
                           code/dflash.py:31-38
+  * ``lm_head``        -- target.lm_head(parallel_hiddens) with sample() of position 0
+                          fused, code/dflash.py:468, 475
   * ``domino_argmax``  -- a Domino correction step: _fused_mlp_bias_argmax_kernel +
                           _reduce_argmax_kernel, code/kernel/domino.py:58-173, 438-482
 """
@@ -74,6 +76,7 @@ class PackedWeight:
     data: torch.Tensor
     rows: int
     cols: int
+    kchunk: int = 0        # > 0: the blocks in K-chunk-major order (pack_lm_head)
 
     @property
     def shape(self) -> tuple[int, int]:
@@ -99,10 +102,28 @@ def pack_operand(W: torch.Tensor) -> PackedWeight:
     return PackedWeight(buf, int(rows), int(cols))
 
 
+LM_HEAD_KCHUNK = 4     # K blocks per chunk of the LM head's layout (kLmHeadKChunk)
+
+
+def pack_lm_head(W: torch.Tensor) -> PackedWeight:
+    """Repack a bf16 [V, K] LM-head weight (K a multiple of 128) into the LM head kernel's
+    layout: MFMA-16 blocks in K-chunk-major order (include/dels.h, dels_pack_lm_head)."""
+    _require_bf16_matrix(W, "W")
+    rows, cols = W.shape
+    lib = _lib.load()
+    nbytes = max(int(lib.dels_packed_bytes(rows, cols)), 16)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=W.device)
+    _lib.check(lib.dels_pack_lm_head(W.data_ptr(), W.stride(0), rows, cols, buf.data_ptr(), buf.numel(),
+                                     _stream_ptr(W.device)), "dels_pack_lm_head")
+    return PackedWeight(buf, int(rows), int(cols), LM_HEAD_KCHUNK)
+
+
 def _weight(w: Weight, name: str, cols: Optional[int] = None, rows: Optional[int] = None):
     """(pointer, leading dimension, layout code, rows, cols) of a weight operand."""
     if isinstance(w, PackedWeight):
         _require_cuda(w.data, name)
+        if w.kchunk:
+            raise ValueError(f"{name} is packed for the LM head (pack_lm_head); use pack_operand here")
         if cols is not None and w.cols != cols:
             raise ValueError(f"{name} has {w.cols} columns, expected {cols}")
         if rows is not None and w.rows != rows:
@@ -394,6 +415,48 @@ def argmax_rows(logits: torch.Tensor, *, out_ids: Optional[torch.Tensor] = None,
     return out_ids, out_score
 
 
+def lm_head(hidden: torch.Tensor, weight: Weight, *, out: Optional[torch.Tensor] = None, argmax_period: int = 0,
+            out_ids: Optional[torch.Tensor] = None,
+            out_score: Optional[torch.Tensor] = None) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor],
+                                                             Optional[torch.Tensor]]:
+    """``bf16(hidden . W^T)`` (code/dflash.py:468) with ``sample()`` of chosen rows fused
+    (code/dflash.py:475).  ``hidden`` [M, K] bf16; ``weight`` [V, K] (from ``pack_lm_head``,
+    or a bf16 matrix packed on the fly), K a multiple of 256.  With ``argmax_period`` p > 0
+    the rows m = j*p are argmaxed instead of stored (ids/scores [ceil(M/p)]).  ``out``
+    ([M, V] bf16, unit column stride) receives the other rows; allocated when None and
+    some row is stored.  Returns ``(out, ids, scores)`` (None where absent)."""
+    _require_bf16_matrix(hidden, "hidden")
+    M, K = hidden.shape
+    if not isinstance(weight, PackedWeight):
+        weight = pack_lm_head(weight)
+    if weight.kchunk != LM_HEAD_KCHUNK:
+        raise ValueError("weight must be packed by pack_lm_head")
+    _require_cuda(weight.data, "weight")
+    if weight.cols != K:
+        raise ValueError(f"weight has {weight.cols} columns, expected {K}")
+    V = weight.rows
+    dev = hidden.device
+    p = int(argmax_period)
+    stores = p != 1
+    if out is None and stores:
+        out = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    if out is not None:
+        _require_bf16_matrix(out, "out", rows=M, cols=V)
+    nrows = (M + p - 1) // p if p > 0 else 0
+    ids = sc = None
+    ld_out = 1
+    if p > 0:
+        ids, sc, ld_out = _outputs(out_ids, out_score, nrows, dev)
+    lib = _lib.load()
+    ws = workspace(dev, lib.dels_lm_head_ws_bytes(M, K, V))
+    _lib.check(lib.dels_lm_head(hidden.data_ptr(), hidden.stride(0), weight.data.data_ptr(), M, K, V,
+                                out.data_ptr() if out is not None else None, out.stride(0) if out is not None else V,
+                                p, ids.data_ptr() if ids is not None else None,
+                                sc.data_ptr() if sc is not None else None, ld_out, ws.data_ptr(), ws.numel(),
+                                _stream_ptr(dev)), "dels_lm_head")
+    return out, ids, sc
+
+
 def domino_argmax(z: torch.Tensor, s: torch.Tensor, fc2_weight: Weight, base_logits: torch.Tensor,
                   guidance_alpha: float, fc2_bias: Optional[torch.Tensor] = None, *,
                   out_ids: Optional[torch.Tensor] = None,
@@ -408,6 +471,8 @@ def domino_argmax(z: torch.Tensor, s: torch.Tensor, fc2_weight: Weight, base_log
     _require_bf16_matrix(s, "s", rows=M, cols=E)
     if not isinstance(fc2_weight, PackedWeight):
         fc2_weight = pack_operand(fc2_weight)
+    if fc2_weight.kchunk:
+        raise ValueError("fc2_weight is packed for the LM head (pack_lm_head); use pack_operand")
     _require_cuda(fc2_weight.data, "fc2_weight")
     if fc2_weight.cols != E:
         raise ValueError(f"fc2_weight has {fc2_weight.cols} columns, expected {E}")

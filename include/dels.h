@@ -340,6 +340,30 @@ int dels_graph_launch(void* graph, void* stream);
 int dels_graph_destroy(void* graph);
 
 /*
+ * Target LM head of a draft block (code/dflash.py:468, target.lm_head(
+ * parallel_hiddens)), with sample() of chosen rows fused (code/dflash.py:475):
+ *   base[m, v] = bf16(hidden[m] . W[v])   (fp32 accumulate, one rounding).
+ * hidden [M, K] bf16 (leading dimension ldh, 16-byte aligned, ldh % 8 == 0);
+ * W [V, K] bf16 packed by dels_pack_lm_head; K a multiple of 256.
+ * With argmax_period > 0, rows m with m % argmax_period == 0 are not stored:
+ * out_ids[j * ld_out] (and out_score) receive the argmax of row j*argmax_period
+ * over its bf16 values (lowest index on ties, first NaN wins), as
+ * sample(base[:, :1]) of a [batch, argmax_period, V] block.  Every other row
+ * goes to base (leading dimension ldo) when base is not NULL.
+ */
+size_t dels_lm_head_ws_bytes(int64_t M, int64_t K, int64_t V);
+/* dels_pack_lm_head: W [rows, cols] bf16 row-major into the LM head's layout --
+ * the MFMA-16 blocks in K-chunk-major order (4 blocks of 32 K per chunk: the
+ * 4 KiB of a 16-row tile in one chunk, then the next tile of the same chunk);
+ * cols a multiple of 128; `packed` holds dels_packed_bytes(rows, cols) bytes. */
+int dels_pack_lm_head(const void* W, int64_t ldw, int64_t rows, int64_t cols, void* packed, size_t packed_bytes,
+                      void* stream);
+int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int64_t K, int64_t V,
+                 void* base, int64_t ldo, int64_t argmax_period,
+                 int64_t* out_ids, float* out_score, int64_t ld_out,
+                 void* ws, size_t ws_bytes, void* stream);
+
+/*
  * Domino correction step (DraftCorrectionGraphRunner._fused_step_triton,
  * code/kernel/domino.py:58-173, 438-482): for rows m < M of z and s [M, E]
  * bf16 (the hidden-state and GRU-state parts of the correction MLP's first

@@ -1,11 +1,13 @@
 """GPU tests of the plain row argmax (sample() at temperature 0) and of the whole
 draft block as one graph (target LM head GEMM, first-position argmax, rollout).
 
-The LM-head GEMM is a library GEMM (hipBLASLt through torch.mm, as nn.Linear in
-the reference); its bf16 output is checked against a float32 CPU product within
-bf16 rounding, and the argmax and the rollout are then checked on the device's
-own base logits (the rollout teacher-forced on the device's ids, as for
-DeLSGraphRunner).
+The LM head is either the library GEMM (hipBLASLt through torch.mm) followed
+by the row argmax, or the hand-written dels_lm_head with the first-position
+argmax fused (position-0 logits are never stored); its bf16 output is checked
+against a float32 product within bf16 rounding, the first ids against
+torch.argmax of the same LM head's values (for the fused head a launch that
+stores every row), and the rollout on the device's own base logits
+(teacher-forced on the device's ids, as for DeLSGraphRunner).
 """
 
 import numpy as np
@@ -48,10 +50,11 @@ def test_argmax_rows(pkg, dev, M, V, dtype, stride_pad):
     np.testing.assert_array_equal(got[~np.isnan(want)], want[~np.isnan(want)])
 
 
+@pytest.mark.parametrize("lm_head", ["library", "fused"])
 @pytest.mark.parametrize("B,k,d,V,E,G,r,act,with_prior", [(3, 6, 256, 5003, 32, 64, 64, "silu", True),
                                                           (8, 15, 512, 30000, 64, 128, 256, "identity", False)])
-def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
-    print(f"case draft_step B={B} k={k} d={d} V={V} G={G} r={r}", flush=True)
+def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior, lm_head):
+    print(f"case draft_step B={B} k={k} d={d} V={V} G={G} r={r} lm_head={lm_head}", flush=True)
     head = _Head(V, E, G, r, act, False, seed=B + V, std=0.2).to(dev)
     g = torch.Generator().manual_seed(7)
     W = (torch.randn(V, d, generator=g) * 0.05).bfloat16()
@@ -60,7 +63,8 @@ def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
     alphas = [0.1 + 0.05 * i for i in range(steps)]
     betas = [0.3 if with_prior else 0.0] * steps
     step = pkg.DeLSDraftStep(local_head=head, lm_head_weight=W.to(dev), batch_size=B, k_draft=k, vocab_size=V,
-                             alpha_values=alphas, beta_values=betas, baseline_logits=prior, device=dev)
+                             alpha_values=alphas, beta_values=betas, baseline_logits=prior, device=dev,
+                             lm_head=lm_head)
     hid = (torch.randn(B, k, d, generator=g)).bfloat16()
     out = step(hid.to(dev))
     torch.cuda.synchronize()
@@ -72,12 +76,20 @@ def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
     torch.testing.assert_close(out2, out, rtol=0, atol=0)
     torch.testing.assert_close(step.static_out, out, rtol=0, atol=0)
     assert out.shape == (B, k) and out.dtype == torch.int64
-    # the GEMM is the LM head: base = bf16(hidden . W^T)
+    # the GEMM is the LM head: base = bf16(hidden . W^T) (positions 1.. stored)
     ref_base = (f(hid).reshape(B * k, d) @ f(W).T).reshape(B, k, V)
-    np.testing.assert_allclose(f(base), ref_base, rtol=2e-2, atol=2e-2)
-    # first position: plain argmax of the device's base logits
+    np.testing.assert_allclose(f(base)[:, 1:], ref_base[:, 1:], rtol=2e-2, atol=2e-2)
+    # first position: argmax of the LM head's own bf16 logits of position 0 (the fused
+    # head does not store them: a second launch of the same kernel stores every row)
+    if lm_head == "fused":
+        full, _, _ = pkg.lm_head(hid.to(dev).reshape(B * k, d), step._w_p)
+        torch.cuda.synchronize()
+        full = full.reshape(B, k, V)
+        torch.testing.assert_close(full[:, 1:], base[:, 1:], rtol=0, atol=0)
+    else:
+        full = base
+    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(full[:, 0, :].cpu(), dim=-1).numpy())
     bn = f(base)
-    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(base[:, 0, :].cpu(), dim=-1).numpy())
     # the rollout on base[:, 1:], teacher-forced on the device's own ids
     prior_np = f(prior.to(torch.bfloat16)) if with_prior else None
     dev_ids = out[:, 1:].cpu().numpy()
@@ -92,18 +104,20 @@ def test_draft_step(pkg, dev, B, k, d, V, E, G, r, act, with_prior):
     step.close()
 
 
-def test_draft_step_full_size(pkg, dev):
+@pytest.mark.parametrize("lm_head", ["library", "fused"])
+def test_draft_step_full_size(pkg, dev, lm_head):
     """The whole draft block at the size the bench times: batch 8, block 16 (k_draft 15,
     14 DeLS steps), W [151936, 4096], local head E = G = 1024, r = 256, silu, bf16 base,
     the Zipf prior and per-step alpha/beta (synth.draft_block_workload).  The LM-head
     GEMM against a float32 CPU product on a sample of rows, the first position against
     torch.argmax, and the 14-step rollout teacher-forced against the oracle."""
-    print("case draft_step full size B=8 k=15 d=4096 V=151936 G=1024 r=256", flush=True)
+    print(f"case draft_step full size B=8 k=15 d=4096 V=151936 G=1024 r=256 lm_head={lm_head}", flush=True)
     wl = pkg.synth.draft_block_workload(dev)
     B, k, d, V = wl.batch, wl.k_draft, wl.d, wl.V
     head = wl.head
     step = pkg.DeLSDraftStep(local_head=head, lm_head_weight=wl.W, batch_size=B, k_draft=k, vocab_size=V,
-                             alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior, device=dev)
+                             alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior, device=dev,
+                             lm_head=lm_head)
     hid = wl.hiddens(1)[0]
     out = step(hid)
     torch.cuda.synchronize()
@@ -111,16 +125,25 @@ def test_draft_step_full_size(pkg, dev):
     out2 = step(hid)
     torch.cuda.synchronize()
     torch.testing.assert_close(out2, out, rtol=0, atol=0)
-    # LM head on a row sample (rows (b, position) of the [B*k, V] product)
-    rows = [0, 17, 45, 77, 119]
+    # LM head on a row sample (rows (b, position) of the [B*k, V] product; position 0
+    # rows are argmaxed in the kernel, not stored)
+    rows = [1, 17, 44, 77, 119]
     hid_rows = f(hid).reshape(B * k, d)[rows]
     W_np = f(wl.W)
     ref_rows = hid_rows @ W_np.T
     got_rows = f(base).reshape(B * k, V)[rows]
     np.testing.assert_allclose(got_rows, ref_rows, rtol=1e-2, atol=2e-3)      # bf16 output rounding
     del W_np
-    # first draft position: torch.argmax of the device's bf16 base logits
-    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(base[:, 0, :].cpu(), dim=-1).numpy())
+    # first draft position: torch.argmax of the LM head's own bf16 logits of position 0
+    if lm_head == "fused":
+        full, _, _ = pkg.lm_head(hid.reshape(B * k, d), step._w_p)
+        torch.cuda.synchronize()
+        full = full.reshape(B, k, V)
+        torch.testing.assert_close(full[:, 1:], base[:, 1:], rtol=0, atol=0)
+    else:
+        full = base
+    np.testing.assert_array_equal(out[:, 0].cpu().numpy(), torch.argmax(full[:, 0, :].cpu(), dim=-1).numpy())
+    del full
     # the rollout over base[:, 1:], teacher-forced on the device's own ids
     bn = f(base)
     dev_ids = out[:, 1:].cpu().numpy()
