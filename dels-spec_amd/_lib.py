@@ -14,7 +14,9 @@ import threading
 import torch  # noqa: F401  -- loads torch's HIP runtime first, so the library binds to it
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
+# DELS_LIBRARY_PATH names another build of the same library (an instrumented
+# one, say); by default the in-tree build is loaded.
+LIB_PATH = os.environ.get("DELS_LIBRARY_PATH") or os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
 
 ABI_VERSION = 2
 DELS_OK = 0

@@ -42,9 +42,15 @@ def hipcc() -> str:
     return cand if os.path.exists(cand) else (shutil.which("hipcc") or "hipcc")
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every HIP source for gfx950 and link the shared library."""
-    os.makedirs(LIB_DIR, exist_ok=True)
+def build(verbose: bool = False, jobs: int | None = None, *, lib_path: str = LIB_PATH,
+          extra_flags: tuple[str, ...] = (), link_flags: tuple[str, ...] = ()) -> str:
+    """Compile every HIP source for gfx950 and link the shared library.
+
+    ``extra_flags`` are added to every compile line and ``link_flags`` to the
+    link line; with ``lib_path`` they give instrumented variants (the host-side
+    sanitizer build of the tests) without touching the product library.
+    """
+    os.makedirs(os.path.dirname(lib_path), exist_ok=True)
     inc = ["-I", os.path.join(REPO_DIR, "include"), "-I", CSRC]
     tmp = tempfile.mkdtemp(prefix="dels_build_")
     try:
@@ -52,7 +58,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         procs = []
         for src in SOURCES:
             obj = os.path.join(tmp, src.replace(".hip", ".o"))
-            cmd = [hipcc(), *HIP_FLAGS, *inc, "-c", os.path.join(CSRC, src), "-o", obj]
+            cmd = [hipcc(), *HIP_FLAGS, *extra_flags, *inc, "-c", os.path.join(CSRC, src), "-o", obj]
             if verbose:
                 print(" ".join(cmd), flush=True)
             procs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
@@ -70,15 +76,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
                 sys.stderr.write(text + "\n")
         if failed:
             raise RuntimeError(f"hipcc failed on {failed}")
-        tmp_lib = LIB_PATH + ".tmp"
-        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp_lib, *objs]
+        tmp_lib = lib_path + ".tmp"
+        cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", *link_flags, "-o", tmp_lib, *objs]
         if verbose:
             print(" ".join(cmd), flush=True)
         subprocess.run(cmd, check=True)
-        os.replace(tmp_lib, LIB_PATH)
+        os.replace(tmp_lib, lib_path)
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
-    return LIB_PATH
+    return lib_path
 
 
 if __name__ == "__main__":

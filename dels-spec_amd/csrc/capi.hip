@@ -7,6 +7,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
@@ -68,8 +69,25 @@ static inline bool valid_dtype(int d) { return d == DELS_DTYPE_F32 || d == DELS_
 static inline size_t dtype_size(int d) { return d == DELS_DTYPE_F32 ? 4 : 2; }
 
 // Checks of a bf16 row-major operand: non-null, 16-byte aligned, ld % 8 == 0, ld >= cols.
+// Extents every entry point keeps within: rows, batch, batch * steps, r, G and
+// E in [0, 2^24), hidden sizes (d, D, K) in [0, 2^26), V in [0, 2^31 - 1).
+// Within them all size arithmetic stays below 2^60; the size queries answer 0
+// for a shape outside them, and check_ws() refuses a need of 0.
+static bool rows_ok(int64_t x) { return x >= 0 && x < (int64_t(1) << 24); }
+static bool inner_ok(int64_t x) { return x >= 0 && x < (int64_t(1) << 26); }
+static bool vocab_ok(int64_t x) { return x >= 0 && x < INT32_MAX; }
+// Leading dimensions and strides (in elements) lie in [0, 2^40), so that every
+// element offset the kernels form stays far inside 64 bits.
+static bool ld_ok(std::initializer_list<int64_t> xs) {
+    for (int64_t x : xs)
+        if (x < 0 || x >= (int64_t(1) << 40)) return false;
+    return true;
+}
+
 static int check_bf16_matrix(const void* p, int64_t ld, int64_t cols, const char* name) {
     if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "%s is NULL", name);
+    if (!ld_ok({ld})) return fail(DELS_ERR_INVALID_ARGUMENT, "%s: leading dimension %lld out of range", name,
+                                  (long long)ld);
     if (ld < cols) return fail(DELS_ERR_INVALID_ARGUMENT, "%s: leading dimension %lld < columns %lld", name,
                                (long long)ld, (long long)cols);
     if (!aligned16(p) || (ld % 8) != 0)
@@ -151,13 +169,15 @@ static int check_argmax_args(const void* rank, int64_t ldrank, const void* B, in
     if (prior && !valid_dtype(prior_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown prior dtype %d", prior_dtype);
     if (!alpha || !beta) return fail(DELS_ERR_INVALID_ARGUMENT, "alpha/beta pointers must be non-NULL");
     if (alpha_stride < 0 || beta_stride < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "negative alpha/beta stride");
+    if (!ld_ok({ldbase, alpha_stride, beta_stride, ld_out}))
+        return fail(DELS_ERR_INVALID_ARGUMENT, "leading dimension or stride out of range");
     if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
     if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
     return DELS_OK;
 }
 
 static int check_ws(const void* ws, size_t ws_bytes, size_t need) {
-    if (need == 0) return DELS_OK;
+    if (need == 0) return fail(DELS_ERR_UNSUPPORTED, "shape past the supported extents");
     if (!ws) return fail(DELS_ERR_WORKSPACE, "workspace is NULL (%zu bytes needed)", need);
     if ((reinterpret_cast<uintptr_t>(ws) & 255u) != 0) return fail(DELS_ERR_WORKSPACE, "workspace must be 256-byte aligned");
     if (ws_bytes < need) return fail(DELS_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", ws_bytes, need);
@@ -175,6 +195,7 @@ static int check_gru_args(const void* gi_table, int64_t ld_gi, int64_t table_row
     if (batch == 0) return DELS_OK;
     if (!gi_table || table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "GRU input table is NULL or empty");
     if (ld_gi < 3 * G) return fail(DELS_ERR_INVALID_ARGUMENT, "GRU input table leading dimension < 3G");
+    if (!ld_ok({ld_gi, ldh_out})) return fail(DELS_ERR_INVALID_ARGUMENT, "GRU leading dimension out of range");
     if (!tokens) return fail(DELS_ERR_INVALID_ARGUMENT, "token ids pointer is NULL");
     int rc;
     if (h_in && (rc = check_bf16_matrix(h_in, ldh_in, G, "h_in")) != DELS_OK) return rc;
@@ -193,6 +214,8 @@ static int check_rollout(const dels_rollout* p) {
     if (!p) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout parameters are NULL");
     if (p->steps <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires steps > 0, got %lld", (long long)p->steps);
     if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires batch > 0");
+    if (!rows_ok(p->steps) || !rows_ok(p->r) || !vocab_ok(p->V))
+        return fail(DELS_ERR_UNSUPPORTED, "rollout: steps and r below 2^24, V below 2^31-1");
     if (p->act != DELS_ACT_IDENTITY && p->act != DELS_ACT_SILU)
         return fail(DELS_ERR_INVALID_ARGUMENT, "unknown rank activation %d", p->act);
     int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
@@ -333,6 +356,8 @@ static int check_markov(const dels_markov_rollout* p) {
     if (p->steps <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout requires steps > 0, got %lld",
                                    (long long)p->steps);
     if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Markov rollout requires batch > 0");
+    if (!rows_ok(p->steps) || !rows_ok(p->r) || !vocab_ok(p->V))
+        return fail(DELS_ERR_UNSUPPORTED, "Markov rollout: steps and r below 2^24, V below 2^31-1");
     if (!p->prev_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "prev_ids is NULL");
     if (p->table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "embedding table is empty");
     int rc = check_bf16_matrix(p->embedding, p->ld_embedding, p->r, "embedding");
@@ -462,6 +487,7 @@ static int check_domino_step(const void* z, int64_t ldz, const void* sv, int64_t
     if (!z || !sv) return fail(DELS_ERR_INVALID_ARGUMENT, "z or s is NULL");
     if ((M > 1 && (ldz < E || lds < E)) || ldz < 0 || lds < 0)
         return fail(DELS_ERR_INVALID_ARGUMENT, "z/s leading dimension < E");
+    if (!ld_ok({ldz, lds, ldbase, ld_out})) return fail(DELS_ERR_INVALID_ARGUMENT, "leading dimension out of range");
     if (!fc2_w) return fail(DELS_ERR_INVALID_ARGUMENT, "fc2 weight is NULL");
     if (!aligned16(fc2_w)) return fail(DELS_ERR_ALIGNMENT, "packed fc2 weight must be 16-byte aligned");
     if (fc2_bias && !valid_dtype(fc2_bias_dtype)) return fail(DELS_ERR_INVALID_ARGUMENT, "unknown fc2 bias dtype %d",
@@ -498,6 +524,10 @@ static int check_domino_rollout(const dels_domino_rollout* p) {
     if (p->batch <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "rollout requires batch > 0");
     if (p->prefix_len <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "Domino rollout requires prefix_len > 0");
     if (p->D <= 0 || p->D % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size D must be a positive multiple of 8");
+    if (!rows_ok(p->steps) || !rows_ok(p->batch) || !rows_ok(p->batch * p->steps) || !inner_ok(p->D) ||
+        !rows_ok(p->E) || !vocab_ok(p->V))
+        return fail(DELS_ERR_UNSUPPORTED, "Domino rollout: batch * steps and E below 2^24, D below 2^26, "
+                    "V below 2^31-1");
     int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
                             p->weights_layout, p->batch, p->G, p->h_b, p->G);
     if (rc != DELS_OK) return rc;
@@ -626,13 +656,14 @@ int dels_workspace_init(void* ws, size_t ws_bytes, void* stream) {
 }
 
 size_t dels_packed_bytes(int64_t rows, int64_t cols) {
-    if (rows <= 0 || cols <= 0) return 0;
+    if (rows <= 0 || cols <= 0 || !vocab_ok(rows) || !inner_ok(cols)) return 0;
     return packed_bytes(rows, cols);
 }
 
 int dels_pack_operand(const void* W, int64_t ldw, int64_t rows, int64_t cols, void* packed, size_t packed_bytes_,
                       void* stream) {
     if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
+    if (!vocab_ok(rows) || !inner_ok(cols)) return fail(DELS_ERR_UNSUPPORTED, "pack: rows below 2^31-1, cols below 2^26");
     if (rows == 0 || cols == 0) return DELS_OK;
     int rc = check_bf16_matrix(W, ldw, cols, "W (to pack)");
     if (rc != DELS_OK) return rc;
@@ -646,6 +677,7 @@ int dels_pack_operand(const void* W, int64_t ldw, int64_t rows, int64_t cols, vo
 }
 
 size_t dels_rank_proj_ws_bytes(int64_t M, int64_t d, int64_t r) {
+    if (!rows_ok(M) || !inner_ok(d) || !rows_ok(r)) return 0;
     return kDataOff + skinny_data_bytes(plan_skinny(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1),
                                                       std::max<int64_t>(r, 1), false));
 }
@@ -678,6 +710,7 @@ int dels_rank_proj(const void* h, int64_t ldh, const void* A, int64_t lda, int a
 }
 
 size_t dels_fused_argmax_ws_bytes(int64_t M, int64_t r, int64_t V) {
+    if (!rows_ok(M) || !rows_ok(r) || !vocab_ok(V)) return 0;
     return kDataOff + align256(argmax_data_bytes(M, r, V));
 }
 
@@ -707,6 +740,7 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
 int dels_debug_set_decode_spin_limit(int limit) { return set_decode_spin_limit(limit); }
 
 size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) {
+    if (!rows_ok(M) || !inner_ok(d) || !rows_ok(r) || !vocab_ok(V)) return 0;
     return lowrank_layout(std::max<int64_t>(M, 1), std::max<int64_t>(d, 1), std::max<int64_t>(r, 1),
                           std::max<int64_t>(V, 1)).total;
 }
@@ -720,7 +754,8 @@ int dels_lowrank_argmax(const void* h, int64_t ldh, const void* A, int64_t lda, 
     int rc = check_argmax_args(nullptr, r, B, ldb, b_layout, base, ldbase, base_dtype, prior, prior_dtype, alpha,
                                alpha_stride, beta, beta_stride, M, r, V, out_ids, ld_out, false);
     if (rc != DELS_OK) return rc;
-    if (d <= 0 || d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8",
+    if (d <= 0 || d % 8 != 0 || !inner_ok(d))
+        return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8 below 2^26",
                                           (long long)d);
     if (act != DELS_ACT_IDENTITY && act != DELS_ACT_SILU)
         return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
@@ -793,7 +828,8 @@ static int check_scale(const float* p, const char* name) {
 static bool fp8_rank_ok(int64_t r) { return r == 128 || r == 256 || r == 512; }
 
 size_t dels_packed_fp8_bytes(int64_t rows, int64_t cols, int layout) {
-    if (rows <= 0 || cols <= 0 || (layout != DELS_LAYOUT_FP8_K128 && layout != DELS_LAYOUT_FP8_K32)) return 0;
+    if (rows <= 0 || cols <= 0 || !vocab_ok(rows) || !inner_ok(cols)) return 0;
+    if (layout != DELS_LAYOUT_FP8_K128 && layout != DELS_LAYOUT_FP8_K32) return 0;
     return packed_fp8_bytes(rows, cols, layout == DELS_LAYOUT_FP8_K128 ? FP8_K128 : FP8_K32);
 }
 
@@ -802,6 +838,7 @@ int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t col
     if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
     if (layout != DELS_LAYOUT_FP8_K128 && layout != DELS_LAYOUT_FP8_K32)
         return fail(DELS_ERR_INVALID_ARGUMENT, "unknown fp8 layout %d", layout);
+    if (!vocab_ok(rows) || !inner_ok(cols)) return fail(DELS_ERR_UNSUPPORTED, "pack: rows below 2^31-1, cols below 2^26");
     if (rows == 0 || cols == 0) return DELS_OK;
     if (!Wq) return fail(DELS_ERR_INVALID_ARGUMENT, "W (to pack) is NULL");
     if (rows > 1 && ldw < cols) return fail(DELS_ERR_INVALID_ARGUMENT, "W leading dimension %lld < cols %lld",
@@ -818,6 +855,7 @@ int dels_pack_operand_fp8(const void* Wq, int64_t ldw, int64_t rows, int64_t col
 }
 
 size_t dels_fused_argmax_fp8_ws_bytes(int64_t M, int64_t r, int64_t V) {
+    if (!rows_ok(M) || !rows_ok(r) || !vocab_ok(V)) return 0;
     return kDataOff + align256(argmax_fp8_data_bytes(M, r, V));
 }
 
@@ -873,7 +911,8 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
     if (!fp8_rank_ok(r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax needs r in {128, 256, 512} (got %lld)",
                                      (long long)r);
     if (!argmax_fp8_supported(M, r)) return fail(DELS_ERR_UNSUPPORTED, "fp8 argmax: too many rows");
-    if (d <= 0 || d % 8 != 0) return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8",
+    if (d <= 0 || d % 8 != 0 || !inner_ok(d))
+        return fail(DELS_ERR_UNSUPPORTED, "hidden size d=%lld must be a positive multiple of 8 below 2^26",
                                           (long long)d);
     if (act != DELS_ACT_IDENTITY && act != DELS_ACT_SILU)
         return fail(DELS_ERR_INVALID_ARGUMENT, "Unsupported DeLS rank_activation code %d", act);
@@ -924,6 +963,7 @@ int dels_argmax_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
                                       (long long)ldx, (long long)V);
     if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
     if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    if (!ld_ok({ldx, ld_out})) return fail(DELS_ERR_INVALID_ARGUMENT, "leading dimension out of range");
     int rc = check_ws(ws, ws_bytes, kDataOff);
     if (rc != DELS_OK) return rc;
     hipError_t e = launch_argmax_rows(x, ldx, dtype, (int)M, (int)V, out_ids, out_score, ld_out, ws,
@@ -951,6 +991,7 @@ int dels_sample_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
                                       (long long)ldx, (long long)V);
     if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
     if (M > 1 && ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
+    if (!ld_ok({ldx, ld_out})) return fail(DELS_ERR_INVALID_ARGUMENT, "leading dimension out of range");
     int rc = check_ws(ws, ws_bytes, kDataOff);
     if (rc != DELS_OK) return rc;
     hipError_t e = launch_sample_rows(x, ldx, dtype, (int)M, (int)V, temperature, seed, offset, out_ids, out_score,
@@ -959,6 +1000,7 @@ int dels_sample_rows(const void* x, int64_t ldx, int dtype, int64_t M, int64_t V
 }
 
 size_t dels_gru_step_ws_bytes(int64_t batch, int64_t G) {
+    if (!rows_ok(batch) || !rows_ok(G)) return 0;
     return kDataOff + skinny_data_bytes(plan_skinny(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1),
                                                       std::max<int64_t>(G, 1), true));
 }
@@ -971,6 +1013,7 @@ int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const
     int rc = check_gru_args(gi_table, ld_gi, table_rows, tokens, h_in, ldh_in, w_hh, w_layout, batch, G, h_out,
                             ldh_out);
     if (rc != DELS_OK) return rc;
+    if (!ld_ok({tok_stride})) return fail(DELS_ERR_INVALID_ARGUMENT, "token stride out of range");
     if (batch == 0) return DELS_OK;
     const SkinnyPlan p = plan_skinny(batch, G, G, true);
     if (!skinny_supported(p)) return fail(DELS_ERR_UNSUPPORTED, "GRU shape needs too many tiles");
@@ -988,6 +1031,7 @@ int dels_gru_step(const void* gi_table, int64_t ld_gi, int64_t table_rows, const
 }
 
 size_t dels_rollout_ws_bytes(int64_t batch, int64_t G, int64_t r, int64_t V) {
+    if (!rows_ok(batch) || !rows_ok(G) || !rows_ok(r) || !vocab_ok(V)) return 0;
     return rollout_layout(std::max<int64_t>(batch, 1), std::max<int64_t>(G, 1), std::max<int64_t>(r, 1),
                           std::max<int64_t>(V, 1)).total;
 }
@@ -1019,6 +1063,7 @@ int dels_gather_argmax(const int64_t* tokens, int64_t tok_stride, const void* E,
     if (M == 0) return DELS_OK;
     if (!tokens) return fail(DELS_ERR_INVALID_ARGUMENT, "token ids pointer is NULL");
     if (table_rows <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "embedding table is empty");
+    if (!ld_ok({tok_stride})) return fail(DELS_ERR_INVALID_ARGUMENT, "token stride out of range");
     if ((rc = check_bf16_matrix(E, lde, r, "E (embedding table)")) != DELS_OK) return rc;
     if ((rc = check_ws(ws, ws_bytes, dels_gather_argmax_ws_bytes(M, r, V))) != DELS_OK) return rc;
     ArgmaxArgs a = gather_args(tokens, tok_stride, E, lde, table_rows, B, ldb, b_layout, base, ldbase, base_dtype,
@@ -1029,6 +1074,7 @@ int dels_gather_argmax(const int64_t* tokens, int64_t tok_stride, const void* E,
 }
 
 size_t dels_markov_rollout_ws_bytes(int64_t batch, int64_t r, int64_t V) {
+    if (!rows_ok(batch) || !rows_ok(r) || !vocab_ok(V)) return 0;
     return kDataOff + align256(argmax_data_bytes(std::max<int64_t>(batch, 1), std::max<int64_t>(r, 1),
                                                  std::max<int64_t>(V, 1)));
 }
@@ -1052,6 +1098,7 @@ size_t dels_lm_head_ws_bytes(int64_t, int64_t, int64_t) { return kDataOff; }
 int dels_pack_lm_head(const void* W, int64_t ldw, int64_t rows, int64_t cols, void* packed, size_t packed_bytes_,
                       void* stream) {
     if (rows < 0 || cols < 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape to pack");
+    if (!vocab_ok(rows) || !inner_ok(cols)) return fail(DELS_ERR_UNSUPPORTED, "pack: rows below 2^31-1, cols below 2^26");
     if (cols % (32 * kLmHeadKChunk) != 0)
         return fail(DELS_ERR_UNSUPPORTED, "LM head layout: cols=%lld must be a multiple of %d", (long long)cols,
                     32 * kLmHeadKChunk);
@@ -1083,6 +1130,7 @@ int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int6
     if (!aligned16(W)) return fail(DELS_ERR_ALIGNMENT, "packed W must be 16-byte aligned");
     if (base && M > 1 && ldo < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
                                               (long long)ldo, (long long)V);
+    if (!ld_ok({ldo, ld_out})) return fail(DELS_ERR_INVALID_ARGUMENT, "leading dimension out of range");
     if (argmax_period > 0) {
         if (!out_ids) return fail(DELS_ERR_INVALID_ARGUMENT, "out_ids is NULL");
         if (ld_out < 1) return fail(DELS_ERR_INVALID_ARGUMENT, "ld_out must be >= 1");
@@ -1111,7 +1159,9 @@ int dels_domino_argmax(const void* z, int64_t ldz, const void* sv, int64_t lds, 
 }
 
 size_t dels_domino_rollout_ws_bytes(int64_t batch, int64_t steps, int64_t D, int64_t G, int64_t E, int64_t V) {
-    (void)V;
+    if (!rows_ok(batch) || !rows_ok(steps) || !rows_ok(batch * steps) || !inner_ok(D) || !rows_ok(G) ||
+        !rows_ok(E) || !vocab_ok(V))
+        return 0;
     return domino_layout(std::max<int64_t>(batch, 1), std::max<int64_t>(steps, 1), std::max<int64_t>(D, 1),
                          std::max<int64_t>(G, 1), std::max<int64_t>(E, 1)).total;
 }

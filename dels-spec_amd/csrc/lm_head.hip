@@ -300,9 +300,10 @@ __global__ __launch_bounds__(kLhThreads) void lm_head_kernel(LmHeadArgs a) {
 }  // namespace
 
 bool lm_head_supported(int64_t M, int64_t K, int64_t V, int64_t argmax_period) {
-    if (M < 1 || K % (64 * kLhKC) != 0 || V < 1 || V >= INT32_MAX) return false;   // an even chunk count
-    if (argmax_period < 0 || (argmax_period > 0 && (M + argmax_period - 1) / argmax_period > kMaxKeyRows)) return false;
-    return M <= (int64_t)kLhRows * 64;
+    if (M < 1 || M > (int64_t)kLhRows * 64 || V < 1 || V >= INT32_MAX) return false;
+    if (K < 1 || K >= (int64_t(1) << 26) || K % (64 * kLhKC) != 0) return false;   // an even chunk count
+    if (argmax_period < 0 || argmax_period >= (int64_t(1) << 24)) return false;
+    return argmax_period == 0 || (M - 1) / argmax_period + 1 <= kMaxKeyRows;
 }
 
 hipError_t launch_lm_head(const void* hidden, int64_t ldh, const void* W, int M, int K, int V, void* base,

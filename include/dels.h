@@ -31,6 +31,10 @@
  *    that may hold anything between calls.  One workspace may therefore serve
  *    every entry point and shape in turn; calls that share it must not
  *    overlap in time (same stream is fine).
+ *  - Extents: rows, batch, batch * steps, r, G and E below 2^24, hidden sizes
+ *    (d, D, K) below 2^26, V below 2^31 - 1, leading dimensions and strides
+ *    in [0, 2^40) elements.  Calls outside them fail their checks, and the
+ *    *_ws_bytes() / *_packed_*bytes() queries return 0 for such shapes.
  *  - Return value: DELS_OK (0) or a negative DELS_ERR_* code; no exception
  *    crosses the ABI.  dels_strerror() names a code, dels_last_error() gives
  *    the detail of the calling thread's last failure.
