@@ -1126,6 +1126,8 @@ int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int6
                     "at most %d argmax rows", (long long)K, kMaxKeyRows);
     int rc;
     if ((rc = check_bf16_matrix(hidden, ldh, K, "hidden")) != DELS_OK) return rc;
+    if (((M - 1) * ldh + K) * 2 >= (int64_t(1) << 31))
+        return fail(DELS_ERR_UNSUPPORTED, "LM head: the hidden rows must span less than 2 GiB");
     if (!W) return fail(DELS_ERR_INVALID_ARGUMENT, "W is NULL");
     if (!aligned16(W)) return fail(DELS_ERR_ALIGNMENT, "packed W must be 16-byte aligned");
     if (base && M > 1 && ldo < V) return fail(DELS_ERR_INVALID_ARGUMENT, "base leading dimension %lld < V %lld",
