@@ -264,6 +264,10 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     uint16_t* h_cur = static_cast<uint16_t*>(p->h_a);
     uint16_t* h_next = static_cast<uint16_t*>(p->h_b);
     const size_t esz = dtype_size(p->base_dtype);
+    const bool packed = p->weights_layout == DELS_LAYOUT_MFMA16;
+    const bool use_decode = G >= kRolloutDecodeMinG && decode_eligible(B, G, r, packed, packed);
+    // steps 1.. advance the GRU inside the decode launch (no GRU launch between steps)
+    const bool fuse_gru = use_decode && decode_gru_eligible(B, G, r);
     for (int step = 0; step < p->steps; ++step) {
         RankArgs ra{};
         ra.h = h_cur; ra.ldh = G;
@@ -288,7 +292,18 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
 
-        if (G >= kRolloutDecodeMinG && decode_eligible(B, G, r, ra.a_packed, aa.b_packed)) {
+        if (fuse_gru && step > 0) {
+            // h = GRU(gi_table[previous ids], h), rank projection and argmax in one launch
+            DecodeGru dg{};
+            dg.gi_table = g.gi_table; dg.ld_gi = g.ld_gi; dg.table_rows = g.table_rows;
+            dg.tokens = p->out_ids + (step - 1); dg.tok_stride = p->steps;
+            dg.w_hh = g.w_hh; dg.b_hh = g.b_hh;
+            dg.h_prev = h_cur; dg.h_out = h_next;
+            ra.h = h_next;
+            e = launch_lowrank_decode(ra, aa, ws, s, &dg);
+            if (e != hipSuccess) return hip_fail(e, "fused rollout step launch");
+            std::swap(h_cur, h_next);
+        } else if (use_decode) {
             // rank projection and argmax in one launch
             e = launch_lowrank_decode(ra, aa, ws, s);
             if (e != hipSuccess) return hip_fail(e, "fused decode step launch");
@@ -299,7 +314,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
             if (e != hipSuccess) return hip_fail(e, "fused argmax launch");
         }
 
-        if (step + 1 < p->steps) {
+        if (step + 1 < p->steps && !fuse_gru) {
             g.tokens = p->out_ids + step;
             g.tok_stride = p->steps;
             g.h_in = h_cur;

@@ -157,6 +157,18 @@ __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + ex
 
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
+// New GRU state of one unit from its input-side (gi) and hidden-side (gh,
+// already rounded to bf16) gate pre-activations and its previous state hp:
+// PyTorch's (r, z, n) order with tanh(x) = 2 sigmoid(2x) - 1, in fp32, every
+// product and sum rounded on its own (code/kernel/dels.py:202-211).
+__device__ __forceinline__ float gru_unit(float gir, float giz, float gin, float ghr, float ghz, float ghn, float hp) {
+#pragma clang fp contract(off)
+    const float rg = sigmoid_f32(gir + ghr);
+    const float zg = sigmoid_f32(giz + ghz);
+    const float ng = 2.0f * sigmoid_f32(2.0f * (gin + rg * ghn)) - 1.0f;
+    return (1.0f - zg) * ng + zg * hp;
+}
+
 // Agent-scope atomics used by the "last workgroup finishes" reductions.
 __device__ __forceinline__ unsigned long long atomic_load_u64(unsigned long long* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

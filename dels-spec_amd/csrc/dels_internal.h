@@ -158,9 +158,25 @@ hipError_t launch_domino_argmax(const DominoArgs& a, void* ws, hipStream_t s);
 bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed);
 // The fp8 decode step (A e4m3 K32, B e4m3 K128): as above with r in {128, 256, 512}.
 bool decode8_eligible(int64_t M, int64_t d, int64_t r);
-// fp8 when ra.a_scale and aa.b_scale are set (decode8_eligible), bf16 otherwise.
+// A rollout step with the local head's GRU fused into the decode launch:
+// h = GRU(gi_table[tokens], h_prev) is computed in the launch (and written to
+// h_out), then the draft step runs on it (ra.h is not read).
+struct DecodeGru {
+    const uint16_t* gi_table; int64_t ld_gi, table_rows;   // [rows, 3G] bf16
+    const int64_t* tokens; int64_t tok_stride;
+    const uint16_t* w_hh;        // [3G, G] in MFMA-16 blocks
+    const uint16_t* b_hh;        // [3G] or NULL
+    const uint16_t* h_prev;      // [M, G], row stride G
+    uint16_t* h_out;             // [M, G], row stride G
+};
+// decode_eligible (bf16, packed), G a multiple of 32 up to 2048, and room in the
+// grid for G/16 GRU workgroups next to the rank workgroups.
+bool decode_gru_eligible(int64_t M, int64_t G, int64_t r);
+// fp8 when ra.a_scale and aa.b_scale are set (decode8_eligible), bf16 otherwise;
+// with `gru` (bf16 only, decode_gru_eligible) a fused rollout step.
 // The tagged words go to [kDecodeOff, kDataOff) of `ws`.
-hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, hipStream_t s);
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& aa, void* ws, hipStream_t s,
+                                 const DecodeGru* gru = nullptr);
 // Polls of the rank-ready count before a workgroup computes the rank itself
 // (test hook; returns the previous value).
 int set_decode_spin_limit(int limit);

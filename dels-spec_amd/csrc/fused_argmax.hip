@@ -345,15 +345,26 @@ bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_pack
     return kDecodeWGs % decode_plan(d, r).nct == 0;
 }
 
+bool decode_gru_eligible(int64_t M, int64_t G, int64_t r) {
+    if (!decode_eligible(M, G, r, true, true) || G > kGruMaxG || G % 32 != 0) return false;
+    const DecodePlan p = decode_plan(G, r);
+    // GRU workgroups after the rank workgroups; the new state's words after the
+    // partial words (at most 128 rank workgroups)
+    return p.nct * p.nz + G / kGruUnits <= kDecodeWGs && p.nct * p.nz <= 128;
+}
+
 bool decode8_eligible(int64_t M, int64_t d, int64_t r) {
     return (r == 128 || r == 256 || r == 512) && decode_eligible(M, d, r, true, true);
 }
 
+static_assert(128 * 256 + 16 * (kGruMaxG / 2) <= kDecodeWGs * 256,
+              "the fused GRU's state words fit after the partial words of 128 rank workgroups");
 static_assert(kDecodeWordBytes >= align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)) +
                                      (size_t)16 * (kDecodeMaxRank / 2) * sizeof(unsigned long long),
               "the reserved decode region holds every workgroup's partial words and the rank words");
 
-hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, hipStream_t s) {
+hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* ws, hipStream_t s,
+                                 const DecodeGru* gru) {
     const DecodePlan p = decode_plan(ra.d, ra.r);
     char* w = static_cast<char*>(ws);
     DecodeKArgs k{};
@@ -380,6 +391,14 @@ hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* 
     k.rank_words = reinterpret_cast<unsigned long long*>(
         w + kDecodeOff + align256((size_t)kDecodeWGs * 256 * sizeof(unsigned long long)));
     k.spin_limit = g_decode_spin_limit;
+    if (gru) {
+        if (ra.a_scale != nullptr) return hipErrorInvalidValue;   // the fused GRU runs with bf16 weights only
+        k.gi_table = gru->gi_table; k.ld_gi = gru->ld_gi; k.table_rows = gru->table_rows;
+        k.tokens = gru->tokens; k.tok_stride = gru->tok_stride;
+        k.w_hh = gru->w_hh; k.b_hh = gru->b_hh;
+        k.h_prev = gru->h_prev; k.h_out = gru->h_out;
+        k.h_words = k.partial_words + 128 * 256;   // past the partial words of <= 128 rank workgroups
+    }
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     if (ra.a_scale != nullptr) {
         k.a_scale = ra.a_scale;
@@ -388,9 +407,9 @@ hipError_t launch_lowrank_decode(const RankArgs& ra, const ArgmaxArgs& a, void* 
         if (a.base_dtype == 2) return launch_decode8_f16(k, pk, s);
         return launch_decode8_f32(k, pk, s);
     }
-    if (a.base_dtype == 1) return launch_decode_bf16(k, ka.ksteps, pk, s);
-    if (a.base_dtype == 2) return launch_decode_f16(k, ka.ksteps, pk, s);
-    return launch_decode_f32(k, ka.ksteps, pk, s);
+    if (a.base_dtype == 1) return launch_decode_bf16(k, ka.ksteps, pk, s, gru != nullptr);
+    if (a.base_dtype == 2) return launch_decode_f16(k, ka.ksteps, pk, s, gru != nullptr);
+    return launch_decode_f32(k, ka.ksteps, pk, s, gru != nullptr);
 }
 
 }  // namespace dels

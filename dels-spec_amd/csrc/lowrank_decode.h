@@ -62,6 +62,14 @@ struct DecodeKArgs {
     unsigned long long* rank_words;      // [16][r/2]: tag << 32 | bf16 pair
     unsigned int* gen;                   // launch generation (control area; advanced once per launch)
     int spin_limit;                      // re-reads of untagged words before computing the rank locally
+    // rollout step with the GRU fused in (GRU instantiations only; h above unused)
+    const uint16_t* gi_table; int64_t ld_gi, table_rows;   // [rows, 3G] bf16: E . W_ih^T + b_ih
+    const int64_t* tokens; int64_t tok_stride;             // the previous step's ids
+    const uint16_t* w_hh;                // [3G, G] in MFMA-16 blocks
+    const uint16_t* b_hh;                // [3G] or NULL
+    const uint16_t* h_prev;              // [M, G] bf16, row stride G
+    uint16_t* h_out;                     // [M, G] bf16, row stride G: the new state
+    unsigned long long* h_words;         // [16][G/2]: tag << 32 | two bf16 of the new state
 };
 
 // Tag of the words of the launch that read generation g: an odd multiple of
@@ -76,11 +84,11 @@ __device__ __forceinline__ uint32_t decode_tag(uint32_t g) {
 // this wave taking every 4th block from kb0 + wave (all loads issued first).
 // A8: A holds e4m3 bytes, widened to bf16 at use.
 template <bool A8, int J>
-__device__ __forceinline__ f32x4 decode_rank_partial(const DecodeKArgs& d, int M, int c, int kb0, int kb1,
-                                                     int wave, int lane) {
+__device__ __forceinline__ f32x4 decode_rank_partial(const DecodeKArgs& d, const uint16_t* hsrc, int64_t ldh, int M,
+                                                     int c, int kb0, int kb1, int wave, int lane) {
     const int col = lane & 15, kg = lane >> 4;
     const bool mok = col < M;
-    const uint16_t* hp = d.h + (int64_t)(mok ? col : 0) * d.ldh + kg * 8;
+    const uint16_t* hp = hsrc + (int64_t)(mok ? col : 0) * ldh + kg * 8;
     u32x4 xv[J], wv[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
@@ -143,35 +151,199 @@ __device__ __forceinline__ float decode_tile_at(const float* red, int m, int n) 
 // wave-summed into `red`.  Rounds of 4*J blocks, J the smallest of 2/4/8/16
 // that covers the slice in one round where it can (no loads of masked blocks).
 template <bool A8, int J>
-__device__ __forceinline__ f32x4 decode_slice_acc(const DecodeKArgs& d, int M, int c, int k0, int k1, int wave,
-                                                  int lane) {
+__device__ __forceinline__ f32x4 decode_slice_acc(const DecodeKArgs& d, const uint16_t* hsrc, int64_t ldh, int M,
+                                                  int c, int k0, int k1, int wave, int lane) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     for (int kb0 = k0; kb0 < k1; kb0 += 4 * J)
-        acc += decode_rank_partial<A8, J>(d, M, c, kb0, min(k1, kb0 + 4 * J), wave, lane);
+        acc += decode_rank_partial<A8, J>(d, hsrc, ldh, M, c, kb0, min(k1, kb0 + 4 * J), wave, lane);
     return acc;
 }
+// hsrc/ldh: the rows of h (global memory, or the fused GRU's new state in LDS).
 template <bool A8>
-__device__ __forceinline__ void decode_slice_partial(const DecodeKArgs& d, int M, int c, int z, float* red, int wave,
-                                                     int lane) {
+__device__ __forceinline__ void decode_slice_partial(const DecodeKArgs& d, const uint16_t* hsrc, int64_t ldh, int M,
+                                                     int c, int z, float* red, int wave, int lane) {
     const int k0 = z * d.kpz, k1 = min(d.ksa, k0 + d.kpz);
     f32x4 acc;
-    if (d.kpz <= 8) acc = decode_slice_acc<A8, 2>(d, M, c, k0, k1, wave, lane);
-    else if (d.kpz <= 16) acc = decode_slice_acc<A8, 4>(d, M, c, k0, k1, wave, lane);
-    else if (d.kpz <= 32) acc = decode_slice_acc<A8, 8>(d, M, c, k0, k1, wave, lane);
-    else acc = decode_slice_acc<A8, 16>(d, M, c, k0, k1, wave, lane);
+    if (d.kpz <= 8) acc = decode_slice_acc<A8, 2>(d, hsrc, ldh, M, c, k0, k1, wave, lane);
+    else if (d.kpz <= 16) acc = decode_slice_acc<A8, 4>(d, hsrc, ldh, M, c, k0, k1, wave, lane);
+    else if (d.kpz <= 32) acc = decode_slice_acc<A8, 8>(d, hsrc, ldh, M, c, k0, k1, wave, lane);
+    else acc = decode_slice_acc<A8, 16>(d, hsrc, ldh, M, c, k0, k1, wave, lane);
     decode_wave_sum(red, acc, wave, lane);
 }
 
+// ---- the fused GRU (rollout steps) ---------------------------------------------
+// In GRU mode a launch first advances the local head,
+//     h = GRU(gi_table[tokens], h_prev)    (code/kernel/dels.py:359-373, 202-211),
+// and then runs the draft step on h.  Workgroups nr .. nr + G/16 - 1 (nr =
+// nct * nz: the first workgroups without rank work) each compute 16 units of h
+// -- gh = h_prev . W_hh^T (+ b_hh) for the units' three gate rows, 96 KiB of
+// W_hh at G = 1024 -- write them to h_out for the next step and publish them as
+// words {tag, two bf16} in h_words.  A rank workgroup reads the units of its K
+// slice from those words into LDS; a workgroup whose words do not arrive
+// computes the units it needs itself, with the same partial sums in the same
+// order, so the result does not depend on who computed it.
+constexpr int kGruUnits = 16;      // units of h per GRU workgroup
+constexpr int kGruMaxG = 2048;     // largest hidden size of the fused GRU: LDS holds [16][G] bf16 of h
+
+// Units u0 .. u0+15 of the new state for rows m < M (zero for rows past M)
+// into hblk[16][16] (bf16 bits, row-major).  gh sums each wave's K blocks
+// (wave, wave + 4, ...) in fp32, then the four waves in a fixed order, and is
+// rounded to bf16 after the bias, as F.linear in bf16.  gred: 3 x 4 x 256
+// floats of LDS.  All threads; ends with a barrier.
+__device__ __forceinline__ void gru_block(const DecodeKArgs& d, int M, int G, int u0, float* gred, uint16_t* hblk) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, kg = lane >> 4;
+    const int KB = G / 32;
+    const bool mok = col < M;
+    const uint16_t* hp = d.h_prev + (int64_t)(mok ? col : 0) * G + kg * 8;
+    const uint16_t* wp[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) wp[g] = d.w_hh + (int64_t)((g * G + u0) / 16) * KB * 512 + lane * 8;
+    f32x4 acc[3];
+#pragma unroll
+    for (int g = 0; g < 3; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb0 = wave; kb0 < KB; kb0 += 4 * 8) {
+        u32x4 xv[8], wv[3][8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int kb = kb0 + 4 * j;
+            const int kc = kb < KB ? kb : wave;   // a valid block when masked
+            xv[j] = *reinterpret_cast<const u32x4*>(hp + kc * 32);
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+                wv[g][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[g] + (int64_t)kc * 512));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool ok = kb0 + 4 * j < KB;
+#pragma unroll
+            for (int g = 0; g < 3; ++g)
+                acc[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(masked_bf16x8(xv[j], (ok && mok) ? ~0u : 0u),
+                                                                 masked_bf16x8(wv[g][j], ok ? ~0u : 0u), acc[g], 0,
+                                                                 0, 0);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < 3; ++g) *reinterpret_cast<f32x4*>(&gred[(g * 4 + wave) * 256 + lane * 4]) = acc[g];
+    __syncthreads();
+    // thread t: row m = t / 16, unit n = t % 16 (element m % 4 of lane (m / 4) * 16 + n)
+    const int m = threadIdx.x >> 4, n = threadIdx.x & 15;
+    const int e = (((m >> 2) * 16 + n) << 2) + (m & 3);
+    uint16_t out = 0;
+    if (m < M) {
+        const int j = u0 + n;
+        float gh[3];
+#pragma unroll
+        for (int g = 0; g < 3; ++g) {
+            gh[g] = (gred[(g * 4 + 0) * 256 + e] + gred[(g * 4 + 1) * 256 + e]) +
+                    (gred[(g * 4 + 2) * 256 + e] + gred[(g * 4 + 3) * 256 + e]);
+            if (d.b_hh) gh[g] = gh[g] + bf16_bits_to_f32(d.b_hh[g * G + j]);
+            gh[g] = round_bf16(gh[g]);
+        }
+        int64_t tok = d.tokens[(int64_t)m * d.tok_stride];
+        tok = tok < 0 ? 0 : (tok >= d.table_rows ? d.table_rows - 1 : tok);
+        const uint16_t* gi = d.gi_table + tok * d.ld_gi;
+        const float hv = bf16_bits_to_f32(d.h_prev[(int64_t)m * G + j]);
+        out = f32_to_bf16_bits(gru_unit(bf16_bits_to_f32(gi[j]), bf16_bits_to_f32(gi[G + j]),
+                                        bf16_bits_to_f32(gi[2 * G + j]), gh[0], gh[1], gh[2], hv));
+    }
+    hblk[m * 16 + n] = out;
+    __syncthreads();
+}
+
+// A GRU workgroup's share: its 16 units to h_out and to the tagged words.
+__device__ __forceinline__ void gru_publish(const DecodeKArgs& d, int M, int G, uint32_t tag, float* gred,
+                                            uint16_t* hblk) {
+    const int u0 = ((int)blockIdx.x - d.nct * d.nz) * kGruUnits;
+    gru_block(d, M, G, u0, gred, hblk);
+    if (threadIdx.x < 128) {
+        const int m = threadIdx.x >> 3, p = threadIdx.x & 7;
+        if (m < M) {
+            const uint32_t pair = (uint32_t)hblk[m * 16 + 2 * p] | ((uint32_t)hblk[m * 16 + 2 * p + 1] << 16);
+            *reinterpret_cast<uint32_t*>(d.h_out + (int64_t)m * G + u0 + 2 * p) = pair;
+            __hip_atomic_store(d.h_words + (int64_t)m * (G / 2) + u0 / 2 + p, ((unsigned long long)tag << 32) | pair,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Units [ub, ue) (multiples of 16) of the new state into s_h[16][G] (rows past
+// M are not written): from the tagged words, re-read (bounded) until each
+// carries `tag`; if some never do, every block of the range is computed here.
+// All threads; ends with a barrier.
+__device__ __forceinline__ void gru_fill(const DecodeKArgs& d, int M, int G, int ub, int ue, uint32_t tag,
+                                      uint16_t* s_h, float* gred, uint16_t* hblk) {
+    const int np = (ue - ub) / 2, nw = M * np;
+    bool ok = d.spin_limit > 0;
+    for (int w0 = threadIdx.x; ok && w0 < nw; w0 += 256 * 8) {
+        unsigned long long w[8];
+        uint32_t missing = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = w0 + 256 * i;
+            if (idx < nw) {
+                const int m = idx / np, p = idx - m * np;
+                w[i] = __hip_atomic_load(d.h_words + (int64_t)m * (G / 2) + ub / 2 + p, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+                missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+            }
+        }
+        // re-read the whole group: every load in flight at once
+        for (int it = 0; missing != 0 && it < d.spin_limit; ++it) {
+            __builtin_amdgcn_s_sleep(2);
+            missing = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int idx = w0 + 256 * i;
+                if (idx < nw) {
+                    const int m = idx / np, p = idx - m * np;
+                    w[i] = __hip_atomic_load(d.h_words + (int64_t)m * (G / 2) + ub / 2 + p, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (w0 + 256 * i < nw) missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
+        }
+        ok = missing == 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = w0 + 256 * i;
+            if (ok && idx < nw) {
+                const int m = idx / np, p = idx - m * np;
+                *reinterpret_cast<uint32_t*>(s_h + m * G + ub + 2 * p) = (uint32_t)w[i];
+            }
+        }
+    }
+    if (!__syncthreads_or(!ok)) return;
+    for (int u0 = ub; u0 < ue; u0 += kGruUnits) {   // the words did not come: compute the range here
+        gru_block(d, M, G, u0, gred, hblk);
+        s_h[(threadIdx.x >> 4) * G + u0 + (threadIdx.x & 15)] = hblk[threadIdx.x];
+    }
+    __syncthreads();
+}
+
 // Phase 1 (see the top of the file).  Ends with a barrier; `red` is free after it.
-template <bool A8>
-__device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, int r, float* red, uint32_t tag) {
+// GRU mode: h is the fused GRU's new state, read into s_h (LDS) for this K slice.
+template <bool A8, bool GRU = false>
+__device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, int r, float* red, uint32_t tag,
+                                                  uint16_t* s_h = nullptr, float* gred = nullptr,
+                                                  uint16_t* hblk = nullptr) {
 #pragma clang fp contract(off)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     if ((int)blockIdx.x >= d.nct * d.nz) return;   // no rank work: straight to the argmax stream
     const int c = (int)blockIdx.x % d.nct;
     const int z = (int)blockIdx.x / d.nct;
-    decode_slice_partial<A8>(d, M, c, z, red, wave, lane);
+    if constexpr (GRU) {
+        const int G = d.ksa * 32;
+        gru_fill(d, M, G, z * d.kpz * 32, min(d.ksa, (z + 1) * d.kpz) * 32, tag, s_h, gred, hblk);
+        decode_slice_partial<A8>(d, s_h, G, M, c, z, red, wave, lane);
+    } else {
+        decode_slice_partial<A8>(d, d.h, d.ldh, M, c, z, red, wave, lane);
+    }
     unsigned long long* pw = d.partial_words + (int64_t)c * d.nz * 256 + threadIdx.x;
     if (z > 0) {
         __hip_atomic_store(pw + z * 256, ((unsigned long long)tag << 32) | __float_as_uint(red[threadIdx.x]),
@@ -228,9 +400,10 @@ __device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, i
 // ones whose tag is not `tag`; if any word is still missing the workgroup
 // computes the whole rank itself (the same partials summed in the same order
 // as phase 1).  Ends with a barrier.
-template <int R, bool A8>
+template <int R, bool A8, bool GRU = false>
 __device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M, float* red, uint32_t tag,
-                                                     uint16_t* s_rank) {
+                                                     uint16_t* s_rank, uint16_t* s_h = nullptr,
+                                                     float* gred = nullptr, uint16_t* hblk = nullptr) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
     constexpr int kPer = R / 32;   // words per thread
@@ -270,10 +443,17 @@ __device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M
         for (int i = 0; i < kPer; ++i) dst[threadIdx.x + 256 * i] = (uint32_t)w[i];
     } else {
 #pragma clang fp contract(off)
+        const uint16_t* hsrc = d.h;
+        int64_t ldh = d.ldh;
+        if constexpr (GRU) {   // the whole new state, from the words or computed here
+            gru_fill(d, M, d.ksa * 32, 0, d.ksa * 32, tag, s_h, gred, hblk);
+            hsrc = s_h;
+            ldh = d.ksa * 32;
+        }
         for (int cc = 0; cc < d.nct; ++cc) {
             float v = 0.f;
             for (int z = 0; z < d.nz; ++z) {
-                decode_slice_partial<A8>(d, M, cc, z, red, wave, lane);
+                decode_slice_partial<A8>(d, hsrc, ldh, M, cc, z, red, wave, lane);
                 v = z == 0 ? red[threadIdx.x] : v + red[threadIdx.x];
                 __syncthreads();   // red is rewritten by the next partial
             }
@@ -315,7 +495,8 @@ __device__ __forceinline__ void decode_rows(const ArgmaxKArgs& a, int kg, float 
     }
 }
 
-template <int KSTEPS, typename BaseT, typename PriorT>
+// GRU: a rollout step with the local head's GRU fused in (see gru_block).
+template <int KSTEPS, typename BaseT, typename PriorT, bool GRU>
 __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
 #pragma clang fp contract(off)
     const ArgmaxKArgs& a = d.am;
@@ -325,6 +506,17 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     __shared__ int s_idx[4][16];
     __shared__ int s_last;
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * r];   // the rank, [16][r] bf16
+    struct GruLds {
+        uint16_t h[16 * kGruMaxG];   // the new state [16][G]
+        float gred[3 * 4 * 256];
+        uint16_t hblk[16 * 16];
+    };
+    struct NoGruLds {
+        uint16_t h[1];
+        float gred[1];
+        uint16_t hblk[1];
+    };
+    __shared__ __attribute__((aligned(16))) std::conditional_t<GRU, GruLds, NoGruLds> gl;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar loop control
@@ -332,7 +524,12 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     const int kg = lane >> 4;
 
     const uint32_t tag = decode_tag(__hip_atomic_load(d.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    decode_rank_phase<false>(d, a.M, r, red, tag);
+    if constexpr (GRU) {
+        const int nr = d.nct * d.nz;
+        if ((int)blockIdx.x >= nr && (int)blockIdx.x < nr + d.ksa * 32 / kGruUnits)
+            gru_publish(d, a.M, d.ksa * 32, tag, gl.gred, gl.hblk);
+    }
+    decode_rank_phase<false, GRU>(d, a.M, r, red, tag, gl.h, gl.gred, gl.hblk);
 
     const int nwaves = gridDim.x * 4;
     int t = decode_first_tile(d) * 4 + wave;
@@ -361,7 +558,7 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     for (int u = 0; u < ND; ++u)
         if (u < cnt) load_tile<KSTEPS, B_PACKED_EXACT>(a, t + u * nwaves, lane, brow, prior, tr[u]);
 
-    decode_rank_into_lds<r, false>(d, a.M, red, tag, s_rank);
+    decode_rank_into_lds<r, false, GRU>(d, a.M, red, tag, s_rank, gl.h, gl.gred, gl.hblk);
     bf16x8 ra[KSTEPS];
     {
         const bool mok = col < a.M;
@@ -484,11 +681,14 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
 
 // Dispatch over K steps of B (r / 32) and the prior type for one base dtype.
 template <typename BaseT>
-hipError_t launch_decode_for_base(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s) {
+hipError_t launch_decode_for_base(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru) {
     auto go = [&](auto ks_tag, auto prior_tag) -> hipError_t {
         constexpr int KS = decltype(ks_tag)::value;
         using PT = decltype(prior_tag);
-        hipLaunchKernelGGL((lowrank_decode_kernel<KS, BaseT, PT>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
+        if (gru)
+            hipLaunchKernelGGL((lowrank_decode_kernel<KS, BaseT, PT, true>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
+        else
+            hipLaunchKernelGGL((lowrank_decode_kernel<KS, BaseT, PT, false>), dim3(kDecodeWGs), dim3(256), 0, s, ka);
         return hipGetLastError();
     };
     auto by_prior = [&](auto ks_tag) -> hipError_t {
@@ -531,9 +731,9 @@ hipError_t launch_decode8_for_base(const DecodeKArgs& ka, int prior_kind, hipStr
     }
 }
 
-hipError_t launch_decode_f32(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
-hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
-hipError_t launch_decode_f16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s);
+hipError_t launch_decode_f32(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru);
+hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru);
+hipError_t launch_decode_f16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru);
 hipError_t launch_decode8_f32(const DecodeKArgs& ka, int prior_kind, hipStream_t s);
 hipError_t launch_decode8_bf16(const DecodeKArgs& ka, int prior_kind, hipStream_t s);
 hipError_t launch_decode8_f16(const DecodeKArgs& ka, int prior_kind, hipStream_t s);

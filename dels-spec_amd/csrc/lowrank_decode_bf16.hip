@@ -4,8 +4,8 @@
 
 namespace dels {
 
-hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s) {
-    return launch_decode_for_base<bf16_t>(ka, ksteps, prior_kind, s);
+hipError_t launch_decode_bf16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru) {
+    return launch_decode_for_base<bf16_t>(ka, ksteps, prior_kind, s, gru);
 }
 
 hipError_t launch_decode8_bf16(const DecodeKArgs& ka, int prior_kind, hipStream_t s) {

@@ -4,8 +4,8 @@
 
 namespace dels {
 
-hipError_t launch_decode_f16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s) {
-    return launch_decode_for_base<f16_t>(ka, ksteps, prior_kind, s);
+hipError_t launch_decode_f16(const DecodeKArgs& ka, int ksteps, int prior_kind, hipStream_t s, bool gru) {
+    return launch_decode_for_base<f16_t>(ka, ksteps, prior_kind, s, gru);
 }
 
 hipError_t launch_decode8_f16(const DecodeKArgs& ka, int prior_kind, hipStream_t s) {

@@ -95,11 +95,7 @@ __device__ __forceinline__ void skinny_epilogue(const SkinnyKArgs& a, const floa
             const float giz = bf16_bits_to_f32(gi[G + g]);
             const float gin = bf16_bits_to_f32(gi[2 * G + g]);
             const float hp = a.x ? bf16_bits_to_f32(a.x[(int64_t)b * a.ldx + g]) : 0.0f;
-            const float rg = sigmoid_f32(gir + ghr);
-            const float zg = sigmoid_f32(giz + ghz);
-            const float ng = 2.0f * sigmoid_f32(2.0f * (gin + rg * ghn)) - 1.0f;
-            const float hn = (1.0f - zg) * ng + zg * hp;
-            a.out[(int64_t)b * a.ldout + g] = f32_to_bf16_bits(hn);
+            a.out[(int64_t)b * a.ldout + g] = f32_to_bf16_bits(gru_unit(gir, giz, gin, ghr, ghz, ghn, hp));
         }
     }
 }

@@ -712,6 +712,40 @@ def test_graph_runner_rollout(pkg, dev, nb, steps, V, E, G, r, act, rank_bias, w
     runner.close()
 
 
+def test_rollout_fused_gru_local_fallback_bit_identical(pkg, dev):
+    """At hidden size 1024 the rollout advances the GRU inside the decode launch of steps 1..
+    (GRU workgroups publish the new state as tagged words, the rank workgroups read them).  With
+    the re-read limit forced to zero every workgroup computes the state and the rank itself, as
+    when the grid is not co-resident: the same partial sums in the same order, so the same bits.
+    The rollout itself meets the oracle in test_graph_runner_rollout."""
+    print("case fused GRU rollout, local fallback", flush=True)
+    V, E, G, r, nb, steps = 30011, 64, 1024, 256, 8, 4
+    head = _Head(V, E, G, r, "silu", True, seed=21, std=0.02).to(dev)
+    g = torch.Generator().manual_seed(5)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0)
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V,
+                                 alpha_values=[0.2] * steps, beta_values=[0.1] * steps, baseline_logits=prior,
+                                 device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g).to(dev)
+    base = (torch.randn(nb, steps, V, generator=g) * 3).to(torch.bfloat16).to(dev)
+    out = runner(prefix, base).clone()
+    sc = runner.static_scores.clone()
+    torch.cuda.synchronize()
+    lib = pkg._lib.load()
+    prev = lib.dels_debug_set_decode_spin_limit(0)
+    try:
+        runner.enqueue_eager()
+        torch.cuda.synchronize()
+    finally:
+        lib.dels_debug_set_decode_spin_limit(prev)
+    assert torch.equal(runner.static_out, out) and torch.equal(runner.static_scores, sc)
+    # and the tagged path again on the workspace the fallback used
+    runner.enqueue_eager()
+    torch.cuda.synchronize()
+    assert torch.equal(runner.static_out, out) and torch.equal(runner.static_scores, sc)
+    runner.close()
+
+
 @pytest.mark.parametrize("head_dtype", [torch.float32, torch.float16])
 def test_graph_runner_accepts_fp32_and_fp16_heads(pkg, dev, head_dtype):
     """A float32 or float16 local head runs as the same head converted once to bf16: base
