@@ -339,8 +339,39 @@ __device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, i
     const int z = (int)blockIdx.x / d.nct;
     if constexpr (GRU) {
         const int G = d.ksa * 32;
-        gru_fill(d, M, G, z * d.kpz * 32, min(d.ksa, (z + 1) * d.kpz) * 32, tag, s_h, gred, hblk);
-        decode_slice_partial<A8>(d, s_h, G, M, c, z, red, wave, lane);
+        const int k0 = z * d.kpz, k1 = min(d.ksa, k0 + d.kpz);
+        if (!A8 && d.kpz > 8 && d.kpz <= 16) {
+            // One round of J = 4 blocks per wave, as decode_slice_partial: the
+            // slice of A goes in flight before the wait for the new state.
+            u32x4 wv[4];
+            const uint16_t* ap = static_cast<const uint16_t*>(d.A) + (int64_t)c * d.ksa * 512 + lane * 8;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int kb = k0 + wave + 4 * j;
+                const int kc = kb < k1 ? kb : min(k0, d.ksa - 1);
+                wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
+            }
+            gru_fill(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
+            const int col = lane & 15, kg = lane >> 4;
+            const bool mok = col < M;
+            const uint16_t* hp = s_h + (mok ? col : 0) * G + kg * 8;
+            f32x4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int kb = k0 + wave + 4 * j;
+                const bool ok = kb < k1;
+                const int kc = ok ? kb : min(k0, d.ksa - 1);
+                const u32x4 xv = *reinterpret_cast<const u32x4*>(hp + kc * 32);
+                part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(masked_bf16x8(xv, (ok && mok) ? ~0u : 0u),
+                                                               masked_bf16x8(wv[j], ok ? ~0u : 0u), part, 0, 0, 0);
+            }
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            acc += part;
+            decode_wave_sum(red, acc, wave, lane);
+        } else {
+            gru_fill(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
+            decode_slice_partial<A8>(d, s_h, G, M, c, z, red, wave, lane);
+        }
     } else {
         decode_slice_partial<A8>(d, d.h, d.ldh, M, c, z, red, wave, lane);
     }
