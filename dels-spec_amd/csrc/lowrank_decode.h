@@ -557,8 +557,18 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
     const uint32_t tag = decode_tag(__hip_atomic_load(d.gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     if constexpr (GRU) {
         const int nr = d.nct * d.nz;
-        if ((int)blockIdx.x >= nr && (int)blockIdx.x < nr + d.ksa * 32 / kGruUnits)
+        if ((int)blockIdx.x >= nr && (int)blockIdx.x < nr + d.ksa * 32 / kGruUnits) {
             gru_publish(d, a.M, d.ksa * 32, tag, gl.gred, gl.hblk);
+        } else if ((int)blockIdx.x >= nr) {
+            // The other workgroups start their B prefetch 3 us late (the 100 MHz
+            // real-time clock), so that the GRU's W_hh and the rank's A loads
+            // reach HBM ahead of it: the rank is on every workgroup's critical
+            // path, and the prefetch still lands before it (14-step rollout at
+            // G = 1024: 366 -> 360 us, flat from 2 to 6 us; a decode step
+            // without the GRU is slower with any delay).
+            const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+            while (__builtin_amdgcn_s_memrealtime() - t0 < 300ull) __builtin_amdgcn_s_sleep(8);
+        }
     }
     decode_rank_phase<false, GRU>(d, a.M, r, red, tag, gl.h, gl.gred, gl.hblk);
 
