@@ -273,15 +273,17 @@ __device__ __forceinline__ void gru_publish(const DecodeKArgs& d, int M, int G, 
 // M are not written): from the tagged words, re-read (bounded) until each
 // carries `tag`; if some never do, every block of the range is computed here.
 // All threads; ends with a barrier.
+template <int NW>
 __device__ __forceinline__ void gru_fill(const DecodeKArgs& d, int M, int G, int ub, int ue, uint32_t tag,
                                       uint16_t* s_h, float* gred, uint16_t* hblk) {
+    static_assert(NW <= 32, "one bit per word in a 32-bit mask");
     const int np = (ue - ub) / 2, nw = M * np;
     bool ok = d.spin_limit > 0;
-    for (int w0 = threadIdx.x; ok && w0 < nw; w0 += 256 * 8) {
-        unsigned long long w[8];
+    for (int w0 = threadIdx.x; ok && w0 < nw; w0 += 256 * NW) {
+        unsigned long long w[NW];
         uint32_t missing = 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NW; ++i) {
             const int idx = w0 + 256 * i;
             if (idx < nw) {
                 const int m = idx / np, p = idx - m * np;
@@ -295,7 +297,7 @@ __device__ __forceinline__ void gru_fill(const DecodeKArgs& d, int M, int G, int
             __builtin_amdgcn_s_sleep(2);
             missing = 0;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
+            for (int i = 0; i < NW; ++i) {
                 const int idx = w0 + 256 * i;
                 if (idx < nw) {
                     const int m = idx / np, p = idx - m * np;
@@ -304,12 +306,12 @@ __device__ __forceinline__ void gru_fill(const DecodeKArgs& d, int M, int G, int
                 }
             }
 #pragma unroll
-            for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < NW; ++i)
                 if (w0 + 256 * i < nw) missing |= (uint32_t)((uint32_t)(w[i] >> 32) != tag) << i;
         }
         ok = missing == 0;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NW; ++i) {
             const int idx = w0 + 256 * i;
             if (ok && idx < nw) {
                 const int m = idx / np, p = idx - m * np;
@@ -323,6 +325,43 @@ __device__ __forceinline__ void gru_fill(const DecodeKArgs& d, int M, int G, int
         s_h[(threadIdx.x >> 4) * G + u0 + (threadIdx.x & 15)] = hblk[threadIdx.x];
     }
     __syncthreads();
+}
+
+// A rank workgroup's partial in GRU mode when its slice is one round of J
+// blocks per wave (decode_slice_partial with that J, the same sums): the slice
+// of A goes in flight before the wait for the new state's words (NW in flight
+// per thread; 4 or 16 measured slower, as were longer sleeps between
+// re-reads).  Ends with a barrier.
+template <int J, int NW>
+__device__ __forceinline__ void gru_rank_partial(const DecodeKArgs& d, int M, int c, int k0, int k1, uint32_t tag,
+                                                 uint16_t* s_h, float* gred, uint16_t* hblk, float* red, int wave,
+                                                 int lane) {
+    const int G = d.ksa * 32;
+    u32x4 wv[J];
+    const uint16_t* ap = static_cast<const uint16_t*>(d.A) + (int64_t)c * d.ksa * 512 + lane * 8;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int kb = k0 + wave + 4 * j;
+        const int kc = kb < k1 ? kb : min(k0, d.ksa - 1);
+        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
+    }
+    gru_fill<NW>(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
+    const int col = lane & 15, kg = lane >> 4;
+    const bool mok = col < M;
+    const uint16_t* hp = s_h + (mok ? col : 0) * G + kg * 8;
+    f32x4 part = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int kb = k0 + wave + 4 * j;
+        const bool ok = kb < k1;
+        const int kc = ok ? kb : min(k0, d.ksa - 1);
+        const u32x4 xv = *reinterpret_cast<const u32x4*>(hp + kc * 32);
+        part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(masked_bf16x8(xv, (ok && mok) ? ~0u : 0u),
+                                                       masked_bf16x8(wv[j], ok ? ~0u : 0u), part, 0, 0, 0);
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc += part;
+    decode_wave_sum(red, acc, wave, lane);
 }
 
 // Phase 1 (see the top of the file).  Ends with a barrier; `red` is free after it.
@@ -340,36 +379,10 @@ __device__ __forceinline__ void decode_rank_phase(const DecodeKArgs& d, int M, i
     if constexpr (GRU) {
         const int G = d.ksa * 32;
         const int k0 = z * d.kpz, k1 = min(d.ksa, k0 + d.kpz);
-        if (!A8 && d.kpz > 8 && d.kpz <= 16) {
-            // One round of J = 4 blocks per wave, as decode_slice_partial: the
-            // slice of A goes in flight before the wait for the new state.
-            u32x4 wv[4];
-            const uint16_t* ap = static_cast<const uint16_t*>(d.A) + (int64_t)c * d.ksa * 512 + lane * 8;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int kb = k0 + wave + 4 * j;
-                const int kc = kb < k1 ? kb : min(k0, d.ksa - 1);
-                wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
-            }
-            gru_fill(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
-            const int col = lane & 15, kg = lane >> 4;
-            const bool mok = col < M;
-            const uint16_t* hp = s_h + (mok ? col : 0) * G + kg * 8;
-            f32x4 part = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int kb = k0 + wave + 4 * j;
-                const bool ok = kb < k1;
-                const int kc = ok ? kb : min(k0, d.ksa - 1);
-                const u32x4 xv = *reinterpret_cast<const u32x4*>(hp + kc * 32);
-                part = __builtin_amdgcn_mfma_f32_16x16x32_bf16(masked_bf16x8(xv, (ok && mok) ? ~0u : 0u),
-                                                               masked_bf16x8(wv[j], ok ? ~0u : 0u), part, 0, 0, 0);
-            }
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            acc += part;
-            decode_wave_sum(red, acc, wave, lane);
+        if (!A8 && d.kpz > 8 && d.kpz <= 16) {   // every fused-GRU plan up to G = 2048
+            gru_rank_partial<4, 8>(d, M, c, k0, k1, tag, s_h, gred, hblk, red, wave, lane);
         } else {
-            gru_fill(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
+            gru_fill<8>(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
             decode_slice_partial<A8>(d, s_h, G, M, c, z, red, wave, lane);
         }
     } else {
@@ -477,7 +490,7 @@ __device__ __forceinline__ void decode_rank_into_lds(const DecodeKArgs& d, int M
         const uint16_t* hsrc = d.h;
         int64_t ldh = d.ldh;
         if constexpr (GRU) {   // the whole new state, from the words or computed here
-            gru_fill(d, M, d.ksa * 32, 0, d.ksa * 32, tag, s_h, gred, hblk);
+            gru_fill<8>(d, M, d.ksa * 32, 0, d.ksa * 32, tag, s_h, gred, hblk);
             hsrc = s_h;
             ldh = d.ksa * 32;
         }
