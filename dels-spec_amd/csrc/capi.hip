@@ -958,6 +958,13 @@ int dels_lowrank_argmax_fp8(const void* h, int64_t ldh, const void* Aq, const fl
         e = launch_lowrank_decode(ra, a, ws, s);
         return e == hipSuccess ? DELS_OK : hip_fail(e, "fp8 fused decode step launch");
     }
+    if (fp8_argmax_tiled(a) && rank_proj_quantizes(L.plan, r)) {
+        // the rank epilogue also writes the rank quantised per row where the
+        // e4m3 tiled argmax reads it: no quantisation launch
+        ra.rank_q = reinterpret_cast<uint8_t*>(w + L.argmax_off);
+        ra.rank_qscale = reinterpret_cast<float*>(w + L.argmax_off + align256((size_t)M * r));
+        a.rank_quantized = true;
+    }
     e = launch_rank_proj(ra, L.plan, ws, L.part_off, s);
     if (e != hipSuccess) return hip_fail(e, "fp8 rank projection launch");
     e = launch_fused_argmax_fp8(a, ws, L.argmax_off, s);

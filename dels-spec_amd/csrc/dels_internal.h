@@ -68,7 +68,14 @@ struct RankArgs {
     const uint16_t* bias; int act;
     int M, d, r;
     uint16_t* rank; int64_t ldrank;
+    // non-null (rank_proj_quantizes): the rank is also written quantised per row
+    // to e4m3 ([M][r] bytes) with its per-row scale [M], as the e4m3 tiled argmax takes it
+    uint8_t* rank_q = nullptr;
+    float* rank_qscale = nullptr;
 };
+// Whether launch_rank_proj with plan p can also write the rank quantised per
+// row to e4m3 (the LDS-tiled GEMM with split K, r = 256 or 512).
+bool rank_proj_quantizes(const SkinnyPlan& p, int64_t r);
 // `ws` is the workspace base (control area); partials go to ws + data_off.
 hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, size_t data_off, hipStream_t s);
 
@@ -92,6 +99,9 @@ struct ArgmaxArgs {
     int64_t rank_rows_stride = 0, rank_rows_count = 0;
     const uint16_t* B; int64_t ldb; bool b_packed;
     const float* b_scale = nullptr;   // non-null: B is e4m3 in K128 blocks, this its per-row scale [V]
+    // e4m3 tiled argmax only: the rank quantised per row is already at the
+    // argmax's data offset (rank_proj_quantizes), no quantisation launch
+    bool rank_quantized = false;
     const void* base; int64_t ldbase; int base_dtype;
     const void* prior; int prior_dtype;
     const float* alpha; int64_t alpha_stride;
@@ -119,6 +129,9 @@ hipError_t launch_sample_rows(const void* x, int64_t ldx, int dtype, int M, int 
 // fp8 argmax (b_scale set): r in {128, 256, 512}, any M up to kMaxKeyRows.
 bool argmax_fp8_supported(int64_t M, int64_t r);
 size_t argmax_fp8_data_bytes(int64_t M, int64_t r, int64_t V);
+// Whether launch_fused_argmax_fp8 runs the e4m3 tiled kernel for `a` (which
+// reads the rank quantised per row from the start of its data region).
+bool fp8_argmax_tiled(const ArgmaxArgs& a);
 hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s);
 
 // ---- target LM head of a draft block: base = bf16(hidden . W^T), argmax rows fused ----

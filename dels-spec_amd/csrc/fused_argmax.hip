@@ -252,6 +252,8 @@ static bool tiled8_eligible(const ArgmaxArgs& a) {
     return tiled_eligible(t);
 }
 
+bool fp8_argmax_tiled(const ArgmaxArgs& a) { return tiled8_eligible(a); }
+
 hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_off, hipStream_t s) {
     const int pk = a.prior == nullptr ? 0 : (a.prior_dtype == 1 ? 2 : (a.prior_dtype == 2 ? 3 : 1));
     char* w = static_cast<char*>(ws);
@@ -276,8 +278,9 @@ hipError_t launch_fused_argmax_fp8(const ArgmaxArgs& a, void* ws, size_t data_of
         // the rank, quantised per row to e4m3
         uint8_t* rank_q = reinterpret_cast<uint8_t*>(w + data_off);
         float* rank_scale = reinterpret_cast<float*>(reinterpret_cast<char*>(rank_q) + align256((size_t)a.M * a.r));
-        hipLaunchKernelGGL(quantize_rank_e4m3_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, a.rank, a.ldrank, a.M,
-                           a.r, rank_q, rank_scale);
+        if (!a.rank_quantized)
+            hipLaunchKernelGGL(quantize_rank_e4m3_kernel, dim3((a.M + 3) / 4), dim3(256), 0, s, a.rank, a.ldrank,
+                               a.M, a.r, rank_q, rank_scale);
         ka.rank_q = rank_q;
         ka.ldrank = a.r;
         ka.rank_scale = rank_scale;

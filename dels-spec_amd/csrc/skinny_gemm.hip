@@ -37,6 +37,7 @@ struct SkinnyKArgs {
     const float* col_scale;             // e4m3 W only: per-column scale, applied before the bias
     const uint16_t* bias; int act;
     uint16_t* out; int64_t ldout;
+    uint8_t* out_q; float* out_qscale;  // split-K rank epilogue: also e4m3 per row (rank_proj_quantizes)
     // GRU epilogue
     const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
     const int64_t* tokens; int64_t tok_stride;
@@ -511,11 +512,18 @@ __global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
 
 // Sum of the split-K partials of the LDS-tiled rank projection, in split
 // order, and the rank epilogue; one thread per 4 output columns (16-byte loads).
+// Q: the rank is also quantised per row to e4m3 with the rule of the e4m3
+// argmax's own quantisation (amax = max |rank[m, :]| of the bf16 values,
+// q = e4m3(rank * (448 / amax)), scale = amax / 448; 1 for an all-zero row):
+// r = 256 or 512, so a workgroup holds whole rows (one or two waves each).
+template <bool Q>
 __global__ __launch_bounds__(256) void rank_splitk_epilogue_kernel(SkinnyKArgs a) {
 #pragma clang fp contract(off)
     const int64_t quads = (int64_t)a.M * a.ncols / 4;
-    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (t >= quads) return;
+    int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (!Q && t >= quads) return;
+    const bool valid = t < quads;
+    if (!valid) t = quads - 1;   // Q: every thread reaches the barrier; its row is not written
     const int m = (int)(t / (a.ncols / 4)), n = (int)(t % (a.ncols / 4)) * 4;
     const int64_t off = (int64_t)m * a.ncols + n;
     const int64_t zs = (int64_t)a.M * a.ncols;
@@ -533,6 +541,7 @@ __global__ __launch_bounds__(256) void rank_splitk_epilogue_kernel(SkinnyKArgs a
         }
     }
     uint32_t packed[2] = {0u, 0u};
+    float xs[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
         float x = v[q];
@@ -540,16 +549,42 @@ __global__ __launch_bounds__(256) void rank_splitk_epilogue_kernel(SkinnyKArgs a
         if (a.bias) x = x + bf16_bits_to_f32(a.bias[n + q]);
         x = round_bf16(x);
         if (a.act == 1) x = round_bf16(silu_f32(x));
+        xs[q] = x;   // the bf16 value itself
         packed[q >> 1] |= (uint32_t)f32_to_bf16_bits(x) << (16 * (q & 1));
     }
     uint16_t* dst = a.out + (int64_t)m * a.ldout + n;
-    if ((((uintptr_t)a.out & 7) | (uintptr_t)(a.ldout & 3)) == 0) {
-        *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
-    } else {   // an output view without 8-byte rows: element stores
-        dst[0] = (uint16_t)packed[0]; dst[1] = (uint16_t)(packed[0] >> 16);
-        dst[2] = (uint16_t)packed[1]; dst[3] = (uint16_t)(packed[1] >> 16);
+    if (valid) {
+        if ((((uintptr_t)a.out & 7) | (uintptr_t)(a.ldout & 3)) == 0) {
+            *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
+        } else {   // an output view without 8-byte rows: element stores
+            dst[0] = (uint16_t)packed[0]; dst[1] = (uint16_t)(packed[0] >> 16);
+            dst[2] = (uint16_t)packed[1]; dst[3] = (uint16_t)(packed[1] >> 16);
+        }
+    }
+    if constexpr (Q) {
+        // row maximum of |rank|: the wave's 64 lanes, then the row's two waves at r = 512
+        __shared__ float s_amax[4];
+        float amax = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) amax = __builtin_fmaxf(amax, __builtin_fabsf(xs[q]));
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, off, 64));
+        const int wave = threadIdx.x >> 6;
+        if ((threadIdx.x & 63) == 0) s_amax[wave] = amax;
+        __syncthreads();
+        if (a.ncols == 512) amax = __builtin_fmaxf(s_amax[wave], s_amax[wave ^ 1]);
+        const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
+        uint32_t qw = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qw |= f32_to_e4m3(xs[q] * inv) << (8 * q);
+        if (valid) {
+            *reinterpret_cast<uint32_t*>(a.out_q + (int64_t)m * a.ncols + n) = qw;
+            if (n == 0) a.out_qscale[m] = amax > 0.f ? amax / kE4M3Max : 1.f;
+        }
     }
 }
+
+bool rank_proj_quantizes(const SkinnyPlan& p, int64_t r) { return p.tiled && p.ksplit > 1 && (r == 256 || r == 512); }
 
 // ---------------------------------------------------------------------------
 // Host side
@@ -649,7 +684,15 @@ hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, si
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || p.ksplit == 1) return e;
         const int64_t quads = (int64_t)ka.M * ka.ncols / 4;
-        hipLaunchKernelGGL(rank_splitk_epilogue_kernel, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, s, ka);
+        const dim3 egrid((unsigned)((quads + 255) / 256));
+        if (a.rank_q != nullptr) {
+            if (!rank_proj_quantizes(p, a.r)) return hipErrorInvalidValue;
+            ka.out_q = a.rank_q;
+            ka.out_qscale = a.rank_qscale;
+            hipLaunchKernelGGL(rank_splitk_epilogue_kernel<true>, egrid, dim3(256), 0, s, ka);
+        } else {
+            hipLaunchKernelGGL(rank_splitk_epilogue_kernel<false>, egrid, dim3(256), 0, s, ka);
+        }
         return hipGetLastError();
     }
     if (p.wm == 1) return launch_skinny<1, 1, EPI_RANK>(ka, p, wmode, s);

@@ -165,6 +165,10 @@ FP8_STEP_CASES = [
     (96, 1000, 128, "silu", True, torch.bfloat16, torch.bfloat16, 20011),    # LDS-tiled rank GEMM, e4m3 A
     # the batched-verification shape: e4m3 rank GEMM, row quantisation, fp8 MFMA-tiled argmax
     (512, 4096, 512, "identity", False, torch.bfloat16, torch.bfloat16, 151936),
+    # the rank quantised per row inside the split-K rank epilogue, ragged last workgroup
+    # of rows (r = 256: four rows per workgroup; r = 512: two)
+    (130, 2048, 256, "silu", True, torch.bfloat16, torch.float32, 30000),
+    (257, 1024, 512, "identity", False, torch.float16, None, 30000),
 ]
 
 
