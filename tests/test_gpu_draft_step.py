@@ -25,7 +25,10 @@ def f(t):
 
 
 @pytest.mark.parametrize("M,V,dtype,stride_pad", [(8, 151936, torch.bfloat16, 0), (5, 4099, torch.float32, 7),
-                                                  (33, 20011, torch.float16, 0), (1, 1, torch.float32, 0)])
+                                                  (33, 20011, torch.float16, 0), (1, 1, torch.float32, 0),
+                                                  # 16-byte pieces: strided rows, and chunks of several rounds
+                                                  (6, 30000, torch.float32, 4), (7, 65536, torch.float16, 8),
+                                                  (5, 300000, torch.float32, 0)])
 def test_argmax_rows(pkg, dev, M, V, dtype, stride_pad):
     """Ids as torch.argmax on the CPU (code/dflash.py:31-33): lowest index of the
     maximum, the first NaN of a row wins, an all -inf row gives 0."""
