@@ -100,3 +100,58 @@ def test_lowrank_argmax_fp8_sweep(pkg, dev, seed):
     ids2, score2 = pkg.lowrank_argmax_fp8(*args, **kw)
     torch.cuda.synchronize()
     assert torch.equal(ids2, ids) and torch.equal(score2, score)
+
+
+@pytest.mark.parametrize("seed", list(range(16)) + [-1])
+def test_graph_runner_rollout_sweep(pkg, dev, seed):
+    """Seeded rollouts over batch, steps, hidden size (below, at and above the
+    hidden size where the GRU runs inside the decode launch, up to its limit
+    2048), rank, activation, rank bias and prior, teacher-forced against the
+    oracle as test_graph_runner_rollout, and replayed bit for bit.  Seed -1:
+    the largest fused-GRU grid (16 rows, G = 2048, r = 512: 128 rank and 128
+    GRU workgroups)."""
+    from test_gpu_parity import _Head
+
+    rng = np.random.default_rng(900 + seed)
+    nb = int(rng.choice([1, 2, 5, 8, 13, 16]))
+    steps = int(rng.choice([1, 2, 3, 5, 9]))
+    V = int(rng.integers(1000, 30000))
+    E = int(rng.choice([16, 32, 64]))
+    G = int(rng.choice([64, 256, 1024, 1536, 2048]))
+    r = int(rng.choice([64, 128, 256, 512]))
+    act = "silu" if rng.random() < 0.5 else "identity"
+    rank_bias = bool(rng.random() < 0.5)
+    with_prior = bool(rng.random() < 0.6)
+    if seed == -1:
+        nb, steps, V, E, G, r, act, rank_bias, with_prior = 16, 4, 20011, 32, 2048, 512, "silu", True, True
+    std = 0.02 if G >= 1024 else 0.1
+    print(f"case rollout sweep seed={seed} nb={nb} steps={steps} V={V} E={E} G={G} r={r} {act} "
+          f"bias={rank_bias} prior={with_prior}", flush=True)
+    head = _Head(V, E, G, r, act, rank_bias, seed=3000 + seed, std=std).to(dev)
+    g = torch.Generator().manual_seed(4000 + seed)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0) if with_prior else None
+    alphas = [float(a) for a in rng.uniform(0.05, 0.6, steps)]
+    betas = [float(b) for b in rng.uniform(0.0, 0.5, steps)] if with_prior else [0.0] * steps
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V, alpha_values=alphas,
+                                 beta_values=betas, baseline_logits=prior, device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    base = (torch.randn(nb, steps, V, generator=g) * 3).to(torch.bfloat16)
+    out = runner(prefix.to(dev), base.to(dev)).clone()
+    scores = runner.static_scores.clone()
+    torch.cuda.synchronize()
+    out2 = runner(prefix.to(dev), base.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(out2, out)
+    dev_ids = out.cpu().numpy()
+    rid, rsc, rsec = oracle.rollout(
+        prefix.numpy().reshape(-1), f(base), embed=f(head.embed_tokens.weight), W_ih=f(head.prefix_gru.weight_ih_l0),
+        W_hh=f(head.prefix_gru.weight_hh_l0), b_hh=None,
+        A=f(head.rank_proj.weight), rank_bias=f(head.rank_proj.bias) if rank_bias else None, act=act,
+        B=f(head.low_rank_lm_head.weight), prior=f(prior.to(torch.bfloat16)) if with_prior else None,
+        alphas=alphas, betas=betas, forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(scores).reshape(-1), rid.reshape(-1), rsc.reshape(-1),
+                              rsec.reshape(-1))
+    # the device's bf16 GRU state may differ from the oracle's by an ulp: allow score drift of 2e-2
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["max_score_err"] < 2e-2, res
+    runner.close()
