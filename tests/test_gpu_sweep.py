@@ -155,3 +155,68 @@ def test_graph_runner_rollout_sweep(pkg, dev, seed):
     assert res["id_mismatch_pinned"] == 0, res
     assert res["max_score_err"] < 2e-2, res
     runner.close()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_gather_argmax_sweep(pkg, dev, seed):
+    """The Markov path's gathered-rank argmax over seeded shapes (GEMV and
+    MFMA-tiled regimes, either layout, every base/prior dtype)."""
+    rng = np.random.default_rng(1200 + seed)
+    M = int(rng.choice([1, 4, 16, 33, 64, 100]))
+    r = int(rng.choice([32, 64, 128, 256, 512]))
+    V = int(rng.integers(500, 40000))
+    if rng.random() < 0.5:
+        V -= V % 32
+    packed = bool(rng.random() < 0.6)
+    bdt = _DTYPES[int(rng.integers(0, 3))]
+    pdt = _DTYPES[int(rng.integers(0, 3))]
+    rows = int(rng.integers(50, 3000))
+    print(f"case gather sweep seed={seed} M={M} r={r} V={V} packed={packed} base={bdt} prior={pdt} rows={rows}",
+          flush=True)
+    g = torch.Generator().manual_seed(5000 + seed)
+    E = torch.randn(rows, r, generator=g).to(torch.bfloat16)
+    W = (torch.randn(V, r, generator=g) * 0.05).to(torch.bfloat16)
+    base = (torch.randn(M, V, generator=g) * 3).to(bdt)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0).to(pdt)
+    alpha = torch.rand(M, generator=g) * 0.6
+    beta = torch.rand(M, generator=g) * 0.6
+    tok = torch.randint(-3, rows + 3, (M,), generator=g)      # out-of-table ids clamp to the ends
+    Wd = W.to(dev)
+    args = (tok.to(dev), E.to(dev), pkg.pack_operand(Wd) if packed else Wd, base.to(dev), prior.to(dev),
+            alpha.to(dev), beta.to(dev))
+    ids, score = pkg.gather_argmax(*args)
+    torch.cuda.synchronize()
+    ids, score = ids.clone(), score.clone()
+    rank = f(E)[np.clip(tok.numpy(), 0, rows - 1)]
+    assert_parity(ids, score, rank, f(W), f(base), f(prior), f(alpha), f(beta))
+    ids2, score2 = pkg.gather_argmax(*args)
+    torch.cuda.synchronize()
+    assert torch.equal(ids2, ids) and torch.equal(score2, score)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_domino_argmax_sweep(pkg, dev, seed):
+    """The Domino correction step over seeded shapes and dtypes against the oracle."""
+    from oracle import domino as DO
+
+    rng = np.random.default_rng(1300 + seed)
+    M = int(rng.choice([1, 3, 8, 16, 29]))
+    E = int(32 * rng.integers(1, 65))
+    V = int(rng.integers(100, 40000))
+    bias_dt = [None, torch.bfloat16, torch.float32][int(rng.integers(0, 3))]
+    base_dt = _DTYPES[int(rng.integers(0, 3))]
+    alpha = float(rng.uniform(0.1, 1.5))
+    print(f"case domino sweep seed={seed} M={M} E={E} V={V} bias={bias_dt} base={base_dt} alpha={alpha:.3f}",
+          flush=True)
+    g = torch.Generator().manual_seed(6000 + seed)
+    z = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    s = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    fc2 = (torch.randn(V, E, generator=g) * 0.02).to(torch.bfloat16)
+    base = (torch.randn(M, V, generator=g) * 3).to(base_dt)
+    bias = torch.randn(V, generator=g).to(bias_dt) if bias_dt is not None else None
+    ids, score = pkg.domino_argmax(z.to(dev), s.to(dev), pkg.pack_operand(fc2.to(dev)), base.to(dev), alpha,
+                                   bias.to(dev) if bias is not None else None)
+    torch.cuda.synchronize()
+    rid, rbest, rsec = DO.domino_step(f(z), f(s), f(fc2), None if bias is None else f(bias), f(base), alpha)
+    res = oracle.check_parity(ids.cpu().numpy(), score.cpu().numpy(), rid, rbest, rsec, score_atol=1e-4)
+    assert res["id_mismatch_pinned"] == 0 and res["score_bad"] == 0, res
