@@ -211,9 +211,11 @@ __device__ __forceinline__ void gru_block(const DecodeKArgs& d, int M, int G, in
             const int kb = kb0 + 4 * j;
             const int kc = kb < KB ? kb : wave;   // a valid block when masked
             xv[j] = *reinterpret_cast<const u32x4*>(hp + kc * 32);
+            // plain (cached) loads: every step of a rollout reads the same
+            // W_hh (6 MB at G = 1024), unlike the streamed B (14-step rollout
+            // 358 -> 347 us against non-temporal loads)
 #pragma unroll
-            for (int g = 0; g < 3; ++g)
-                wv[g][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp[g] + (int64_t)kc * 512));
+            for (int g = 0; g < 3; ++g) wv[g][j] = *reinterpret_cast<const u32x4*>(wp[g] + (int64_t)kc * 512);
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -343,7 +345,7 @@ __device__ __forceinline__ void gru_rank_partial(const DecodeKArgs& d, int M, in
     for (int j = 0; j < J; ++j) {
         const int kb = k0 + wave + 4 * j;
         const int kc = kb < k1 ? kb : min(k0, d.ksa - 1);
-        wv[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512));
+        wv[j] = *reinterpret_cast<const u32x4*>(ap + (int64_t)kc * 512);   // cached: every step reads this A
     }
     gru_fill<NW>(d, M, G, k0 * 32, k1 * 32, tag, s_h, gred, hblk);
     const int col = lane & 15, kg = lane >> 4;
