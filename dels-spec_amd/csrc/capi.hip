@@ -251,23 +251,26 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     g.batch = B;
     g.G = G;
 
-    // h0 = GRU(gi_table[prefix], 0)   (code/kernel/dels.py:426-433)
-    g.tokens = p->prefix_ids;
-    g.tok_stride = 1;
-    g.h_in = nullptr;
-    g.ldh_in = G;
-    g.h_out = static_cast<uint16_t*>(p->h_a);
-    g.ldh_out = G;
-    hipError_t e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
-    if (e != hipSuccess) return hip_fail(e, "GRU step launch");
-
     uint16_t* h_cur = static_cast<uint16_t*>(p->h_a);
     uint16_t* h_next = static_cast<uint16_t*>(p->h_b);
     const size_t esz = dtype_size(p->base_dtype);
     const bool packed = p->weights_layout == DELS_LAYOUT_MFMA16;
     const bool use_decode = G >= kRolloutDecodeMinG && decode_eligible(B, G, r, packed, packed);
-    // steps 1.. advance the GRU inside the decode launch (no GRU launch between steps)
+    // every step advances the GRU inside its decode launch, the first one from
+    // the zero state on the prefix ids: no GRU launch at all
     const bool fuse_gru = use_decode && decode_gru_eligible(B, G, r);
+    hipError_t e = hipSuccess;
+    if (!fuse_gru) {
+        // h0 = GRU(gi_table[prefix], 0)   (code/kernel/dels.py:426-433)
+        g.tokens = p->prefix_ids;
+        g.tok_stride = 1;
+        g.h_in = nullptr;
+        g.ldh_in = G;
+        g.h_out = h_cur;
+        g.ldh_out = G;
+        e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);
+        if (e != hipSuccess) return hip_fail(e, "GRU step launch");
+    }
     for (int step = 0; step < p->steps; ++step) {
         RankArgs ra{};
         ra.h = h_cur; ra.ldh = G;
@@ -292,17 +295,24 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
         aa.ld_out = p->steps;
 
-        if (fuse_gru && step > 0) {
-            // h = GRU(gi_table[previous ids], h), rank projection and argmax in one launch
+        if (fuse_gru) {
+            // h = GRU(gi_table[previous ids], h) -- step 0: GRU(gi_table[prefix], 0)
+            // (code/kernel/dels.py:426-433) --, rank projection and argmax in one launch
             DecodeGru dg{};
             dg.gi_table = g.gi_table; dg.ld_gi = g.ld_gi; dg.table_rows = g.table_rows;
-            dg.tokens = p->out_ids + (step - 1); dg.tok_stride = p->steps;
             dg.w_hh = g.w_hh; dg.b_hh = g.b_hh;
-            dg.h_prev = h_cur; dg.h_out = h_next;
-            ra.h = h_next;
+            if (step == 0) {
+                dg.tokens = p->prefix_ids; dg.tok_stride = 1;
+                dg.h_prev = nullptr; dg.h_out = h_cur;
+                ra.h = h_cur;
+            } else {
+                dg.tokens = p->out_ids + (step - 1); dg.tok_stride = p->steps;
+                dg.h_prev = h_cur; dg.h_out = h_next;
+                ra.h = h_next;
+            }
             e = launch_lowrank_decode(ra, aa, ws, s, &dg);
             if (e != hipSuccess) return hip_fail(e, "fused rollout step launch");
-            std::swap(h_cur, h_next);
+            if (step > 0) std::swap(h_cur, h_next);
         } else if (use_decode) {
             // rank projection and argmax in one launch
             e = launch_lowrank_decode(ra, aa, ws, s);

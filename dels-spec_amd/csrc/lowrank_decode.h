@@ -67,7 +67,7 @@ struct DecodeKArgs {
     const int64_t* tokens; int64_t tok_stride;             // the previous step's ids
     const uint16_t* w_hh;                // [3G, G] in MFMA-16 blocks
     const uint16_t* b_hh;                // [3G] or NULL
-    const uint16_t* h_prev;              // [M, G] bf16, row stride G
+    const uint16_t* h_prev;              // [M, G] bf16, row stride G; NULL: a zero state
     uint16_t* h_out;                     // [M, G] bf16, row stride G: the new state
     unsigned long long* h_words;         // [16][G/2]: tag << 32 | two bf16 of the new state
 };
@@ -196,15 +196,16 @@ __device__ __forceinline__ void gru_block(const DecodeKArgs& d, int M, int G, in
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, kg = lane >> 4;
     const int KB = G / 32;
+    const int KBl = d.h_prev ? KB : 0;   // a zero previous state (a first step): gh = b_hh
     const bool mok = col < M;
-    const uint16_t* hp = d.h_prev + (int64_t)(mok ? col : 0) * G + kg * 8;
+    const uint16_t* hp = d.h_prev ? d.h_prev + (int64_t)(mok ? col : 0) * G + kg * 8 : nullptr;
     const uint16_t* wp[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) wp[g] = d.w_hh + (int64_t)((g * G + u0) / 16) * KB * 512 + lane * 8;
     f32x4 acc[3];
 #pragma unroll
     for (int g = 0; g < 3; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int kb0 = wave; kb0 < KB; kb0 += 4 * 8) {
+    for (int kb0 = wave; kb0 < KBl; kb0 += 4 * 8) {
         u32x4 xv[8], wv[3][8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -247,7 +248,7 @@ __device__ __forceinline__ void gru_block(const DecodeKArgs& d, int M, int G, in
         int64_t tok = d.tokens[(int64_t)m * d.tok_stride];
         tok = tok < 0 ? 0 : (tok >= d.table_rows ? d.table_rows - 1 : tok);
         const uint16_t* gi = d.gi_table + tok * d.ld_gi;
-        const float hv = bf16_bits_to_f32(d.h_prev[(int64_t)m * G + j]);
+        const float hv = d.h_prev ? bf16_bits_to_f32(d.h_prev[(int64_t)m * G + j]) : 0.f;
         out = f32_to_bf16_bits(gru_unit(bf16_bits_to_f32(gi[j]), bf16_bits_to_f32(gi[G + j]),
                                         bf16_bits_to_f32(gi[2 * G + j]), gh[0], gh[1], gh[2], hv));
     }
