@@ -348,7 +348,8 @@ def bench_fp8(pkg, name, args, dev, torch):
     tiled = M >= 64
     return {"workload": name, "M": M, "d": d, "r": r, "V": V, "weights": "e4m3 (A K32, B K128 blocks)",
             "kernel": "lowrank_decode8_kernel" if M <= 16 else
-            ("rank_gemm_tiled_kernel (e4m3 A) + quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel"
+            ("rank_gemm_tiled_kernel (e4m3 A) + rank_splitk_epilogue_kernel (quantising)"
+             " + fused_argmax_tiled8_kernel"
              if tiled else "skinny_gemm_kernel (e4m3 A) + fused_argmax_gemv8_kernel"),
             "rows_per_s": M / (us * 1e-6), "us_per_step": us, "algorithmic_bytes": nbytes,
             "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
