@@ -1,6 +1,8 @@
 // Device-side helpers shared by the gfx950 kernels of the DeLS draft path.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -41,6 +43,29 @@ __device__ __forceinline__ float load_f32(const f16_t* p) {
     _Float16 h;
     __builtin_memcpy(&h, &b, 2);
     return (float)h;
+}
+
+// The same loads kept as loaded (fp32 bits, or a 16-bit value zero-extended by
+// the load itself) and widened by widen_raw<T> where the value is used: a
+// conversion right after a load in a streaming loop makes the compiler wait for
+// that load, and for every load issued before it.
+__device__ __forceinline__ uint32_t load_raw(const float* p) {
+    return __float_as_uint(__builtin_nontemporal_load(p));
+}
+__device__ __forceinline__ uint32_t load_raw(const bf16_t* p) { return __builtin_nontemporal_load(&p->bits); }
+__device__ __forceinline__ uint32_t load_raw(const f16_t* p) { return __builtin_nontemporal_load(&p->bits); }
+template <typename T>
+__device__ __forceinline__ float widen_raw(uint32_t w) {
+    if constexpr (std::is_same<T, float>::value) {
+        return __uint_as_float(w);
+    } else if constexpr (std::is_same<T, bf16_t>::value) {
+        return __uint_as_float(w << 16);
+    } else {
+        const uint16_t b = (uint16_t)w;
+        _Float16 h;
+        __builtin_memcpy(&h, &b, 2);
+        return (float)h;
+    }
 }
 
 // 16-byte operand loads: eight bf16 values.

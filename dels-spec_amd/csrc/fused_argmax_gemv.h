@@ -63,12 +63,13 @@ enum : int {
 };
 
 // Operands of one 16-row vocabulary tile held by a lane: the B MFMA operand for
-// every K step, and the four base logits and the prior of its column.
+// every K step, and the four base logits and the prior of its column as loaded
+// (load_raw; widened at use with widen_raw).
 template <int KSTEPS>
 struct TileRegs {
     bf16x8 b[KSTEPS];
-    float base[4];
-    float prior;
+    uint32_t base[4];
+    uint32_t prior;
 };
 
 template <int KSTEPS, int MODE, typename BaseT, typename PriorT>
@@ -100,9 +101,9 @@ __device__ __forceinline__ void load_tile(const ArgmaxKArgs& a, int t, int lane,
         }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) tr.base[q] = load_f32(brow[q] + vc);
-    if constexpr (!is_no_prior<PriorT>::value) tr.prior = load_f32(prior + vc);
-    else tr.prior = 0.f;
+    for (int q = 0; q < 4; ++q) tr.base[q] = load_raw(brow[q] + vc);
+    if constexpr (!is_no_prior<PriorT>::value) tr.prior = load_raw(prior + vc);
+    else tr.prior = 0u;
 }
 
 // End of a workgroup's share of the argmax over rows m0 .. m0+15: reduce the
@@ -245,8 +246,8 @@ __global__ __launch_bounds__(256) void fused_argmax_gemv_kernel(ArgmaxKArgs a) {
         const int v = tile * 16 + col;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            float sc = __builtin_fmaf(acc[q], al[q], tr.base[q]);
-            if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
+            float sc = __builtin_fmaf(acc[q], al[q], widen_raw<BaseT>(tr.base[q]));
+            if (use_prior[q]) sc = __builtin_fmaf(-be[q], widen_raw<PriorT>(tr.prior), sc);
             const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];

@@ -634,8 +634,8 @@ __global__ __launch_bounds__(256) void lowrank_decode_kernel(DecodeKArgs d) {
         const int v = tile * 16 + col;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            float sc = __builtin_fmaf(acc[q], al[q], tr.base[q]);
-            if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
+            float sc = __builtin_fmaf(acc[q], al[q], widen_raw<BaseT>(tr.base[q]));
+            if (use_prior[q]) sc = __builtin_fmaf(-be[q], widen_raw<PriorT>(tr.prior), sc);
             const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
             best[q] = take ? sc : best[q];
             bidx[q] = take ? v : bidx[q];
