@@ -55,6 +55,8 @@ def parse_args():
                     help="add the whole draft block (target LM head + first argmax + DeLS rollout, one graph)")
     ap.add_argument("--also-fp8", action=argparse.BooleanOptionalAction, default=True,
                     help="add the fp8 variant (e4m3 A and B with per-channel scales) of the workload's shape")
+    ap.add_argument("--also-domino", action=argparse.BooleanOptionalAction, default=True,
+                    help="add one Domino correction step (code/kernel/domino.py:58-173) at the draft block's batch")
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--cpu-configs", action="store_true",
@@ -290,6 +292,29 @@ def bench_workload(pkg, name, args, dev, torch):
     rec["argmax_hbm_frac"] = rec["argmax_GBs"] / HBM_PEAK_GBS
     return rec, x0
 
+
+
+def bench_domino(pkg, args, dev, torch):
+    """One Domino correction step, argmax_v alpha * (SiLU(z + s) . fc2[v]) + base[v] (code/kernel/domino.py:
+    58-173), for the draft block's 8 rows at E = 1024, V = 151936, bf16 base, no fc2 bias: fc2 (311 MB, more
+    than the 256 MB last-level cache) streamed once per step."""
+    M, E, V = 8, 1024, 151936
+    g = torch.Generator(device=dev).manual_seed(5)
+    z = torch.randn(M, E, generator=g, device=dev).to(torch.bfloat16)
+    s = torch.randn(M, E, generator=g, device=dev).to(torch.bfloat16)
+    fc2 = pkg.pack_operand((torch.randn(V, E, generator=g, device=dev) * 0.02).to(torch.bfloat16))
+    base = (torch.randn(M, V, generator=g, device=dev) * 3).to(torch.bfloat16)
+    ids = torch.empty(M, dtype=torch.int64, device=dev)
+    score = torch.empty(M, dtype=torch.float32, device=dev)
+    steps = max(20, min(args.steps, 200))
+    ms, graph = time_graph(torch, lambda i: pkg.domino_argmax(z, s, fc2, base, 0.7, out_ids=ids, out_score=score),
+                           steps, dev)
+    del graph
+    us = ms * 1e3 / steps
+    nbytes = 2 * V * E + 2 * M * V + 4 * M * E + 12 * M
+    return {"workload": f"domino step: {M} rows, E {E}, V {V}, bf16 base, no bias", "kernel": "domino_argmax_kernel",
+            "us_per_step": us, "rows_per_s": M / (us * 1e-6), "algorithmic_bytes": nbytes,
+            "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
 
 
 def bench_fp8(pkg, name, args, dev, torch):
@@ -630,6 +655,11 @@ def main():
             out["draft_step"] = bench_draft_step(pkg, args, dev, torch)
         except Exception as e:  # informative record only
             out["draft_step"] = {"error": repr(e)}
+    if args.also_domino and args.workload != "qwen3_8b_m512":
+        try:
+            out["domino"] = bench_domino(pkg, args, dev, torch)
+        except Exception as e:  # informative record only
+            out["domino"] = {"error": repr(e)}
     if args.also_fp8 and args.workload != "qwen3_8b_m512":
         try:
             out["fp8"] = bench_fp8(pkg, args.workload, args, dev, torch)

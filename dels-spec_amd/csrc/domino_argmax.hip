@@ -38,8 +38,8 @@ constexpr int kDomKC = 16;   // K steps (of 32) per register set
 template <typename BaseT, typename BiasT>
 struct DomRegs {
     bf16x8 b[kDomKC];
-    float base[4];
-    float bias;
+    uint32_t base[4];   // as loaded (load_raw), widened at use
+    uint32_t bias;
 };
 
 template <typename BaseT, typename BiasT>
@@ -115,9 +115,9 @@ __global__ __launch_bounds__(256) void domino_argmax_kernel(DominoArgs a, Argmax
                                     ok ? 0xffffffffu : 0u);
         }
 #pragma unroll
-        for (int q = 0; q < 4; ++q) tr.base[q] = load_f32(brow[q] + vc);
-        if constexpr (!is_no_prior<BiasT>::value) tr.bias = load_f32(bias + vc);
-        else tr.bias = 0.f;
+        for (int q = 0; q < 4; ++q) tr.base[q] = load_raw(brow[q] + vc);
+        if constexpr (!is_no_prior<BiasT>::value) tr.bias = load_raw(bias + vc);
+        else tr.bias = 0u;
     };
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
     auto consume = [&](const DomRegs<BaseT, BiasT>& tr, int u) {
@@ -136,8 +136,8 @@ __global__ __launch_bounds__(256) void domino_argmax_kernel(DominoArgs a, Argmax
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float dot = acc[q];
-                if constexpr (!is_no_prior<BiasT>::value) dot = dot + tr.bias;
-                const float sc = __builtin_fmaf(dot, al[q], tr.base[q]);
+                if constexpr (!is_no_prior<BiasT>::value) dot = dot + widen_raw<BiasT>(tr.bias);
+                const float sc = __builtin_fmaf(dot, al[q], widen_raw<BaseT>(tr.base[q]));
                 const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);
                 best[q] = take ? sc : best[q];
                 bidx[q] = take ? v : bidx[q];
