@@ -21,8 +21,8 @@ namespace dels {
 template <int KS8>
 struct TileRegs8 {
     i32x8 b[KS8];
-    float base[4];
-    float prior;
+    uint32_t base[4];   // base logits and prior as loaded (load_raw), widened at use
+    uint32_t prior;
     float bscale;
 };
 
@@ -39,15 +39,15 @@ __device__ __forceinline__ void load_tile8(const ArgmaxKArgs& a, int t, int lane
         tr.b[j] = i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q) tr.base[q] = load_f32(brow[q] + vc);
-    if constexpr (!is_no_prior<PriorT>::value) tr.prior = load_f32(prior + vc);
-    else tr.prior = 0.f;
+    for (int q = 0; q < 4; ++q) tr.base[q] = load_raw(brow[q] + vc);
+    if constexpr (!is_no_prior<PriorT>::value) tr.prior = load_raw(prior + vc);
+    else tr.prior = 0u;
     tr.bscale = __builtin_nontemporal_load(a.b_scale + vc);
 }
 
 // Contract one tile against the e4m3 rank operand and fold its 16 columns into
 // the lane's running argmax of rows 4*(lane/16) + q.
-template <int KS8>
+template <int KS8, typename BaseT, typename PriorT>
 __device__ __forceinline__ void consume_tile8(const ArgmaxKArgs& a, const i32x8 (&rq)[KS8], const float (&rsc)[4],
                                               const TileRegs8<KS8>& tr, int tile, int col, const float (&al)[4],
                                               const float (&be)[4], const bool (&use_prior)[4], float (&best)[4],
@@ -61,8 +61,8 @@ __device__ __forceinline__ void consume_tile8(const ArgmaxKArgs& a, const i32x8 
     for (int q = 0; q < 4; ++q) {
         float dot = acc[q] * rsc[q];
         dot = dot * tr.bscale;
-        float sc = __builtin_fmaf(dot, al[q], tr.base[q]);
-        if (use_prior[q]) sc = __builtin_fmaf(-be[q], tr.prior, sc);
+        float sc = __builtin_fmaf(dot, al[q], widen_raw<BaseT>(tr.base[q]));
+        if (use_prior[q]) sc = __builtin_fmaf(-be[q], widen_raw<PriorT>(tr.prior), sc);
         const bool take = (v < a.V) & argmax_better(sc, v, best[q], bidx[q]);   // no short circuit: branch-free
         best[q] = take ? sc : best[q];
         bidx[q] = take ? v : bidx[q];
@@ -85,21 +85,21 @@ __device__ __forceinline__ void stream_tiles8(const ArgmaxKArgs& a, const i32x8 
         if (t + nwaves < ntiles) load_tile8<KS8>(a, t + nwaves, lane, brow, prior, tb);
     }
     if (t + nwaves >= ntiles) {
-        consume_tile8<KS8>(a, rq, rsc, ta, t, col, al, be, use_prior, best, bidx);
+        consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, ta, t, col, al, be, use_prior, best, bidx);
         return;
     }
     while (true) {
-        consume_tile8<KS8>(a, rq, rsc, ta, t, col, al, be, use_prior, best, bidx);
+        consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, ta, t, col, al, be, use_prior, best, bidx);
         if (t + 2 * nwaves >= ntiles) {
-            consume_tile8<KS8>(a, rq, rsc, tb, t + nwaves, col, al, be, use_prior, best, bidx);
+            consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, tb, t + nwaves, col, al, be, use_prior, best, bidx);
             break;
         }
         load_tile8<KS8>(a, t + 2 * nwaves, lane, brow, prior, ta);
         __builtin_amdgcn_sched_barrier(0);   // the refill is issued before the other tile is touched
         t += nwaves;
-        consume_tile8<KS8>(a, rq, rsc, tb, t, col, al, be, use_prior, best, bidx);
+        consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, tb, t, col, al, be, use_prior, best, bidx);
         if (t + 2 * nwaves >= ntiles) {
-            consume_tile8<KS8>(a, rq, rsc, ta, t + nwaves, col, al, be, use_prior, best, bidx);
+            consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, ta, t + nwaves, col, al, be, use_prior, best, bidx);
             break;
         }
         load_tile8<KS8>(a, t + 2 * nwaves, lane, brow, prior, tb);

@@ -719,19 +719,19 @@ __global__ __launch_bounds__(256) void lowrank_decode8_kernel(DecodeKArgs d) {
     for (; k + 2 * ND8 <= cnt; k += ND8) {
 #pragma unroll
         for (int u = 0; u < ND8; ++u) {
-            consume_tile8<KS8>(a, rq, rsc, tr[u], t + (k + u) * nwaves, col, al, be, use_prior, best, bidx);
+            consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, tr[u], t + (k + u) * nwaves, col, al, be, use_prior, best, bidx);
             load_tile8<KS8>(a, t + (k + u + ND8) * nwaves, lane, brow, prior, tr[u]);
         }
     }
 #pragma unroll
     for (int u = 0; u < ND8; ++u) {
-        if (k + u < cnt) consume_tile8<KS8>(a, rq, rsc, tr[u], t + (k + u) * nwaves, col, al, be, use_prior, best, bidx);
+        if (k + u < cnt) consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, tr[u], t + (k + u) * nwaves, col, al, be, use_prior, best, bidx);
         if (k + u + ND8 < cnt) load_tile8<KS8>(a, t + (k + u + ND8) * nwaves, lane, brow, prior, tr[u]);
     }
 #pragma unroll
     for (int u = 0; u < ND8; ++u)
         if (k + u + ND8 < cnt)
-            consume_tile8<KS8>(a, rq, rsc, tr[u], t + (k + u + ND8) * nwaves, col, al, be, use_prior, best, bidx);
+            consume_tile8<KS8, BaseT, PriorT>(a, rq, rsc, tr[u], t + (k + u + ND8) * nwaves, col, al, be, use_prior, best, bidx);
     argmax_wg_finish(a, best, bidx, 0, s_val, s_idx, s_last, nullptr);
     if (s_last == 1 && threadIdx.x == 0) __hip_atomic_fetch_add(d.gen, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
