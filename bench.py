@@ -186,8 +186,16 @@ def set_bytes(x):
     return sum(t.numel() * t.element_size() for t in (x.h, x.A, x.B, x.base, x.prior))
 
 
-def time_graph(torch, record, steps, dev, reps=3):
-    """Capture `record(i)` for i < steps in one graph; best of `reps` timed replays (ms)."""
+def replay_stats(ms_list):
+    """Median, p10, p90 and min of per-replay times (ms)."""
+    xs = sorted(ms_list)
+    q = lambda p: xs[min(len(xs) - 1, max(0, round(p * (len(xs) - 1))))]  # noqa: E731
+    return {"median": q(0.5), "p10": q(0.1), "p90": q(0.9), "min": xs[0], "replays": len(xs)}
+
+
+def time_graph(torch, record, steps, dev, reps=11):
+    """Capture `record(i)` for i < steps in one graph; the median of `reps` timed replays (ms),
+    with the spread of the replays (``replay_stats``) as a second value."""
     stream = torch.cuda.Stream(device=dev)
     stream.wait_stream(torch.cuda.current_stream(dev))
     graph = torch.cuda.CUDAGraph()
@@ -201,7 +209,7 @@ def time_graph(torch, record, steps, dev, reps=3):
     torch.cuda.synchronize(dev)
     graph.replay()                       # warm replay
     torch.cuda.synchronize(dev)
-    best = None
+    times = []
     cur = torch.cuda.current_stream(dev)
     for _ in range(reps):
         e0 = torch.cuda.Event(enable_timing=True)
@@ -211,9 +219,14 @@ def time_graph(torch, record, steps, dev, reps=3):
         graph.replay()
         e1.record(cur)
         torch.cuda.synchronize(dev)
-        ms = e0.elapsed_time(e1)
-        best = ms if best is None else min(best, ms)
-    return best, graph
+        times.append(e0.elapsed_time(e1))
+    st = replay_stats(times)
+    return st["median"], graph, st
+
+
+def per_step_us(st, steps):
+    """``replay_stats`` of graph replays of ``steps`` launches, as µs per launch."""
+    return {k: (v * 1e3 / steps if k != "replays" else v) for k, v in st.items()}
 
 
 def bench_workload(pkg, name, args, dev, torch):
@@ -257,12 +270,12 @@ def bench_workload(pkg, name, args, dev, torch):
         pkg.rank_proj(sets[i].h, weights[i][0], None, sets[i].act, out=ranks[i])
     torch.cuda.synchronize(dev)
 
-    ms_total, g_step = time_graph(torch, step, args.steps, dev)
+    ms_total, g_step, st_step = time_graph(torch, step, args.steps, dev)
     # the graph replays must reproduce the eager results
     for i in range(nsets):
         if not (torch.equal(outs[i][0], eager[i][0]) and torch.equal(outs[i][1], eager[i][1])):
             raise RuntimeError(f"graph replay differs from eager results on set {i}")
-    ms_kernel_total, g_arg = time_graph(torch, argmax_only, args.steps, dev)
+    ms_kernel_total, g_arg, st_arg = time_graph(torch, argmax_only, args.steps, dev)
     del g_step, g_arg
 
     ms_step = ms_total / args.steps
@@ -284,6 +297,8 @@ def bench_workload(pkg, name, args, dev, torch):
         "sets": nsets,
         "set_MB": per / 2**20,
         "ids_set0": ids_set0,
+        "us_per_step_spread": per_step_us(st_step, args.steps),
+        "us_fused_argmax_spread": per_step_us(st_arg, args.steps),
     }
     rec["hbm_frac_step"] = rec["step_GBs"] / HBM_PEAK_GBS
     rec["mfma_frac_step"] = rec["step_TFLOPs"] / BF16_MFMA_PEAK_TFLOPS
@@ -307,14 +322,67 @@ def bench_domino(pkg, args, dev, torch):
     ids = torch.empty(M, dtype=torch.int64, device=dev)
     score = torch.empty(M, dtype=torch.float32, device=dev)
     steps = max(20, min(args.steps, 200))
-    ms, graph = time_graph(torch, lambda i: pkg.domino_argmax(z, s, fc2, base, 0.7, out_ids=ids, out_score=score),
-                           steps, dev)
+    ms, graph, st = time_graph(torch, lambda i: pkg.domino_argmax(z, s, fc2, base, 0.7, out_ids=ids,
+                                                                  out_score=score), steps, dev)
     del graph
     us = ms * 1e3 / steps
     nbytes = 2 * V * E + 2 * M * V + 4 * M * E + 12 * M
     return {"workload": f"domino step: {M} rows, E {E}, V {V}, bf16 base, no bias", "kernel": "domino_argmax_kernel",
             "us_per_step": us, "rows_per_s": M / (us * 1e-6), "algorithmic_bytes": nbytes,
-            "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS}
+            "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "us_per_step_spread": per_step_us(st, steps)}
+
+
+def fp8_id_agreement(pkg, x, w8, torch):
+    """The fp8 step's ids against the bf16 path's on one input set, under the top-2 margin rule.
+
+    Reference ids: the bf16 kernels on the unquantised weights (the GPU tests pin
+    them to the oracle).  A row is "pinned" when the bf16 top-2 margin exceeds
+    twice the row's bound on the fp8 error,
+    ``max_v |alpha| (|eR|.(|B| + |eB|) + |rank|.|eB|)[v]`` (+1e-4 for fp32
+    rounding), where ``eB`` is B's e4m3 rounding and ``eR`` the difference
+    between the rank the fp8 MFMAs contract (the e4m3 A's rank, quantised per row
+    as the kernels do) and the bf16 rank; all of it evaluated in fp64 on the
+    device.  On pinned rows the ids must agree; elsewhere either pick is within
+    rounding.
+    """
+    f64, f32 = torch.float64, torch.float32
+    A8, B8 = w8
+    ids8, _ = pkg.lowrank_argmax_fp8(x.h, A8, B8, x.base, x.prior, x.alpha, x.beta, act=x.act)
+    ids_b, _ = pkg.lowrank_argmax(x.h, pkg.pack_operand(x.A), pkg.pack_operand(x.B), x.base, x.prior, x.alpha,
+                                  x.beta, act=x.act)
+    rank_b = pkg.rank_proj(x.h, x.A, None, x.act).to(f64)
+    qA, sA = pkg.quantize_e4m3_rows(x.A)
+    qB, sB = pkg.quantize_e4m3_rows(x.B)
+    Ad = qA.view(torch.float8_e4m3fn).to(f64) * sA.to(f64)[:, None]
+    Bd = qB.view(torch.float8_e4m3fn).to(f64) * sB.to(f64)[:, None]
+    rank8 = (x.h.to(f64) @ Ad.t()).to(f32).to(torch.bfloat16)
+    if x.act == "silu":
+        rank8 = torch.nn.functional.silu(rank8.float()).to(torch.bfloat16)
+    r8 = rank8.float()
+    amax = r8.abs().amax(dim=1)
+    nz = amax > 0
+    inv = torch.where(nz, 448.0 / torch.where(nz, amax, torch.ones_like(amax)), torch.ones_like(amax))
+    scl = torch.where(nz, amax / 448.0, torch.ones_like(amax))
+    used = (r8 * inv[:, None]).to(torch.float8_e4m3fn).to(f64) * scl.to(f64)[:, None]
+    Bf = x.B.to(f64)
+    eB = (Bd - Bf).abs()
+    eR = (used - rank_b).abs()
+    alpha, beta = x.alpha.to(f64), x.beta.to(f64)
+    E = alpha.abs()[:, None] * (eR @ (Bf.abs() + eB).t() + rank_b.abs() @ eB.t())
+    Emax = E.amax(dim=1) + 1e-4
+    del E
+    sc = (rank_b @ Bf.t()) * alpha[:, None] + x.base.to(f64)
+    sc = torch.where((beta != 0)[:, None], sc - beta[:, None] * x.prior.to(f64)[None, :], sc)
+    top2 = torch.topk(sc, 2, dim=1).values
+    del sc
+    pinned = (top2[:, 0] - top2[:, 1]) > 2 * Emax
+    match = ids8 == ids_b
+    npin = int(pinned.sum())
+    return {"rows": int(match.numel()), "match": float(match.float().mean()), "pinned_rows": npin,
+            "pinned_match": float(match[pinned].float().mean()) if npin else None,
+            "median_bound": float(Emax.median()),
+            "reference": "bf16 kernels on the unquantised weights (seeded input set)"}
 
 
 def bench_fp8(pkg, name, args, dev, torch):
@@ -329,6 +397,7 @@ def bench_fp8(pkg, name, args, dev, torch):
     M, d, r, V = s["M"], s["d"], s["r"], s["V"]
     weights = [(pkg.quantize_pack_fp8(x.A, "k32"), pkg.quantize_pack_fp8(x.B, "k128")) for x in sets]
     ranks = [pkg.rank_proj(x.h, x.A, None, x.act) for x in sets]   # for the argmax-only timing
+    agreement = fp8_id_agreement(pkg, sets[0], weights[0], torch)   # set 0: the seeded inputs
     for x in sets:   # the bf16 weights are not read by the fp8 step
         x.A = x.B = None
     torch.cuda.empty_cache()
@@ -347,7 +416,7 @@ def bench_fp8(pkg, name, args, dev, torch):
     torch.cuda.synchronize(dev)
     eager = [(o[0].clone(), o[1].clone()) for o in outs]
     steps = min(args.steps, 200)
-    ms_total, g = time_graph(torch, step, steps, dev)
+    ms_total, g, st_step = time_graph(torch, step, steps, dev)
     del g
     for i in range(nsets):
         if not (torch.equal(outs[i][0], eager[i][0]) and torch.equal(outs[i][1], eager[i][1])):
@@ -362,7 +431,7 @@ def bench_fp8(pkg, name, args, dev, torch):
 
     argmax_only(0)
     torch.cuda.synchronize(dev)
-    ms_arg, g = time_graph(torch, argmax_only, steps, dev)
+    ms_arg, g, st_arg = time_graph(torch, argmax_only, steps, dev)
     del g
     us_arg = ms_arg * 1e3 / steps
     sb = x0.base.element_size()
@@ -380,9 +449,12 @@ def bench_fp8(pkg, name, args, dev, torch):
             "GBs": nbytes / (us * 1e-6) / 1e9, "hbm_frac": nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
             "mfma_frac": flops / (us * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS,
             "sets": nsets,
+            "us_per_step_spread": per_step_us(st_step, steps),
+            "id_match_vs_bf16": agreement,
             "fused_argmax_only": {"kernel": "quantize_rank_e4m3_kernel + fused_argmax_tiled8_kernel"
                                             if tiled else "fused_argmax_gemv8_kernel",
-                                  "us_per_launch": us_arg, "algorithmic_bytes": arg_bytes,
+                                  "us_per_launch": us_arg, "us_per_launch_spread": per_step_us(st_arg, steps),
+                                  "algorithmic_bytes": arg_bytes,
                                   "hbm_frac": arg_bytes / (us_arg * 1e-6) / 1e9 / HBM_PEAK_GBS,
                                   "mfma_frac": arg_flops / (us_arg * 1e-6) / 1e12 / FP8_MFMA_PEAK_TFLOPS}}
 
@@ -413,8 +485,9 @@ def bench_draft_step(pkg, args, dev, torch):
     cur = torch.cuda.current_stream(dev)
 
     def timed(fn):
-        best = None
-        for _ in range(3):
+        """Median over 7 timed runs of ``n`` calls, µs per call."""
+        times = []
+        for _ in range(7):
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize(dev)
@@ -423,9 +496,8 @@ def bench_draft_step(pkg, args, dev, torch):
                 fn(i)
             e1.record(cur)
             torch.cuda.synchronize(dev)
-            ms = e0.elapsed_time(e1) / n
-            best = ms if best is None else min(best, ms)
-        return best * 1e3
+            times.append(e0.elapsed_time(e1) / n)
+        return replay_stats(times)["median"] * 1e3
 
     def block(i):
         step.static_hidden.copy_(hiddens[i % 3])
@@ -631,11 +703,15 @@ def main():
             "algorithmic_bytes": roof_bytes,
             "us_per_launch": roof_us,
         },
-        "step": {k: rec[k] for k in ("us_per_step", "step_bytes", "step_GBs", "hbm_frac_step", "step_TFLOPs",
-                                     "mfma_frac_step")},
+        "timing": "median of 11 replays of one graph of K launches (HIP events on the launch stream); "
+                  "spreads give p10/p90/min over the replays",
+        "step": {k: rec[k] for k in ("us_per_step", "us_per_step_spread", "step_bytes", "step_GBs",
+                                     "hbm_frac_step", "step_TFLOPs", "mfma_frac_step")},
         "fused_argmax_only": {"kernel": " + ".join(ROWMAJOR_M16_KERNELS if args.workload != "qwen3_8b_m512"
                                                    else ROOFLINE_KERNELS[args.workload]),
-                              "us_per_launch": rec["us_fused_argmax"], "algorithmic_bytes": rec["argmax_bytes"],
+                              "us_per_launch": rec["us_fused_argmax"],
+                              "us_per_launch_spread": rec["us_fused_argmax_spread"],
+                              "algorithmic_bytes": rec["argmax_bytes"],
                               "GBs": rec["argmax_GBs"], "hbm_frac": rec["argmax_hbm_frac"]},
     }
     if args.also_m512 and args.workload != "qwen3_8b_m512":
@@ -643,7 +719,8 @@ def main():
             r512, _ = bench_workload(pkg, "qwen3_8b_m512", argparse.Namespace(**{**vars(args), "sets": 0,
                                                                                    "steps": min(args.steps, 100)}),
                                      dev, torch)
-            out["m512"] = {k: r512[k] for k in ("rows_per_s", "us_per_step", "us_fused_argmax", "argmax_GBs",
+            out["m512"] = {k: r512[k] for k in ("rows_per_s", "us_per_step", "us_per_step_spread",
+                                                "us_fused_argmax", "us_fused_argmax_spread", "argmax_GBs",
                                                 "argmax_hbm_frac", "argmax_TFLOPs", "argmax_mfma_frac",
                                                 "step_GBs", "hbm_frac_step", "step_TFLOPs", "mfma_frac_step")}
             out["m512"]["argmax_traffic"] = traffic_all.get("qwen3_8b_m512", {}).get("hbm_bytes_per_launch")

@@ -24,6 +24,7 @@
 // GEMV kernel's (argmax_wg_finish).
 #include <algorithm>
 #include <climits>
+#include <mutex>
 
 #include "dels_device.h"
 #include "dels_internal.h"
@@ -168,14 +169,16 @@ __global__ __launch_bounds__(256) void domino_argmax_kernel(DominoArgs a, Argmax
 
 template <typename BaseT, typename BiasT>
 hipError_t launch_domino_inst(const DominoArgs& a, const ArgmaxKArgs& fin, int gx, int gy, size_t lds, hipStream_t s) {
-    // the operands of E = 2048 take 128 KiB of dynamic LDS: allow it once per kernel
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&domino_argmax_kernel<BaseT, BiasT>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)domino_lds_bytes(kDominoMaxE));
-        if (e != hipSuccess) return e;
-        attr_set = true;
-    }
+    // the operands of E = 2048 take 128 KiB of dynamic LDS: allow it once per kernel instance (the
+    // attribute belongs to the function, not to a device); call_once makes concurrent first launches
+    // from several host threads safe, and every caller sees the call's result
+    static std::once_flag once;
+    static hipError_t attr_err = hipSuccess;
+    std::call_once(once, [] {
+        attr_err = hipFuncSetAttribute(reinterpret_cast<const void*>(&domino_argmax_kernel<BaseT, BiasT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)domino_lds_bytes(kDominoMaxE));
+    });
+    if (attr_err != hipSuccess) return attr_err;
     hipLaunchKernelGGL((domino_argmax_kernel<BaseT, BiasT>), dim3(gx, gy, 1), dim3(256), lds, s, a, fin);
     return hipGetLastError();
 }

@@ -9,3 +9,4 @@ baseline), never as a fallback for the HIP path.
 from .dels_oracle import *  # noqa: F401,F403
 from . import sampling  # noqa: F401
 from . import domino  # noqa: F401
+from . import bounds  # noqa: F401

@@ -37,8 +37,8 @@ def _rank(h: torch.Tensor, A: torch.Tensor, act: str) -> torch.Tensor:
     return rank
 
 
-def eager_step_bf16(h, A, B, base, prior: Optional[torch.Tensor], alpha, beta, act: str = "identity"):
-    """int64 [M] ids of one draft step on the reference's eager bf16 path.
+def eager_logits_bf16(h, A, B, base, prior: Optional[torch.Tensor], alpha, beta, act: str = "identity"):
+    """bf16 [M, V] final logits of one draft step on the reference's eager bf16 path.
 
     ``h`` [M, d], ``A`` [r, d], ``B`` [V, r] bf16; ``base`` [M, V] and ``prior``
     [V] (cast to bf16, the runner's buffer dtype); ``alpha``/``beta`` fp32 [M].
@@ -53,7 +53,13 @@ def eager_step_bf16(h, A, B, base, prior: Optional[torch.Tensor], alpha, beta, a
         pb = (b * prior.to(bf).reshape(1, -1).float()).to(bf)
         with_prior = logits - pb                     # 453-455
         logits = torch.where(b != 0, with_prior, logits)
-    return torch.argmax(logits, dim=-1)              # 456
+    return logits
+
+
+def eager_step_bf16(h, A, B, base, prior: Optional[torch.Tensor], alpha, beta, act: str = "identity"):
+    """int64 [M] ids of one draft step on the reference's eager bf16 path (arguments as
+    ``eager_logits_bf16``)."""
+    return torch.argmax(eager_logits_bf16(h, A, B, base, prior, alpha, beta, act), dim=-1)   # 456
 
 
 def step_fp32(h, A, B, base, prior: Optional[torch.Tensor], alpha, beta, act: str = "identity"):

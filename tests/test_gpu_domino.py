@@ -57,10 +57,10 @@ def test_domino_step_strided_inputs_and_outputs(pkg, dev):
 
 
 class _Draft(nn.Module):
-    def __init__(self, D, G, E, V, fc1_bias, fc2_bias, g):
+    def __init__(self, D, G, E, V, fc1_bias, fc2_bias, g, gru_bias=False):
         super().__init__()
         self.embed_proj = nn.Sequential(nn.Linear(D + G, E, bias=fc1_bias), nn.SiLU(), nn.Linear(E, V, bias=fc2_bias))
-        self.prefix_gru = nn.GRU(D, G, num_layers=1, batch_first=True, bias=False)
+        self.prefix_gru = nn.GRU(D, G, num_layers=1, batch_first=True, bias=gru_bias)
         with torch.no_grad():
             for p in self.parameters():
                 p.copy_(torch.randn(p.shape, generator=g) * 0.02)
@@ -75,15 +75,17 @@ class _Target(nn.Module):
             self.model.embed_tokens.weight.copy_(torch.randn(V, D, generator=g))
 
 
-@pytest.mark.parametrize("B,S,P,D,G,E,V,fc1_bias,fc2_bias", [
-    (2, 6, 2, 256, 128, 256, 3001, True, True),
-    (1, 14, 2, 4096, 1024, 1024, 151936, False, False),
+@pytest.mark.parametrize("B,S,P,D,G,E,V,fc1_bias,fc2_bias,gru_bias", [
+    (2, 6, 2, 256, 128, 256, 3001, True, True, False),
+    (1, 14, 2, 4096, 1024, 1024, 151936, False, False, False),
+    (3, 5, 3, 512, 256, 512, 20011, True, False, True),     # GRU with b_ih and b_hh
 ])
-def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, fc2_bias):
+def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, fc2_bias, gru_bias):
     """The hipGraph rollout against the oracle's, fed the device's own ids (each step is then
     checked on its own history): ids under the margin rule, scores within 1e-3."""
+    print(f"case domino rollout B={B} S={S} P={P} D={D} G={G} E={E} V={V} gru_bias={gru_bias}", flush=True)
     g = torch.Generator().manual_seed(11 + V)
-    draft = _Draft(D, G, E, V, fc1_bias, fc2_bias, g).to(torch.bfloat16)
+    draft = _Draft(D, G, E, V, fc1_bias, fc2_bias, g, gru_bias).to(torch.bfloat16)
     target = _Target(V, D, g).to(torch.bfloat16)
     runner = pkg.DraftCorrectionGraphRunner(draft_model=draft.to(dev), target_model=target.to(dev), batch_size=B,
                                             steps=S, hidden_dim=D, gru_hidden_dim=G, vocab_size=V,
@@ -98,7 +100,9 @@ def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, 
     ids = out.cpu().numpy()
     W1 = _f(draft.embed_proj[0].weight)
     ref_ids, ref_sc, ref_sec = DO.domino_rollout(
-        prefix.numpy(), _f(hiddens), _f(base), W_hh=_f(draft.prefix_gru.weight_hh_l0), b_hh=None,
+        prefix.numpy(), _f(hiddens), _f(base), W_hh=_f(draft.prefix_gru.weight_hh_l0),
+        b_hh=_f(draft.prefix_gru.bias_hh_l0) if gru_bias else None,
+        b_ih=_f(draft.prefix_gru.bias_ih_l0) if gru_bias else None,
         w_z=W1[:, :D], fc1_bias=None if not fc1_bias else _f(draft.embed_proj[0].bias), w_s=W1[:, D:],
         fc2=_f(draft.embed_proj[2].weight), fc2_bias=None if not fc2_bias else _f(draft.embed_proj[2].bias),
         alpha=0.8, embed=_f(target.model.embed_tokens.weight), W_ih=_f(draft.prefix_gru.weight_ih_l0),

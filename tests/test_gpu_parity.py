@@ -650,11 +650,11 @@ def test_gru_step(pkg, dev, nb, G):
 class _Head(torch.nn.Module):
     """Duck-typed local head: the attributes DeLSGraphRunner reads."""
 
-    def __init__(self, V, E, G, r, act, rank_bias, seed, std=0.2):
+    def __init__(self, V, E, G, r, act, rank_bias, seed, std=0.2, gru_bias=False):
         super().__init__()
         g = torch.Generator().manual_seed(seed)
         self.embed_tokens = torch.nn.Embedding(V, E)
-        self.prefix_gru = torch.nn.GRU(E, G, num_layers=1, batch_first=True, bias=False)
+        self.prefix_gru = torch.nn.GRU(E, G, num_layers=1, batch_first=True, bias=gru_bias)
         self.rank_proj = torch.nn.Linear(G, r, bias=rank_bias)
         self.low_rank_lm_head = torch.nn.Linear(r, V, bias=False)
         self.rank_activation = act
@@ -662,6 +662,9 @@ class _Head(torch.nn.Module):
             self.embed_tokens.weight.copy_(torch.randn(V, E, generator=g))
             self.prefix_gru.weight_ih_l0.copy_(torch.randn(3 * G, E, generator=g) * std)
             self.prefix_gru.weight_hh_l0.copy_(torch.randn(3 * G, G, generator=g) * std)
+            if gru_bias:
+                self.prefix_gru.bias_ih_l0.copy_(torch.randn(3 * G, generator=g) * 0.3)
+                self.prefix_gru.bias_hh_l0.copy_(torch.randn(3 * G, generator=g) * 0.3)
             self.rank_proj.weight.copy_(torch.randn(r, G, generator=g) * std)
             if rank_bias:
                 self.rank_proj.bias.copy_(torch.randn(r, generator=g) * 0.1)
@@ -782,6 +785,88 @@ def test_graph_runner_accepts_fp32_and_fp16_heads(pkg, dev, head_dtype):
     torch.testing.assert_close(r_bf16.static_scores, sc, rtol=0, atol=0)
     r_other.close()
     r_bf16.close()
+
+
+def _fp32_reference_rollout(head, prefix, base, prior, alphas, betas, forced):
+    """The reference runner's rollout for an fp32 head, every buffer fp32 (code/kernel/dels.py:252,
+    260-276, 425-467), on the CPU with torch's own GRU cell: per step the fp32 scores
+    ``act(F.linear(h, A, b)) . B^T * alpha + base - beta * prior``; the GRU fed ``forced``."""
+    gru = head.prefix_gru
+    cell = torch.nn.GRUCell(gru.input_size, gru.hidden_size, bias=gru.bias)
+    with torch.no_grad():
+        cell.weight_ih.copy_(gru.weight_ih_l0)
+        cell.weight_hh.copy_(gru.weight_hh_l0)
+        if gru.bias:
+            cell.bias_ih.copy_(gru.bias_ih_l0)
+            cell.bias_hh.copy_(gru.bias_hh_l0)
+    emb = head.embed_tokens.weight
+    nb, steps, V = base.shape
+    scores = torch.empty(nb, steps, V)
+    with torch.no_grad():
+        h = cell(emb[prefix.reshape(-1)], torch.zeros(nb, gru.hidden_size))
+        for s in range(steps):
+            rank = torch.nn.functional.linear(h, head.rank_proj.weight, head.rank_proj.bias)
+            if head.rank_activation == "silu":
+                rank = torch.nn.functional.silu(rank)
+            sc = rank @ head.low_rank_lm_head.weight.t() * alphas[s] + base[:, s]
+            if betas[s] != 0.0:
+                sc = sc - betas[s] * prior
+            scores[:, s] = sc
+            if s + 1 < steps:
+                h = cell(emb[forced[:, s]], h)
+    return scores
+
+
+@pytest.mark.parametrize("nb,steps,V,E,G,r,std", [(4, 6, 20011, 32, 256, 128, 0.06),
+                                                  (8, 5, 30011, 64, 1024, 256, 0.02)])
+def test_graph_runner_fp32_head_against_fp32_reference(pkg, dev, nb, steps, V, E, G, r, std):
+    """An fp32 local head with weights that bf16 cannot represent.  The reference keeps
+    every buffer in fp32; this runner streams the weights in bf16.  Teacher-forced on the
+    device's ids, every step's id must equal the fp32 reference's wherever the reference's
+    top-2 margin exceeds 2^-5 of the row's low-rank magnitude ``alpha max_v |rank|.|B_v|``
+    (a budget for bf16 weights, state and rank: each rounds by at most 2^-9 relative);
+    elsewhere the device's pick must be a near-maximum.  Prints the overall agreement."""
+    print(f"case fp32 head vs fp32 reference nb={nb} steps={steps} V={V} G={G} r={r}", flush=True)
+    g = torch.Generator().manual_seed(900 + G)
+    head = _Head(V, E, G, r, "silu", True, seed=901 + G, std=std).float()
+    with torch.no_grad():                                   # fp32 values off the bf16 grid
+        for p in head.parameters():
+            p.add_(torch.randn(p.shape, generator=g) * p.abs().mean() * 2 ** -8)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0)
+    alphas = [0.25 + 0.05 * i for i in range(steps)]
+    betas = [0.3] * steps
+    runner = pkg.DeLSGraphRunner(local_head=head.to(dev), batch_size=nb, steps=steps, vocab_size=V,
+                                 alpha_values=alphas, beta_values=betas, baseline_logits=prior, device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    base = torch.randn(nb, steps, V, generator=g) * 3
+    out = runner(prefix.to(dev), base.to(dev)).cpu()
+    runner.close()
+    head = head.cpu()
+    ref = _fp32_reference_rollout(head, prefix, base, prior, alphas, betas, out)
+    top2 = torch.topk(ref, 2, dim=-1).values.double()
+    margin = top2[..., 0] - top2[..., 1]
+    with torch.no_grad():
+        pick = torch.gather(ref, 2, out.unsqueeze(-1)).squeeze(-1).double()
+        ref_ids = torch.argmax(ref, dim=-1)
+        # the low-rank magnitude per (row, step) along the teacher-forced history
+        mags = torch.empty(nb, steps)
+        gru = head.prefix_gru
+        cell = torch.nn.GRUCell(gru.input_size, gru.hidden_size, bias=gru.bias)
+        cell.load_state_dict({"weight_ih": gru.weight_ih_l0, "weight_hh": gru.weight_hh_l0})
+        h = cell(head.embed_tokens.weight[prefix.reshape(-1)], torch.zeros(nb, G))
+        for s in range(steps):
+            rank = torch.nn.functional.silu(torch.nn.functional.linear(h, head.rank_proj.weight, head.rank_proj.bias))
+            mags[:, s] = (rank.abs() @ head.low_rank_lm_head.weight.abs().t()).amax(dim=1) * alphas[s]
+            if s + 1 < steps:
+                h = cell(head.embed_tokens.weight[out[:, s]], h)
+    budget = mags.double() * 2 ** -5
+    pinned = margin > budget
+    match = out == ref_ids
+    print(f"  fp32 head: id agreement {match.double().mean():.4f} ({int(match.sum())}/{match.numel()}), pinned "
+          f"{int(pinned.sum())}, pinned agreement {match[pinned].double().mean():.4f}", flush=True)
+    assert bool(match[pinned].all()), torch.nonzero(pinned & ~match)
+    assert bool((pick >= top2[..., 0] - budget).all())
+    assert int(pinned.sum()) >= match.numel() // 4
 
 
 def test_runner_driven_by_position_mix_head(pkg, dev, tmp_path):

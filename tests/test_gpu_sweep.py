@@ -157,6 +157,52 @@ def test_graph_runner_rollout_sweep(pkg, dev, seed):
     runner.close()
 
 
+@pytest.mark.parametrize("nb,steps,G,r,V", [(8, 5, 1024, 256, 30011),     # GRU inside every decode launch
+                                             (3, 4, 256, 128, 20011)])      # the GRU step kernel between launches
+def test_graph_runner_rollout_with_gru_bias(pkg, dev, nb, steps, G, r, V):
+    """A local head whose GRU has biases (b_ih folded into the input table, b_hh
+    into gh, and gh = b_hh at the zero-state first step), teacher-forced against
+    the oracle with both biases."""
+    from test_gpu_parity import _Head
+
+    print(f"case rollout gru bias nb={nb} steps={steps} G={G} r={r} V={V}", flush=True)
+    E = 64
+    head = _Head(V, E, G, r, "silu", True, seed=77 + G, std=0.02 if G >= 1024 else 0.1, gru_bias=True).to(dev)
+    g = torch.Generator().manual_seed(78 + G)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0)
+    alphas = [1.0 + 0.05 * i for i in range(steps)]
+    betas = [0.05] * steps
+    runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V, alpha_values=alphas,
+                                 beta_values=betas, baseline_logits=prior, device=dev)
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    # small base logits: the low-rank term, and with it the GRU state, decides the ids
+    base = (torch.randn(nb, steps, V, generator=g) * 0.05).to(torch.bfloat16)
+    out = runner(prefix.to(dev), base.to(dev)).clone()
+    scores = runner.static_scores.clone()
+    torch.cuda.synchronize()
+    dev_ids = out.cpu().numpy()
+    gru = head.prefix_gru
+    rid, rsc, rsec = oracle.rollout(
+        prefix.numpy().reshape(-1), f(base), embed=f(head.embed_tokens.weight), W_ih=f(gru.weight_ih_l0),
+        b_ih=f(gru.bias_ih_l0), W_hh=f(gru.weight_hh_l0), b_hh=f(gru.bias_hh_l0),
+        A=f(head.rank_proj.weight), rank_bias=f(head.rank_proj.bias), act="silu",
+        B=f(head.low_rank_lm_head.weight), prior=f(prior.to(torch.bfloat16)), alphas=alphas, betas=betas,
+        forced_ids=dev_ids)
+    res = oracle.check_parity(dev_ids.reshape(-1), f(scores).reshape(-1), rid.reshape(-1), rsc.reshape(-1),
+                              rsec.reshape(-1))
+    assert res["id_mismatch_pinned"] == 0, res
+    assert res["max_score_err"] < 2e-2, res
+    # without b_hh the oracle picks other ids: the device's ids show that the bias reaches its GRU
+    rid0, _, _ = oracle.rollout(
+        prefix.numpy().reshape(-1), f(base), embed=f(head.embed_tokens.weight), W_ih=f(gru.weight_ih_l0),
+        b_ih=f(gru.bias_ih_l0), W_hh=f(gru.weight_hh_l0), b_hh=None,
+        A=f(head.rank_proj.weight), rank_bias=f(head.rank_proj.bias), act="silu",
+        B=f(head.low_rank_lm_head.weight), prior=f(prior.to(torch.bfloat16)), alphas=alphas, betas=betas,
+        forced_ids=dev_ids)
+    assert not np.array_equal(rid0, dev_ids)
+    runner.close()
+
+
 @pytest.mark.parametrize("seed", range(8))
 def test_gather_argmax_sweep(pkg, dev, seed):
     """The Markov path's gathered-rank argmax over seeded shapes (GEMV and

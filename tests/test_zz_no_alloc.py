@@ -5,12 +5,14 @@ Called through the C ABI (ctypes) and compared, bit for bit, with
 dels_lowrank_argmax on a fresh zeroed workspace: same kernels, so the same ids
 and scores.  Each case makes two calls in a row, the second with a smaller
 input, so the second runs on what the first left in the shared array.  The
-first test must be the process's first call of the entry point (this file
-holds the only callers): it checks that a first call under stream capture is
-refused, since that call clears the array.
+first test checks, in a fresh child process (so that no earlier call has set
+the array up), that a first call under stream capture is refused, since that
+call clears the array.
 """
 
-import ctypes
+import os
+import subprocess
+import sys
 
 import pytest
 import torch
@@ -64,21 +66,45 @@ def _noalloc(pkg, x, A, B):
     return ids, sc
 
 
-def test_first_call_under_capture_is_refused(pkg, dev):
-    print("case noalloc: first call under capture", flush=True)
-    lib = pkg._lib.load()
-    x, A, B = _inputs(pkg, dev, 4, 256, 64, 3001, seed=1, packed=True)
-    ids = torch.zeros(4, dtype=torch.int64, device=dev)
-    sc = torch.zeros(4, dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
-    side = torch.cuda.Stream()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(graph, stream=side):
-            rc = lib.dels_lowrank_argmax_noalloc(*_args(pkg, x, A, B, ids, sc), side.cuda_stream)
-    assert rc == DELS_ERR_INVALID_ARGUMENT
-    assert b"must not be captured" in lib.dels_last_error()
-    del graph
+_FIRST_CALL_CHILD = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+sys.path.insert(0, sys.argv[2])
+import torch
+import __graft_entry__
+import test_zz_no_alloc as t
+pkg = __graft_entry__.load_package()
+dev = torch.device("cuda:0")
+lib = pkg._lib.load()
+x, A, B = t._inputs(pkg, dev, 4, 256, 64, 3001, seed=1, packed=True)
+ids = torch.zeros(4, dtype=torch.int64, device=dev)
+sc = torch.zeros(4, dtype=torch.float32, device=dev)
+torch.cuda.synchronize()
+side = torch.cuda.Stream()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        rc = lib.dels_lowrank_argmax_noalloc(*t._args(pkg, x, A, B, ids, sc), side.cuda_stream)
+assert rc == t.DELS_ERR_INVALID_ARGUMENT, rc
+assert b"must not be captured" in lib.dels_last_error()
+del graph
+# after the refusal an eager call sets the array up and matches the workspace entry point
+got = t._noalloc(pkg, x, A, B)
+want = t._with_workspace(pkg, x, A, B)
+torch.cuda.synchronize()
+assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
+print("first-call child ok", flush=True)
+"""
+
+
+def test_first_call_under_capture_is_refused():
+    """In a child process that has made no call of the entry point yet."""
+    print("case noalloc: first call under capture (child process)", flush=True)
+    here = os.path.dirname(os.path.abspath(__file__))
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_CHILD, os.path.dirname(here), here],
+                         capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0 and "first-call child ok" in res.stdout, (res.returncode, res.stdout[-2000:],
+                                                                         res.stderr[-2000:])
 
 
 @pytest.mark.parametrize("first,second", [
