@@ -183,6 +183,36 @@ constexpr uint32_t half_neg_inf() { return std::is_same<T, bf16_t>::value ? 0xff
 template <typename BaseT>
 constexpr int stages_per_chunk() { return kLineBytes / ((int)sizeof(BaseT) * kTileCols); }
 
+// Vocabulary rows of a tile enter the 32x32 MFMAs permuted: operand row m (the
+// lane's row l%32 of the A operand) holds tile column 16*((m>>2)&1) + 4*(m>>3) +
+// (m&3), so that output lane l holds the consecutive columns 16h .. 16h+15.
+// That column is row perm_row(m) of 16-row block row 2T + perm_block(m).
+__device__ __forceinline__ int perm_block(int m) { return (m >> 2) & 1; }
+__device__ __forceinline__ int perm_row(int m) { return 4 * (m >> 3) + (m & 3); }
+
+// A base chunk in LDS: one 128-byte line per row, its 16-byte pieces rotated by
+// the row, so that 32 consecutive rows read at one column spread over the banks.
+__device__ __forceinline__ int line_swizzle(int r) { return (r >> 1) & 7; }
+// Byte `byte` of row r's line.
+__device__ __forceinline__ const char* line_at(const char* q, int r, int byte) {
+    return q + r * kLineBytes + (((byte >> 4) ^ line_swizzle(r)) << 4) + (byte & 15);
+}
+// Direct-to-LDS load i (of kRowsPerWG / 8) of the chunk whose first column is
+// col0: rows 8i .. 8i+7 of the workgroup (first row m_wg), each a whole line;
+// lane L fetches piece (L%8) ^ swizzle of row 8i + L/8.  Rows past M repeat row
+// M-1; columns past V are clamped into the row (their candidates are masked).
+template <typename BaseT>
+__device__ __forceinline__ void dma_base_lines(const TiledKArgs& a, int m_wg, int col0, int i, char* q) {
+    constexpr int kPieceElems = 16 / (int)sizeof(BaseT);
+    const int lane = threadIdx.x & 63;
+    const int r = 8 * i + (lane >> 3);
+    const int p = (lane & 7) ^ line_swizzle(r);
+    const int col = min(col0 + p * kPieceElems, a.V - kPieceElems);
+    const int m = min(m_wg + r, a.M - 1);
+    dma16(a.base, (uint32_t)m * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT) + (uint32_t)col * (uint32_t)sizeof(BaseT),
+          q + i * 1024);
+}
+
 }  // namespace tiled
 
 // EXACT: V is a multiple of the 32-column tile, so no tile needs masking.
@@ -259,7 +289,6 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));   // vmcnt(0); expcnt and lgkmcnt left free
 
     const char* Bg = reinterpret_cast<const char*>(a.B);
-    const char* baseg = static_cast<const char*>(a.base);
     const char* priorg = static_cast<const char*>(a.prior);
 
     // B tile of stage st: the 32 vocabulary rows enter the MFMA permuted -- operand
@@ -267,8 +296,8 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
     // lane l ends with the 16 consecutive columns 16h .. 16h+15 of its row.  LDS
     // block s (1 KiB) is the A operand of K step s in lane order (lane L: column
     // pi(L%32), K 16s + 8h .. +7), gathered from block row 2T + ((m>>2)&1).
-    const int hh = (rl >> 2) & 1;
-    const uint32_t b_lane = (uint32_t)(((4 * (rl >> 3) + (rl & 3)) + 16 * h) * 16);
+    const int hh = perm_block(rl);
+    const uint32_t b_lane = (uint32_t)((perm_row(rl) + 16 * h) * 16);
     auto issue_b = [&](BBuf& S, int st, int piece) {
         const int blk = min(2 * tile_of(st) + hh, a.nblk16 - 1);
         const int s = wave * kBPieces + piece;                      // K step of this load
@@ -285,19 +314,9 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
             dma4(priorg, (uint32_t)v * 2u, S.prior[wave]);
         }
     };
-    // Base chunk c: load i (of 32) brings rows 8i .. 8i+7, each a whole 128-byte
-    // line; lane L takes row 8i + L/8 and, of its eight 16-byte pieces, piece
-    // (L%8) ^ swz(row), so that slot k of a row holds piece k ^ swz(row).
-    constexpr int kPieceElems = 16 / (int)sizeof(BaseT);
-    auto swz = [](int r) { return (r >> 1) & 7; };
+    // Base chunk c (clamped to the workgroup's last): whole lines of the rows.
     auto issue_q = [&](QBuf& Q, int c, int piece) {
-        const int i = wave * kQPieces + piece;
-        const int r = 8 * i + (lane >> 3);
-        const int p = (lane & 7) ^ swz(r);
-        const int col = min((T0 + min(c, last_chunk) * SPC) * kTileCols + p * kPieceElems, a.V - kPieceElems);
-        const int m = min(m_wg + r, a.M - 1);
-        dma16(baseg, (uint32_t)m * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT) + (uint32_t)col * (uint32_t)sizeof(BaseT),
-              Q.q + i * 1024);
+        dma_base_lines<BaseT>(a, m_wg, (T0 + min(c, last_chunk) * SPC) * kTileCols, wave * kQPieces + piece, Q.q);
     };
 
     // Epilogue operands of one stage in registers: the base values of the lane's
@@ -315,8 +334,7 @@ __global__ __launch_bounds__(tiled::kThreads) void fused_argmax_tiled_kernel(Til
         const int vs = tile_of(st) * kTileCols;
         const int v = vs + 16 * h + 4 * g;                           // column of candidate 4g
         const bool partial = !EXACT && vs + kTileCols > a.V;          // only the last tile of the vocabulary
-        const int byte = ((st % SPC) * kTileCols + 16 * h + 4 * g) * (int)sizeof(BaseT);   // within the line
-        const char* src = Q.q + qrow * kLineBytes + (((byte >> 4) ^ swz(qrow)) << 4) + (byte & 15);
+        const char* src = line_at(Q.q, qrow, ((st % SPC) * kTileCols + 16 * h + 4 * g) * (int)sizeof(BaseT));
         if constexpr (sizeof(BaseT) == 4) {
             const u32x4 w = *reinterpret_cast<const u32x4*>(src);
 #pragma unroll

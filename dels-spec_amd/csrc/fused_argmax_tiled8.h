@@ -13,16 +13,20 @@
 //
 // The structure is the bf16 tiled kernel's (fused_argmax_tiled.h): 8 waves of
 // 32 rows, 256 rows and a contiguous chunk of 32-column vocabulary tiles per
-// workgroup, one tile per pipeline stage, stage buffers filled by
-// direct-to-LDS loads, the combine of stage st-1 interleaved between the MFMAs
-// of stage st.  What differs is the operand order: the 32x32x64 MFMA takes, for
-// lane l, 32 consecutive K bytes 32*(l/32) .. of row l%32 of a 64-deep step.
-// The K128 blocks (16 rows x 128 K, lane L: row L%16, K 32*(L/16) .. +31 as two
-// 16-byte halves) hold exactly those runs, so the B tile is gathered into
-// step-major LDS blocks of 2 KiB ([half][lane][16 B]) by the loads themselves;
-// every operand read is then two contiguous KiB.  The rank operand uses the
-// same K order (bytes in natural order within each 32-byte run), so the MFMA,
-// which pairs A and B by (lane group, byte), computes the plain dot product.
+// workgroup, one tile per stage, B double-buffered in LDS by direct-to-LDS
+// loads, the base logits in whole 128-byte lines per row (a two-chunk ring),
+// the vocabulary rows of a tile permuted so that each lane holds 16 consecutive
+// columns, the combine of stage st-1 interleaved between the MFMAs of stage st.
+// What differs is the operand order: the 32x32x64 MFMA takes, for lane l, 32
+// consecutive K bytes 32*(l/32) .. of row l%32 of a 64-deep step.  The K128
+// blocks (16 rows x 128 K, lane L: row L%16, K 32*(L/16) .. +31 as two 16-byte
+// halves) hold exactly those runs, so the B tile is gathered into step-major
+// LDS blocks of 2 KiB ([half][lane][16 B]) by the loads themselves; every
+// operand read is then two contiguous KiB.  The rank operand uses the same K
+// order (bytes in natural order within each 32-byte run), so the MFMA, which
+// pairs A and B by (lane group, byte), computes the plain dot product.  B is
+// half the bytes of the bf16 kernel's, so the base logits are most of what the
+// CUs take in.
 #pragma once
 
 #include "fp8.h"
@@ -35,32 +39,12 @@ namespace tiled8 {
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
 constexpr int kTileCols = 32;
-constexpr int kLdsBytes = 160 * 1024;
 constexpr int kSideBytes = 256;   // per wave and stage: the prior slice, the B scales
 constexpr int kOperandAhead = 2;
 
 // 64-deep K steps of r = 128 * KS8.
 template <int KS8>
 constexpr int steps() { return 2 * KS8; }
-template <int KS8>
-constexpr int b_bytes() { return steps<KS8>() * 2048; }
-template <typename BaseT>
-constexpr int base_bytes_per_wave() { return 32 * kTileCols * (int)sizeof(BaseT); }
-template <int KS8, typename BaseT>
-constexpr int stage_bytes() {
-    return b_bytes<KS8>() + kWaves * (base_bytes_per_wave<BaseT>() + 2 * kSideBytes);
-}
-template <int KS8, typename BaseT>
-constexpr int num_buffers() {
-    constexpr int n = kLdsBytes / stage_bytes<KS8, BaseT>();
-    return n > 4 ? 4 : n;
-}
-// Direct-to-LDS loads per wave and stage: B (two per step, split over the
-// waves), base, prior, B scales.
-template <int KS8, typename BaseT, bool PRIOR>
-constexpr int loads_per_stage() {
-    return 2 * steps<KS8>() / kWaves + (sizeof(BaseT) == 4 ? 4 : 2) + (PRIOR ? 1 : 0) + 1;
-}
 
 __device__ __forceinline__ f32x16 mfma_e4m3_32x32x64(const i32x8& a, const i32x8& b, f32x16 acc) {
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc, 0, 0, 0, 127, 0, 127);
@@ -73,46 +57,49 @@ template <int KS8, typename BaseT, typename PriorT, bool EXACT>
 __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(TiledKArgs a) {
 #pragma clang fp contract(off)
     using namespace tiled8;
-    constexpr int kSteps = steps<KS8>();
-    constexpr int kB = b_bytes<KS8>();
-    constexpr int kBaseW = base_bytes_per_wave<BaseT>();
+    using tiled::kLineBytes;
+    using tiled::kRowsPerWG;
+    constexpr int kSteps = steps<KS8>();                             // 64-deep K steps
     constexpr bool kPrior = !is_no_prior<PriorT>::value;
-    constexpr int NBUF = num_buffers<KS8, BaseT>();
-    constexpr int P = NBUF - 1;                          // stages in flight
-    constexpr int E = loads_per_stage<KS8, BaseT, kPrior>();
-    constexpr int nb = 2 * kSteps / kWaves;              // B loads per wave and stage
-    constexpr int nbase = sizeof(BaseT) == 4 ? 4 : 2;
+    constexpr int SPC = tiled::stages_per_chunk<BaseT>();            // 2 (16-bit base) or 1 (fp32)
+    constexpr int kBPieces = 2 * kSteps / kWaves;                    // 1-KiB B loads per wave and stage
+    constexpr int kQPieces = kRowsPerWG * kLineBytes / 1024 / kWaves; // base chunk loads per wave (4)
+    constexpr int kEB = kBPieces + 1 + (kPrior ? 1 : 0);              // + the B scales, + the prior
     constexpr int kWB = sizeof(BaseT) == 4 ? 16 : 8;
     constexpr int kWP = sizeof(PriorT) == 4 ? 16 : 8;
     constexpr int kCands = 16;
     constexpr int kAhead = kOperandAhead;
-    static_assert(NBUF >= 2, "stage does not fit twice in LDS");
     static_assert((2 * kSteps) % kWaves == 0, "B loads per stage must split over the waves");
-    static_assert(2 * E <= 63, "vmcnt holds the loads of two stages");
 
-    struct __attribute__((aligned(1024))) Stage {
-        char b[kB];                              // [step][half][lane][16 B]
-        char base[kWaves][kBaseW];
+    struct __attribute__((aligned(1024))) BBuf {
+        char b[kSteps * 2048];                   // [step][half][lane][16 B]
         char prior[kWaves][kSideBytes];
         char bsc[kWaves][kSideBytes];            // fp32 scales of the tile's 32 vocabulary rows
     };
-    struct NoStage {};
-    __shared__ Stage lds0, lds1;
-    __shared__ std::conditional_t<(NBUF > 2), Stage, NoStage> lds2;
-    __shared__ std::conditional_t<(NBUF > 3), Stage, NoStage> lds3;
+    struct __attribute__((aligned(1024))) QBuf {
+        char q[kRowsPerWG * kLineBytes];         // one 128-byte line of base logits per row
+    };
+    __shared__ BBuf bb0, bb1;
+    __shared__ QBuf qb0, qb1;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rl = lane & 31;
     const int h = lane >> 5;
-    const int mw = blockIdx.y * 256 + wave * 32;
+    const int m_wg = blockIdx.y * kRowsPerWG;
+    const int mw = m_wg + wave * 32;
     const bool wave_active = mw < a.M;
-    const int T0 = (int)(((int64_t)blockIdx.x * a.ntiles) / gridDim.x);
-    const int nst = (int)(((int64_t)(blockIdx.x + 1) * a.ntiles) / gridDim.x) - T0;
-    auto tile_of = [&](int st) { return T0 + st; };
+    // vocabulary chunk: tiles [T0, T0 + nst), starting on a base chunk boundary
+    const int nunits = (a.ntiles + SPC - 1) / SPC;
+    const int u0 = (int)(((int64_t)blockIdx.x * nunits) / gridDim.x);
+    const int u1 = (int)(((int64_t)(blockIdx.x + 1) * nunits) / gridDim.x);
+    const int T0 = u0 * SPC;
+    const int nst = max(0, min(a.ntiles, u1 * SPC) - T0);
+    const int last_chunk = max(nst - 1, 0) / SPC;
+    auto tile_of = [&](int st) { return min(T0 + min(st, max(nst - 1, 0)), a.ntiles - 1); };
 
     // ---- the rank operand: this lane's row, K runs 64s + 32h .. +31, e4m3 ----
-    // (quantised by quantize_rank_e4m3_kernel: rank_q [M][ldrank] bytes, sR [M])
+    // (quantised beforehand: rank_q [M][ldrank] bytes, sR [M])
     const int mrow = min(mw + rl, a.M - 1);
     const uint8_t* rqp = a.rank_q + (int64_t)mrow * a.ldrank + 32 * h;
     i32x8 rq[kSteps];
@@ -132,81 +119,71 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     const uint32_t psel_lo = use_prior ? 0x01000c0cu : 0x0c0c0c0cu;   // v_perm_b32: bytes 1,0 -> 3,2
     float best = -__builtin_inff();
     int bidx = INT_MAX;
-    const uint32_t row_off = (uint32_t)mrow * (uint32_t)a.ldbase * (uint32_t)sizeof(BaseT);
     // Drain the loads above before any direct-to-LDS load (see the bf16 kernel:
     // otherwise the compiler waits for every stage load before each MFMA).
     __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));   // vmcnt(0)
 
     const char* Bg = reinterpret_cast<const char*>(a.B);
-    const char* baseg = static_cast<const char*>(a.base);
     const char* priorg = static_cast<const char*>(a.prior);
     const char* bscg = reinterpret_cast<const char*>(a.b_scale);
 
-    // B gather: load (step s, half h2) puts, in MFMA lane l, 16 bytes of the
-    // K128 block (row block 2T + (l%32)/16, K block s/2), lane (l%16) +
-    // 16*(2*(s%2) + l/32), half h2.
-    const uint32_t b_lane = (uint32_t)(lane & 15) * 16;
-    const uint32_t b_hi = ((lane >> 4) & 1) ? (uint32_t)KS8 * kFp8K128Block : 0u;
-    auto issue_piece = [&](Stage& S, int st, int piece) {
-        const int T = tile_of(st);
-        const int vs = T * kTileCols;
-        if (piece < nb) {
-            const int rb0 = min(2 * T, a.nblk16 - 1);
-            const bool two = 2 * T + 1 < a.nblk16;
-            const char* bt = Bg + (int64_t)rb0 * KS8 * kFp8K128Block;
-            const int ii = wave * nb + piece;               // (step, half) of this load
-            const int s = ii >> 1, h2 = ii & 1;
-            const uint32_t off = b_lane + (two ? b_hi : 0u) + (uint32_t)(s >> 1) * kFp8K128Block +
-                                 (uint32_t)(2 * (s & 1) + h) * 256 + (uint32_t)h2 * 1024;
-            dma16(bt, off, S.b + s * 2048 + h2 * 1024);
-        } else if (piece < nb + nbase) {
-            const int g = piece - nb;
-            char* dst = S.base[wave] + g * 1024;
-            if constexpr (sizeof(BaseT) == 4) {
-                const int v = min(vs + 4 * (2 * g + h), a.V - 4);
-                dma16(baseg, row_off + (uint32_t)v * 4u, dst);
-            } else {
-                const int v = min(vs + 8 * (2 * g + h), a.V - 8);
-                dma16(baseg, row_off + (uint32_t)v * 2u, dst);
-            }
-        } else if (piece == nb + nbase) {
-            const int v = min(vs + (lane & 31), a.V - 1);
-            dma4(bscg, (uint32_t)v * 4u, S.bsc[wave]);
+    // B gather: load (step s, half h2) puts, in MFMA lane l, 16 bytes of the K128
+    // block (block row 2T + perm_block(l%32), K block s/2), lane perm_row(l%32) +
+    // 16*(2*(s%2) + l/32), half h2 -- the 32 vocabulary rows permuted as in the
+    // bf16 kernel, so that lane l ends with the columns 16h .. 16h+15.
+    const int hh = tiled::perm_block(rl);
+    const uint32_t b_lane = (uint32_t)(tiled::perm_row(rl) * 16 + h * 256);
+    auto issue_b = [&](BBuf& S, int st, int piece) {
+        const int blk = min(2 * tile_of(st) + hh, a.nblk16 - 1);
+        const int ii = wave * kBPieces + piece;            // (step, half) of this load
+        const int s = ii >> 1, h2 = ii & 1;
+        const uint32_t off = (uint32_t)blk * (uint32_t)(KS8 * kFp8K128Block) + (uint32_t)(s >> 1) * kFp8K128Block +
+                             (uint32_t)(s & 1) * 512 + (uint32_t)h2 * 1024 + b_lane;
+        dma16(Bg, off, S.b + s * 2048 + h2 * 1024);
+    };
+    auto issue_side = [&](BBuf& S, int st, int which) {   // 0: B scales, 1: prior
+        const int vs = tile_of(st) * kTileCols;
+        if (which == 0) {
+            dma4(bscg, (uint32_t)min(vs + (lane & 31), a.V - 1) * 4u, S.bsc[wave]);
         } else if constexpr (kPrior) {
-            if constexpr (sizeof(PriorT) == 4) {
-                const int v = min(vs + (lane & 31), a.V - 1);
-                dma4(priorg, (uint32_t)v * 4u, S.prior[wave]);
-            } else {
-                const int v = min(vs + 2 * (lane & 15), a.V - 2);
-                dma4(priorg, (uint32_t)v * 2u, S.prior[wave]);
-            }
+            if constexpr (sizeof(PriorT) == 4) dma4(priorg, (uint32_t)min(vs + (lane & 31), a.V - 1) * 4u, S.prior[wave]);
+            else dma4(priorg, (uint32_t)min(vs + 2 * (lane & 15), a.V - 2) * 2u, S.prior[wave]);
         }
     };
-    auto issue_stage = [&](Stage& S, int st) {
-#pragma unroll
-        for (int piece = 0; piece < E; ++piece) issue_piece(S, st, piece);
+    auto issue_q = [&](QBuf& Q, int c, int piece) {
+        tiled::dma_base_lines<BaseT>(a, m_wg, (T0 + min(c, last_chunk) * SPC) * kTileCols, wave * kQPieces + piece,
+                                     Q.q);
+    };
+    // Loads of the next stage: B, the B scales and the prior of st + 1, then (the
+    // stages that open a chunk) base chunk c_next -- last, so that a wait for B can
+    // leave it in flight.
+    auto issue_piece = [&](BBuf& S, int st_next, QBuf& Q, int c_next, int piece) {
+        if (piece < kBPieces) issue_b(S, st_next, piece);
+        else if (piece < kEB) issue_side(S, st_next, piece - kBPieces);
+        else issue_q(Q, c_next, piece - kEB);
     };
 
-    // Epilogue operands of one stage in registers (candidate j = 4g + q is the
-    // lane's column 8g + 4h + q): base, prior and B scale values; columns past
-    // V carry a -inf base.
+    // Epilogue operands of one stage in registers (candidate j is the lane's
+    // column 16h + j): base, prior and B scale values; columns past V carry a
+    // -inf base.
     struct EpiRegs {
         uint32_t b[kWB];
         uint32_t p[kWP];
         float sb[16];
     };
     constexpr uint32_t kNegInf = sizeof(BaseT) == 4 ? 0xff800000u : tiled::half_neg_inf<BaseT>();
-    auto load_epi_group = [&](const Stage& S, int st, int g, EpiRegs& e) {
+    const int qrow = wave * 32 + rl;
+    auto load_epi_group = [&](const QBuf& Q, const BBuf& S, int st, int g, EpiRegs& e) {
         const int vs = tile_of(st) * kTileCols;
-        const int v = vs + 8 * g + 4 * h;
+        const int v = vs + 16 * h + 4 * g;
         const bool partial = !EXACT && vs + kTileCols > a.V;
+        const char* src = tiled::line_at(Q.q, qrow, ((st % SPC) * kTileCols + 16 * h + 4 * g) * (int)sizeof(BaseT));
         if constexpr (sizeof(BaseT) == 4) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(S.base[wave] + g * 1024 + lane * 16);
+            const u32x4 w = *reinterpret_cast<const u32x4*>(src);
 #pragma unroll
             for (int q = 0; q < 4; ++q) e.b[4 * g + q] = (partial && v + q >= a.V) ? kNegInf : w[q];
         } else {
-            const uint2 w = *reinterpret_cast<const uint2*>(S.base[wave] + (g >> 1) * 1024 +
-                                                            (rl + 32 * (g & 1)) * 16 + h * 8);
+            const uint2 w = *reinterpret_cast<const uint2*>(src);
             uint32_t w0 = w.x, w1 = w.y;
             if (partial) {
                 w0 = v < a.V ? w0 : ((w0 & 0xffff0000u) | kNegInf);
@@ -217,11 +194,11 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
             e.b[2 * g] = w0;
             e.b[2 * g + 1] = w1;
         }
-        const f32x4 sv = *reinterpret_cast<const f32x4*>(S.bsc[wave] + (8 * g + 4 * h) * 4);
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(S.bsc[wave] + (16 * h + 4 * g) * 4);
 #pragma unroll
         for (int q = 0; q < 4; ++q) e.sb[4 * g + q] = sv[q];
         if constexpr (kPrior) {
-            const char* pp = S.prior[wave] + (8 * g + 4 * h) * (int)sizeof(PriorT);
+            const char* pp = S.prior[wave] + (16 * h + 4 * g) * (int)sizeof(PriorT);
             if constexpr (sizeof(PriorT) == 4) {
                 const u32x4 w = *reinterpret_cast<const u32x4*>(pp);
 #pragma unroll
@@ -233,10 +210,10 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
             }
         }
     };
-    // Candidate j of stage stp; the empty volatile asm statements pin its work
-    // between the MFMAs (pure arithmetic would otherwise be gathered after the
-    // last MFMA of the stage).
-    auto epi_one = [&](const f32x16& accp, const EpiRegs& e, int slot0, int j) {
+    // Candidate j of the previous stage (first column cb); the empty volatile asm
+    // statements pin its work between the MFMAs (pure arithmetic would otherwise
+    // be gathered after the last MFMA of the stage).
+    auto epi_one = [&](const f32x16& accp, const EpiRegs& e, int cb, int j) {
         float av = accp[j];
         float sbv = e.sb[j];
         const uint32_t bw = e.b[sizeof(BaseT) == 4 ? j : (j >> 1)];
@@ -257,13 +234,14 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
         }
         const bool take = sc > best;   // candidates arrive in increasing index order
         best = take ? sc : best;
-        bidx = take ? slot0 + j : bidx;   // slot0 = 16 * stage, wave-uniform
+        bidx = take ? cb + j : bidx;
         asm volatile("" : "+v"(best), "+v"(bidx));
     };
     constexpr int kPer = (kCands + kSteps - 1) / kSteps;   // candidates per MFMA slot
-    auto contract = [&](const Stage& S, int st, Stage& next, int st_next, const f32x16& accp, const EpiRegs& ep,
-                        int stp, EpiRegs& ep_next) {
-        f32x16 acc;
+    auto contract = [&](auto issue_q_tag, const BBuf& S, const QBuf& Q, int st, BBuf& Sn, QBuf& Qn, int c_next,
+                        f32x16& acc, const f32x16& accp, const EpiRegs& ep, int cbp, EpiRegs& epn) {
+        constexpr bool ISSUE_Q = decltype(issue_q_tag)::value;
+        constexpr int E = kEB + (ISSUE_Q ? kQPieces : 0);
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[i] = 0.f;
         auto opnd = [&](int s) {
@@ -272,8 +250,6 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
             return i32x8{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], (int)hi[0], (int)hi[1], (int)hi[2],
                          (int)hi[3]};
         };
-        const bool issue = st_next >= 0;
-        const int slot0 = __builtin_amdgcn_readfirstlane(stp * 16);
         i32x8 opq[kAhead];
 #pragma unroll
         for (int i = 0; i < kAhead; ++i) opq[i] = opnd(i < kSteps ? i : 0);
@@ -286,30 +262,34 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int c = s * kPer; c < (s + 1) * kPer && c < kCands; ++c) {
-                epi_one(accp, ep, slot0, c);
-                if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
+                epi_one(accp, ep, cbp, c);
+                if ((c & 3) == 3) load_epi_group(Q, S, st, c >> 2, epn);
             }
 #pragma unroll
             for (int piece = 0; piece < E; ++piece)
-                if (s == piece * kSteps / E && issue) issue_piece(next, st_next, piece);
+                if (s == piece * kSteps / E) issue_piece(Sn, st + 1, Qn, c_next, piece);
         }
         // candidates not reached in the loop (fewer slots than 16 / kPer)
 #pragma unroll
         for (int c = kSteps * kPer; c < kCands; ++c) {
-            epi_one(accp, ep, slot0, c);
-            if ((c & 3) == 3) load_epi_group(S, st, c >> 2, ep_next);
+            epi_one(accp, ep, cbp, c);
+            if ((c & 3) == 3) load_epi_group(Q, S, st, c >> 2, epn);
         }
-        return acc;
+    };
+    auto issue_all = [&](auto issue_q_tag, BBuf& Sn, int st_next, QBuf& Qn, int c_next) {
+        constexpr int E = kEB + (decltype(issue_q_tag)::value ? kQPieces : 0);
+#pragma unroll
+        for (int piece = 0; piece < E; ++piece) issue_piece(Sn, st_next, Qn, c_next, piece);
     };
 
-    auto buf = [&](int i) -> Stage& {
-        if constexpr (NBUF > 3) { if (i == 3) return lds3; }
-        if constexpr (NBUF > 2) { if (i == 2) return lds2; }
-        return i == 1 ? lds1 : lds0;
-    };
+    // Pipeline as the bf16 kernel's: B(0), its side slices and base chunk 0 up
+    // front; at stage st every wave waits for its own loads of B(st) (the chunk
+    // loads issued during an even stage may stay in flight through the next
+    // barrier), the barrier publishes st, and the loads of st + 1 (and of the
+    // next chunk when st opens one) go out while st is contracted.
     f32x16 acc_prev;
     EpiRegs ep_prev, ep_cur;
-    int st_prev = 0;
+    int cb_prev = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         acc_prev[i] = 0.f;
@@ -320,46 +300,43 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
 #pragma unroll
     for (int i = 0; i < kWP; ++i) ep_prev.p[i] = 0u;
 
+    issue_all(std::true_type{}, bb0, 0, qb0, 0);
+    for (int st0 = 0; st0 < nst; st0 += 4) {
 #pragma unroll
-    for (int i = 0; i < P; ++i)
-        if (i < nst) issue_stage(buf(i), i);
-    for (int st0 = 0; st0 < nst; st0 += NBUF) {
-#pragma unroll
-        for (int u = 0; u < NBUF; ++u) {
+        for (int u = 0; u < 4; ++u) {
             const int st = st0 + u;
-            if (st < nst) {
-                const int younger = min(P - 1, nst - 1 - st);
-                if constexpr (P >= 3) {
-                    if (younger >= 2) tiled::stage_barrier<2 * E>();
-                    else if (younger == 1) tiled::stage_barrier<E>();
-                    else tiled::stage_barrier<0>();
-                } else if constexpr (P == 2) {
-                    if (younger >= 1) tiled::stage_barrier<E>();
-                    else tiled::stage_barrier<0>();
-                } else {
-                    tiled::stage_barrier<0>();
-                }
-                const int st_next = st + P < nst ? st + P : -1;
-                if (wave_active) {
-                    acc_prev = contract(buf(u), st, buf((u + P) % NBUF), st_next, acc_prev, ep_prev, st_prev, ep_cur);
-                    ep_prev = ep_cur;
-                    st_prev = st;
-                } else if (st_next >= 0) {
-                    issue_stage(buf((u + P) % NBUF), st_next);
-                }
+            if (st >= nst) break;
+            if (SPC == 2 && (u & 1) == 1) tiled::stage_barrier<kQPieces>();
+            else tiled::stage_barrier<0>();
+            BBuf& S = (u & 1) ? bb1 : bb0;
+            BBuf& Sn = (u & 1) ? bb0 : bb1;
+            const int cbuf = SPC == 2 ? ((u >> 1) & 1) : (u & 1);
+            const QBuf& Q = cbuf ? qb1 : qb0;
+            QBuf& Qn = cbuf ? qb0 : qb1;
+            const int c_next = st / SPC + 1;
+            const bool opens = (st % SPC) == 0;
+            if (wave_active) {
+                f32x16 acc;
+                if (opens) contract(std::true_type{}, S, Q, st, Sn, Qn, c_next, acc, acc_prev, ep_prev, cb_prev, ep_cur);
+                else contract(std::false_type{}, S, Q, st, Sn, Qn, c_next, acc, acc_prev, ep_prev, cb_prev, ep_cur);
+                acc_prev = acc;
+                ep_prev = ep_cur;
+                cb_prev = tile_of(st) * kTileCols + 16 * h;
+            } else if (opens) {
+                issue_all(std::true_type{}, Sn, st + 1, Qn, c_next);
+            } else {
+                issue_all(std::false_type{}, Sn, st + 1, Qn, c_next);
             }
         }
     }
     if (wave_active && nst > 0) {
 #pragma unroll
-        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, __builtin_amdgcn_readfirstlane(st_prev * 16), c);
+        for (int c = 0; c < kCands; ++c) epi_one(acc_prev, ep_prev, cb_prev, c);
     }
+    // no direct-to-LDS load may land after this point: the finish reuses the buffers
+    __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));
 
-    // decode the slot, merge the two column quads of the row, one key per row
-    if (bidx != INT_MAX) {
-        const int st = bidx >> 4, c = bidx & 15;
-        bidx = tile_of(st) * kTileCols + 8 * (c >> 2) + 4 * h + (c & 3);
-    }
+    // merge the two column halves of the row, one key per row
     const float ov = __shfl_xor(best, 32, 64);
     const int oi = __shfl_xor(bidx, 32, 64);
     if (argmax_better(ov, oi, best, bidx)) {
@@ -369,7 +346,7 @@ __global__ __launch_bounds__(tiled8::kThreads) void fused_argmax_tiled8_kernel(T
     const int m = mw + rl;
     const int fin_m[1] = {(h == 0 && m < a.M) ? m : -1};
     const unsigned long long fin_key[1] = {bidx == INT_MAX ? 0ull : pack_argmax(best, (uint32_t)bidx)};
-    tiled_argmax_finish(a, fin_m, fin_key, reinterpret_cast<int*>(&lds0));
+    tiled_argmax_finish(a, fin_m, fin_key, reinterpret_cast<int*>(&bb0));
 }
 
 template <int KS8, typename BaseT, typename PriorT>
