@@ -466,21 +466,18 @@ def bench_draft_step(pkg, args, dev, torch):
     local head hidden 1024 (embeddings 1024, rank 256, silu), per-position alpha/beta
     U[0, 0.6], the Zipf log-prior; hidden states ~ N(0, 1).
 
-    Algorithmic bytes: the LM head (W once, hidden, base logits written) + the
-    first-position argmax + per DeLS step the low-rank head, rank projection,
-    base rows and prior, and per GRU step W_hh and the input-table rows.  The
-    `fused_lm_head` record times the same block with the hand-written LM head
-    (position 0 argmaxed inside it, its logits never written)."""
+    The block as DeLSDraftStep builds it by default: the hand-written LM head
+    (lm_head_kernel, the position-0 argmax fused, its logits never written) and the
+    14-step rollout.  Algorithmic bytes: W once, hidden, the base rows of positions
+    1..k-1 written, the first ids; per DeLS step the low-rank head, rank projection,
+    base rows and prior; per GRU step W_hh and the input-table rows.  The
+    `library_lm_head` record times the same block with the library GEMM (hipBLASLt
+    through torch.mm, as nn.Linear) followed by the position-0 argmax."""
     wl = pkg.synth.draft_block_workload(dev)
     B, k, d, V, E, G, r = 8, 15, 4096, 151936, 1024, 1024, 256
     steps = k - 1
     W = wl.W
-    step = pkg.DeLSDraftStep(local_head=wl.head, lm_head_weight=W, batch_size=B, k_draft=k, vocab_size=V,
-                             alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior, device=dev)
     hiddens = wl.hiddens(3)
-    for i in range(3):
-        step(hiddens[i])
-    torch.cuda.synchronize(dev)
     n = 20
     cur = torch.cuda.current_stream(dev)
 
@@ -499,52 +496,59 @@ def bench_draft_step(pkg, args, dev, torch):
             times.append(e0.elapsed_time(e1) / n)
         return replay_stats(times)["median"] * 1e3
 
-    def block(i):
-        step.static_hidden.copy_(hiddens[i % 3])
-        step.replay()
+    def make(lm_head):
+        st = pkg.DeLSDraftStep(local_head=wl.head, lm_head_weight=W, batch_size=B, k_draft=k, vocab_size=V,
+                               alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior,
+                               device=dev, lm_head=lm_head)
+        for i in range(3):
+            st(hiddens[i])
+        torch.cuda.synchronize(dev)
+        return st
 
-    us_block = timed(block)
-    # the LM head of the block: the library GEMM (hipBLASLt through torch.mm, as nn.Linear)
-    us_gemm = timed(lambda i: torch.mm(hiddens[i % 3].view(B * k, d), W.t(), out=step.static_base.view(B * k, V)))
-    us_rollout = timed(lambda i: step.runner.replay())
-    gemm_bytes = 2 * V * d + 2 * B * k * d + 2 * B * k * V
+    def block_of(st):
+        def run(i):
+            st.static_hidden.copy_(hiddens[i % 3])
+            st.replay()
+        return run
+
     step_bytes = 2 * V * r + 2 * r * G + 2 * B * V + 2 * V + 12 * B      # low-rank head, A, base rows, prior, outputs
     gru_bytes = 2 * 3 * G * G + 2 * B * 3 * G + 4 * B * G                  # W_hh, input-table rows, state
-    total = gemm_bytes + 2 * B * V + steps * step_bytes + steps * gru_bytes
-    step.close()
-    # the same block with the hand-written LM head, the position-0 argmax fused into it
-    fstep = pkg.DeLSDraftStep(local_head=wl.head, lm_head_weight=W, batch_size=B, k_draft=k, vocab_size=V,
-                              alpha_values=wl.alphas, beta_values=wl.betas, baseline_logits=wl.prior, device=dev,
-                              lm_head="fused")
-    for i in range(3):
-        fstep(hiddens[i])
-    torch.cuda.synchronize(dev)
 
-    def fblock(i):
-        fstep.static_hidden.copy_(hiddens[i % 3])
-        fstep.replay()
-
-    us_fblock = timed(fblock)
+    # the default block: the hand-written LM head
+    step = make("auto")
+    assert step._fused_head, "the bench shape takes the hand-written LM head"
+    us_block = timed(block_of(step))
+    us_rollout = timed(lambda i: step.runner.replay())
     first = torch.empty(B, dtype=torch.int64, device=dev)
     first_sc = torch.empty(B, dtype=torch.float32, device=dev)
-    us_head = timed(lambda i: pkg.lm_head(hiddens[i % 3].view(B * k, d), fstep._w_p,
-                                          out=fstep.static_base.view(B * k, V), argmax_period=k, out_ids=first,
+    us_head = timed(lambda i: pkg.lm_head(hiddens[i % 3].view(B * k, d), step._w_p,
+                                          out=step.static_base.view(B * k, V), argmax_period=k, out_ids=first,
                                           out_score=first_sc))
-    fstep.close()
-    # hand-written head: W once, hidden, the base rows of positions 1..k-1 written, the first ids
+    step.close()
     head_bytes = 2 * V * d + 2 * B * k * d + 2 * B * (k - 1) * V + 12 * B
-    ftotal = head_bytes + steps * step_bytes + steps * gru_bytes
+    total = head_bytes + steps * step_bytes + steps * gru_bytes
+
+    # the same block with the library GEMM + row argmax
+    lstep = make("library")
+    us_lblock = timed(block_of(lstep))
+    us_gemm = timed(lambda i: torch.mm(hiddens[i % 3].view(B * k, d), W.t(), out=lstep.static_base.view(B * k, V)))
+    lstep.close()
+    gemm_bytes = 2 * V * d + 2 * B * k * d + 2 * B * k * V
+    ltotal = gemm_bytes + 2 * B * V + steps * step_bytes + steps * gru_bytes
     return {"workload": "draft block: batch 8, block 16 (k_draft 15), d 4096, V 151936, local head G 1024 r 256",
+            "lm_head": "lm_head_kernel (hand-written, position-0 argmax fused)",
             "us_per_block": us_block, "draft_tokens_per_s": B * k / (us_block * 1e-6),
-            "us_lm_head_gemm": us_gemm, "us_rollout_14_steps": us_rollout,
+            "us_lm_head": us_head, "lm_head_GBs": head_bytes / (us_head * 1e-6) / 1e9,
+            "lm_head_hbm_frac": head_bytes / (us_head * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "us_rollout_14_steps": us_rollout,
             "algorithmic_bytes": total, "GBs": total / (us_block * 1e-6) / 1e9,
             "hbm_frac": total / (us_block * 1e-6) / 1e9 / HBM_PEAK_GBS,
-            "fused_lm_head": {"kernel": "lm_head_kernel (position-0 argmax fused, hand-written)",
-                              "us_per_block": us_fblock, "us_lm_head": us_head,
-                              "lm_head_GBs": head_bytes / (us_head * 1e-6) / 1e9,
-                              "lm_head_hbm_frac": head_bytes / (us_head * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                              "algorithmic_bytes": ftotal,
-                              "hbm_frac": ftotal / (us_fblock * 1e-6) / 1e9 / HBM_PEAK_GBS}}
+            "library_lm_head": {"lm_head": "hipBLASLt through torch.mm + argmax_rows_kernel",
+                                "us_per_block": us_lblock, "us_lm_head_gemm": us_gemm,
+                                "lm_head_GBs": gemm_bytes / (us_gemm * 1e-6) / 1e9,
+                                "lm_head_hbm_frac": gemm_bytes / (us_gemm * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                                "algorithmic_bytes": ltotal,
+                                "hbm_frac": ltotal / (us_lblock * 1e-6) / 1e9 / HBM_PEAK_GBS}}
 
 
 def cpu_model() -> str:

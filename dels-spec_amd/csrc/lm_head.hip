@@ -6,40 +6,47 @@
 // Shape: M rows of hidden (a draft block's batch x k positions, about a
 // hundred) against W [V, K] (K = 4096, V = 151936: 1.245 GB of bf16).  At this
 // M the product is bound by streaming W from HBM once (about M FLOP per byte,
-// far under the MFMA ridge), so the kernel is built around that stream.  W is
-// packed once (dels_pack_lm_head) into MFMA-16 blocks in K-chunk-major order:
-// the 4 KiB of one 16-row tile in one K chunk (128 K) are contiguous, and so
-// are the tiles of one chunk, so that the whole GPU reads W as one sweep per
-// chunk (DRAM-page friendly) instead of thousands of 128 KiB-strided pieces.
-//   * one wave per SIMD, each owning 64 vocabulary columns at a time (four
-//     16-row tiles) for all 128 rows of its row group; W goes straight from
-//     HBM into registers, double-buffered by K chunk (register sets of 8 K
-//     steps of 16), the loads of the next chunk spread between the MFMAs of
-//     the current one (four sets were no faster: register pressure made the
-//     compiler wait for them early);
-//   * hidden, shared by every column, is staged through LDS in chunks of
-//     128 rows x 128 K (32 KiB, a ring of three), copied two chunks ahead by
-//     direct-to-LDS loads.  A CU returns its loads in issue order, so waiting
-//     for hidden chunk g+1 waits for every W load issued before it: issuing
-//     it two chunks ahead keeps the two youngest W chunks in flight through
-//     that wait (one ahead made every wait drain all but the newest W set);
-//   * v_mfma_f32_32x32x16_bf16: A = 32 rows x 16 K of hidden (one LDS KiB),
-//     B = 32 columns x 16 K of W gathered from two MFMA-16 blocks (two
-//     contiguous 512-byte runs per load); every LDS read feeds two MFMAs.
-// Accumulators: row 32 rb + 8 (j/4) + 4 (l/32) + j%4, column 32 cb + l%32.
-//
-// Epilogue of a pass (64 columns): the values are rounded to bf16 (as
-// nn.Linear's output) and staged through the wave's 4 KiB of LDS per 16
-// columns.  Rows m with argmax_period > 0 and m % argmax_period == 0 are argmax
-// rows: their bf16 values enter the argmax (lowest index on ties, the first
-// NaN wins, as torch.argmax) as 64-bit keys merged by LDS atomic maxima into
-// one key per row of the workgroup, and are not stored; every other row is
-// stored to `base` (16-byte stores) when it is given.  (A device-scope atomic
-// per tile here would make the wave wait for its returned value -- and so,
-// loads returning in order, for all of its W loads in flight -- at every
-// epilogue.)  At the end each workgroup merges its row keys into the global
-// ones; the last workgroup to finish decodes them and returns keys and
-// counter to zero.
+// far under the MFMA ridge), and on this GPU by what a CU can pull through its
+// L1 from L2 (about 25 GB/s per CU under a streaming load, ~6.5 TB/s over the
+// chip): every byte that reaches a CU counts, whether it comes from HBM or
+// from L2.  W (4.9 MB per CU) has to arrive once; hidden (1 MB per row group
+// of 128) arrives once per pass over a CU's columns.  So a workgroup keeps the
+// accumulators of ALL its columns at once -- one pass, hidden staged once per
+// CU -- where a pass of 256 columns staged it about three times (805 MB over
+// the chip against W's 1.245 GB).
+//   * W is packed once (dels_pack_lm_head) into MFMA-16 blocks in
+//     K-chunk-major order: the 4 KiB of one 16-row tile in one K chunk
+//     (128 K) are contiguous, and so are the tiles of one chunk, so that the
+//     whole GPU reads W as one sweep per chunk (DRAM-page friendly).
+//   * One workgroup per CU, eight waves (two per SIMD).  The workgroup's
+//     16-row vocabulary tiles are dealt to the waves (tile T0 + w + 8j to wave
+//     w), at most kLhNT = 5 per wave and pass: 8 row blocks x 5 tiles of 16x16
+//     fp32 accumulators = 160 registers.  At V = 151936 over 256 CUs a
+//     workgroup has 37-38 tiles, so one pass.
+//   * W goes from HBM into LDS by direct-to-LDS loads: one 1 KiB block per
+//     tile and K step of 32, already in v_mfma_f32_16x16x32_bf16's operand
+//     layout (lane l = vocabulary row l%16, K 8(l/16)..+7), into two step
+//     slots private to the wave; the loads of step t+1 are issued before the
+//     wait for step t, so one step of loads stays in flight through every
+//     wait.  (With the in-flight step in registers instead, 160 accumulators
+//     + two register sets left the compiler short of registers at two waves
+//     per SIMD: it spilled.)
+//   * hidden is staged through LDS by direct-to-LDS loads of whole 128-byte
+//     lines: a chunk is 128 rows x 128 K (32 KiB: [64-K half][row][16-byte
+//     slot], piece q of a row in slot q ^ (row % 8) so that the operand reads
+//     of 16 rows spread over the banks), a ring of two: the barrier that
+//     starts chunk g publishes it and frees the buffer of g-1, into which
+//     each wave then issues its four loads of chunk g+1.
+//   * D = W . hidden^T: lane l ends with hidden row l%16 and vocabulary rows
+//     4(l/16)..+3 of the tile, i.e. four consecutive logits of one row: one
+//     8-byte store.
+// Rows m with argmax_period > 0 and m % argmax_period == 0 are argmax rows:
+// their bf16 values enter the argmax (lowest index on ties, the first NaN
+// wins, as torch.argmax) as 64-bit keys, reduced over the wave's tiles in
+// registers and over the waves by LDS atomic maxima, and are not stored;
+// every other row is stored to `base` when it is given.  At the end each
+// workgroup merges its row keys into the global ones; the last workgroup to
+// finish decodes them and returns keys and counter to zero.
 #include <algorithm>
 
 #include "dels_device.h"
@@ -49,24 +56,25 @@ namespace dels {
 
 namespace {
 
-constexpr int kLhWaves = 4;                 // one per SIMD: two W sets and 128 accumulators
+constexpr int kLhWaves = 8;                          // two per SIMD
 constexpr int kLhThreads = kLhWaves * 64;
-constexpr int kLhRows = 128;                // rows per workgroup: 4 blocks of 32
-constexpr int kLhRB = kLhRows / 32;
-constexpr int kLhCB = 2;                    // 32-column blocks per wave and pass: each LDS read feeds two MFMAs
-constexpr int kLhKC = kLmHeadKChunk;       // 32-K blocks per chunk (8 MFMA K steps of 16)
-constexpr int kLhS = 2 * kLhKC;
-constexpr int kLhChunkBytes = kLhRB * kLhS * 1024;    // 32 KiB of hidden per chunk
-constexpr int kLhHLoads = kLhRB * kLhS / kLhWaves;    // 16-byte hidden loads per lane and chunk
-constexpr int kLhWLoads = kLhCB * kLhS;               // 16-byte W loads per lane and chunk
-constexpr int kLhRing = 3;                  // hidden chunks in LDS: in use, landed, in flight
+constexpr int kLhRows = 128;                         // rows per row group: 8 blocks of 16
+constexpr int kLhRB = kLhRows / 16;
+constexpr int kLhNT = 5;                             // 16-row vocabulary tiles per wave and pass
+constexpr int kLhTilesPerPass = kLhWaves * kLhNT;
+constexpr int kLhKC = kLmHeadKChunk;                 // 32-K blocks (K steps) per chunk
+constexpr int kLhChunkBytes = kLhRows * kLhKC * 64;  // 128 rows x 128 K of bf16 = 32 KiB
+constexpr int kLhHalfBytes = kLhRows * 128;          // one 64-K half of a chunk: a 128-byte line per row
+constexpr int kLhHLoads = kLhChunkBytes / 1024 / kLhWaves;   // direct-to-LDS loads per wave and chunk
+constexpr int kLhRing = 2;                           // hidden chunks in LDS: in use, in flight
+static_assert(kLhHLoads == kLhKC, "one hidden load per wave and K step");
 
 struct LmHeadArgs {
     const uint16_t* hidden; int64_t ldh;
-    const uint16_t* W;                      // [V, K] in MFMA-16 blocks
+    const uint16_t* W;                      // [V, K] in MFMA-16 blocks, K-chunk-major
     int M, K, V;
     uint16_t* base; int64_t ldo;            // bf16 output (nullptr: none)
-    bool vec_store;                         // base 16-byte aligned and ldo % 8 == 0
+    bool vec_store;                         // base 8-byte aligned and ldo % 4 == 0
     int argmax_period;                      // 0: no argmax rows
     int64_t* out_ids; float* out_score; int64_t ld_out;
     unsigned long long* keys; int64_t key_stride;
@@ -83,241 +91,242 @@ __device__ __forceinline__ unsigned long long lh_shfl_xor(unsigned long long x, 
     return ((unsigned long long)hi << 32) | lo;
 }
 
-typedef bf16x8 WSet[kLhCB][kLhS];
-
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding (its direct-to-LDS loads included, which the compiler does not
-// track) and its LDS operations are done, then the workgroup barrier.
+// track; they return in issue order).
 template <int N>
-__device__ __forceinline__ void lh_wait_barrier() {
+__device__ __forceinline__ void lh_wait_vm() {
     static_assert(N >= 0 && N < 64, "vmcnt out of range");
     asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0070 | 0x0f00);   // vmcnt(N) only
+    asm volatile("" ::: "memory");
+}
+
+// Workgroup barrier after this wave's LDS operations are done.
+__device__ __forceinline__ void lh_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
 
-__global__ __launch_bounds__(kLhThreads) void lm_head_kernel(LmHeadArgs a) {
-    __shared__ __attribute__((aligned(1024))) char ring[kLhRing][kLhChunkBytes];
-    __shared__ __attribute__((aligned(16))) uint16_t stage[kLhWaves][kLhRows * 16];
-    __shared__ int s_last;
-    __shared__ unsigned long long s_keys[kLhRows];   // argmax keys of the workgroup's rows
+struct LmHeadCtx {
+    const LmHeadArgs* a;
+    char (*ring)[kLhChunkBytes];            // hidden chunks
+    char* wslots;                           // this wave's two W step slots
+    unsigned long long* s_keys;
+    int lane, wave, row0, ntiles, nchunks, G;   // G: chunks of the walk (passes x chunks per pass)
+};
 
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int l32 = lane & 31, hk = lane >> 5;
-    const int row0 = blockIdx.y * kLhRows;
-    const int KB = a.K / 32;                 // 32-K blocks per 16-row tile of W
-    const int nchunks = KB / kLhKC;
+// Direct-to-LDS load j (0 .. kLhHLoads-1) of this wave for hidden chunk g
+// (K columns [c*128, c*128+128) with c = g % nchunks) into ring buffer g % 2.
+// Load i = wave * kLhHLoads + j of the chunk covers half i / 16, rows
+// 8 (i % 16) .. +7: lane l fetches row 8 (i % 16) + l/8, the piece that lands
+// in slot l % 8.  Rows past M repeat row M-1 (never stored).  Byte offsets fit
+// 32 bits (the hidden rows span less than 2 GiB, checked at launch).
+__device__ __forceinline__ void lh_issue_hidden(const LmHeadCtx& x, int g, int j) {
+    const LmHeadArgs& a = *x.a;
+    const int c = g % x.nchunks;
+    const int i = x.wave * kLhHLoads + j;
+    const int half = i >> 4;
+    const int row = 8 * (i & 15) + (x.lane >> 3);
+    const int q = (x.lane & 7) ^ (row & 7);
+    const int m = min(x.row0 + row, a.M - 1);
+    const uint32_t off = (uint32_t)(((int64_t)m * a.ldh + c * (kLhKC * 32) + half * 64 + q * 8) * 2);
+    dma16(a.hidden, off, x.ring[g % kLhRing] + i * 1024);
+}
 
-    // 16-row vocabulary tiles [T0, T1) of this workgroup, 16 per pass: in pass p
-    // wave w takes tiles T0 + 16p + 4w + i (slots i < 4; column block i / 2), so
-    // at every chunk the workgroup reads one contiguous run of W (16 tiles x
-    // 4 KiB in the K-chunk-major layout) and all workgroups together one
-    // contiguous range.  In a last, partial pass a column block whose tiles all
-    // lie past T1 skips its MFMAs.  (Dealing the slots round-robin over the
-    // waves, so that a partial pass has fewer live blocks per wave, measured
-    // 5 % slower.)
-    const int ntiles = (a.V + 15) / 16;
-    const int T0 = (int)(((int64_t)blockIdx.x * ntiles) / gridDim.x);
-    const int T1 = (int)(((int64_t)(blockIdx.x + 1) * ntiles) / gridDim.x);
-    constexpr int kTilesPerPass = 2 * kLhCB * kLhWaves;
-    const int npass = (T1 - T0 + kTilesPerPass - 1) / kTilesPerPass;
-    const int G = npass * nchunks;           // chunks of the walk, the same for every wave
+// One pass of a wave that owns NT tiles (tile j = tile0 + 8 j), chunks
+// [g0, g0 + nchunks) of the walk.  Every load is a direct-to-LDS load that the
+// compiler does not track: the waits below count them.
+template <int NT>
+__device__ __forceinline__ void lh_pass(const LmHeadCtx& x, int g0, int tile0) {
+    const LmHeadArgs& a = *x.a;
+    const int lane = x.lane, l16 = lane & 15, lq = lane >> 4;
 
-    // tile of slot i of this wave in pass p; past T1 it repeats the workgroup's last tile (L2 hits, results dropped)
-    auto tile16 = [&](int p, int i) {
-        const int x = T0 + p * kTilesPerPass + 2 * kLhCB * wave + i;
-        return x < T1 ? x : T1 - 1;
-    };
-    auto tile_live = [&](int p, int i) { return T0 + p * kTilesPerPass + 2 * kLhCB * wave + i < T1; };
-    auto kchunk = [&](int g) { return g % nchunks; };
-
-    // ---- hidden: chunk c = K blocks [c*KC, (c+1)*KC); LDS block (rb, s) holds the
-    // 32x16 A operand of row block rb and K step s in lane order (row l%32, K 16 s + 8 (l/32)).
-    // Chunk g of the walk goes to ring buffer g % 3 by kLhHLoads direct-to-LDS
-    // loads per lane (past the walk: its last chunk again); byte offsets fit
-    // 32 bits (the hidden rows span less than 2 GiB, checked at launch).
-    auto issue_hidden_one = [&](int g, int i) {
-        const int c = kchunk(g < G ? g : G - 1);
-        char* buf = ring[g % kLhRing];
-        const int j = wave * kLhHLoads + i;
-        const int rb = j / kLhS, s = j % kLhS;
-        const int row = min(row0 + rb * 32 + l32, a.M - 1);
-        const uint32_t off = (uint32_t)(((int64_t)row * a.ldh + c * (kLhKC * 32) + s * 16 + hk * 8) * 2);
-        dma16(a.hidden, off, buf + j * 1024);
-    };
-
-    // ---- W: the B operand of column block cb, K step s of chunk g: column 32 cb + l%32
-    // of the pass -> slot 2 cb + (l%32)/16, row l%16; K 16 s + 8 (l/32) -> 32-K block
-    // c*KC + s/2, lane (l%16) + 16 (2 (s%2) + l/32) of that 1 KiB block, which the
-    // K-chunk-major layout keeps at block ((c * ntiles + tile) * KC + s/2).
-    // Load q (0 <= q < kLhWLoads) of chunk g: column block q / kLhS, K step q % kLhS.
-    auto load_w_one = [&](int g, WSet& w, int q) {
-        const int gg = g < G ? g : G - 1;
-        const int p = gg / nchunks, c = kchunk(gg);
-        const int cb = q / kLhS, s = q % kLhS;
-        const int t = tile16(p, 2 * cb + (l32 >> 4));
-        const uint16_t* bp = a.W + ((int64_t)c * ntiles + t) * (kLhKC * 512) + ((l32 & 15) + 16 * hk) * 8;
-        w[cb][s] = load_bf16x8_nt(bp + (s >> 1) * 512 + (s & 1) * 256);
-    };
-
-    f32x16 acc[kLhRB][kLhCB];
+    f32x4 acc[kLhRB][NT > 0 ? NT : 1];
 #pragma unroll
     for (int rb = 0; rb < kLhRB; ++rb)
 #pragma unroll
-        for (int cb = 0; cb < kLhCB; ++cb)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) acc[rb][cb][j] = 0.f;
+        for (int j = 0; j < NT; ++j) acc[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Contraction of chunk g for the first NCB column blocks, with the loads of
-    // the step (W chunk gw into `ahead`, hidden chunk gh) spread between the
-    // MFMA slots k = (s * kLhRB + rb) * kLhCB + cb of 64: W load q at slot
-    // 4q + 1, hidden load i at slot 4i + 3, so the loads go out in the order
-    // W0 H0 W1 H1 .. W7 H7 W8 .. W15 whatever NCB is (a skipped column block
-    // keeps its slots, without the MFMA).  A operands (hidden) are read from
-    // LDS one K step ahead.
-    static_assert(kLhS * kLhRB * kLhCB == 64 && kLhWLoads == 16 && kLhHLoads == 8, "slot plan");
-    auto contract_issue = [&](auto ncb_tag, int g, const WSet& w, int gw, WSet& ahead, int gh) {
-        constexpr int NCB = decltype(ncb_tag)::value;
-        const char* buf = ring[g % kLhRing] + lane * 16;
-        bf16x8 hq[2][kLhRB];
-        if constexpr (NCB > 0) {
+    // W block of tile j at chunk c, K step s: ((c * ntiles + tile) * KC + s) KiB,
+    // copied to KiB j of the step's slot (lane l's 16 bytes at 16 l: the
+    // operand layout as it lies in memory).
+    auto issue_w = [&](int c, int s, int slot) {
 #pragma unroll
-            for (int rb = 0; rb < kLhRB; ++rb) hq[0][rb] = *reinterpret_cast<const bf16x8*>(buf + rb * kLhS * 1024);
-        }
-#pragma unroll
-        for (int s = 0; s < kLhS; ++s) {
-            if (NCB > 0 && s + 1 < kLhS) {
-#pragma unroll
-                for (int rb = 0; rb < kLhRB; ++rb)
-                    hq[(s + 1) & 1][rb] = *reinterpret_cast<const bf16x8*>(buf + (rb * kLhS + s + 1) * 1024);
-            }
-#pragma unroll
-            for (int rb = 0; rb < kLhRB; ++rb)
-#pragma unroll
-                for (int cb = 0; cb < kLhCB; ++cb) {
-                    const int k = (s * kLhRB + rb) * kLhCB + cb;
-                    __builtin_amdgcn_sched_barrier(0);
-                    if (cb < NCB)
-                        acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(hq[s & 1][rb], w[cb][s], acc[rb][cb],
-                                                                              0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                    if ((k & 3) == 1) load_w_one(gw, ahead, k >> 2);
-                    if ((k & 3) == 3 && (k >> 2) < kLhHLoads) issue_hidden_one(gh, k >> 2);
-                }
+        for (int j = 0; j < NT; ++j) {
+            const uint16_t* blk = a.W + ((int64_t)c * x.ntiles + tile0 + 8 * j) * (kLhKC * 512) + s * 512;
+            dma16(blk, (uint32_t)lane * 16u, x.wslots + slot * (kLhNT * 1024) + j * 1024);
         }
     };
 
-    // ---- epilogue of pass p, 16 columns (one tile) at a time through the wave's 4 KiB of LDS
-    uint16_t* stg = stage[wave];
-    auto epilogue = [&](int p) {
+    // K step s of chunk g with the W blocks of slot `slot`: B operand = 16
+    // hidden rows x 32 K from the ring (row 16 rb + l%16, K 32 s + 8 (l/16):
+    // half s/2, piece 4 (s%2) + l/16).
+    auto contract = [&](int g, int s, int slot) {
+        if constexpr (NT > 0) {
+            bf16x8 w[NT];
 #pragma unroll
-        for (int cb = 0; cb < kLhCB; ++cb) {
+            for (int j = 0; j < NT; ++j)
+                w[j] = *reinterpret_cast<const bf16x8*>(x.wslots + slot * (kLhNT * 1024) + j * 1024 + lane * 16);
+            const char* buf = x.ring[g % kLhRing] + (s >> 1) * kLhHalfBytes;
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int i = 2 * cb + half;          // slot of the pass
-                if ((l32 >> 4) == half) {
+            for (int rb = 0; rb < kLhRB; ++rb) {
+                const int row = rb * 16 + l16;
+                const int q = (((s & 1) << 2) | lq) ^ (row & 7);
+                const bf16x8 hb = *reinterpret_cast<const bf16x8*>(buf + row * 128 + q * 16);
 #pragma unroll
-                    for (int rb = 0; rb < kLhRB; ++rb)
-#pragma unroll
-                        for (int j = 0; j < 16; ++j)
-                            stg[(rb * 32 + 8 * (j >> 2) + 4 * hk + (j & 3)) * 16 + (l32 & 15)] =
-                                f32_to_bf16_bits(acc[rb][cb][j]);
-                }
-                if (half == 1) {
-#pragma unroll
-                    for (int rb = 0; rb < kLhRB; ++rb)
-#pragma unroll
-                        for (int j = 0; j < 16; ++j) acc[rb][cb][j] = 0.f;
-                }
-                if (!tile_live(p, i)) continue;       // wave-uniform
-                const int v0 = tile16(p, i) * 16;
-                const int vend = min(a.V, v0 + 16);
-                if (a.base != nullptr) {
-                    for (int q = lane; q < kLhRows * 2; q += 64) {
-                        const int r = q >> 1, c8 = (q & 1) * 8;
-                        const int m = row0 + r;
-                        if (m >= a.M || v0 + c8 >= vend || (a.argmax_period > 0 && m % a.argmax_period == 0)) continue;
-                        uint16_t* dst = a.base + (int64_t)m * a.ldo + v0 + c8;
-                        if (a.vec_store && v0 + c8 + 8 <= vend) {
-                            *reinterpret_cast<u32x4*>(dst) = *reinterpret_cast<const u32x4*>(stg + r * 16 + c8);
-                        } else {
-                            for (int e = 0; e < 8 && v0 + c8 + e < vend; ++e) dst[e] = stg[r * 16 + c8 + e];
-                        }
-                    }
-                }
-                if (a.argmax_period > 0) {
-                    // argmax rows m = j * period of this row group, four per round (16 lanes each)
-                    const int j0 = (row0 + a.argmax_period - 1) / a.argmax_period;
-                    const int mend = min(row0 + kLhRows, a.M);
-                    const int c16 = lane & 15, q4 = lane >> 4;
-                    for (int jb = j0; jb * a.argmax_period < mend; jb += 4) {
-                        const int jr = jb + q4;
-                        const int m = jr * a.argmax_period;
-                        const int v = v0 + c16;
-                        unsigned long long key = 0ull;
-                        if (m < mend && v < vend) key = lh_key(bf16_bits_to_f32(stg[(m - row0) * 16 + c16]), (uint32_t)v);
-#pragma unroll
-                        for (int off = 1; off < 16; off <<= 1) {
-                            const unsigned long long o = lh_shfl_xor(key, off);
-                            key = o > key ? o : key;
-                        }
-                        if (c16 == 0 && key != 0ull)
-                            __hip_atomic_fetch_max(&s_keys[m - row0], key, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_WORKGROUP);
-                    }
-                }
+                for (int j = 0; j < NT; ++j)
+                    acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w[j], hb, acc[rb][j], 0, 0, 0);
             }
         }
     };
 
-    // ---- walk over chunks g = p * nchunks + c: chunk g uses W set g % 2 and
-    // hidden buffer g % 3.  Step g contracts chunk g while it issues the W
-    // loads of g+1 (unconditionally: past the walk they reload its last chunk)
-    // and the hidden loads of g+2, then waits for hidden g+1 and synchronises
-    // the workgroup.  Every step issues the same loads in the same order, so at
-    // its end exactly kAfter loads are younger than the last load of hidden
-    // g+1 (the 8 W loads that follow it in the previous step and the 24 of this
-    // one; epilogue stores only add to them): waiting for vmcnt(kAfter) lands
-    // g+1 and leaves those in flight.  The prologue issues the loads of the two
-    // steps before step 0.  nchunks is even, so both steps of a loop turn
-    // belong to one pass; the epilogue of a pass runs between passes.
-    constexpr int kAfter = (kLhWLoads - kLhHLoads) + kLhWLoads + kLhHLoads;
-    static_assert(kAfter < 64, "vmcnt range");
+    // Step (g, s): W of the next step into the other slot (whose reads, by the
+    // previous step, are done); wait for this step's W -- in issue order, so
+    // everything older has landed too (the hidden loads of chunk g among
+    // them); at s == 0 the barrier that publishes hidden chunk g and frees the
+    // buffer of g-1, and the loads of chunk g+1 into it; then the MFMAs.
+    // Younger than this step's W at the wait: the next step's NT loads
+    // (unless LAST) and, at s == 1, the kLhHLoads hidden loads of step s == 0.
+    auto step = [&](auto last_tag, int g, int s) {
+        constexpr bool LAST = decltype(last_tag)::value;
+        const int c = g % x.nchunks;
+        if constexpr (!LAST) {
+            if (s + 1 < kLhKC) issue_w(c, s + 1, (s + 1) & 1);
+            else issue_w(c + 1, 0, 0);
+        }
+        constexpr int N = LAST ? 0 : NT;
+        if (s == 1 && g + 1 < x.G) lh_wait_vm<N + kLhHLoads>();
+        else lh_wait_vm<N>();
+        if (s == 0) {
+            lh_barrier();
+            if (g + 1 < x.G) {
+#pragma unroll
+                for (int j = 0; j < kLhHLoads; ++j) lh_issue_hidden(x, g + 1, j);
+            }
+        }
+        contract(g, s, s & 1);
+    };
+
+    issue_w(0, 0, 0);
+    const int g1 = g0 + x.nchunks - 1;    // last chunk of the pass: its last step prefetches nothing
+    for (int g = g0; g < g1; ++g) {
+        step(std::false_type{}, g, 0);
+        step(std::false_type{}, g, 1);
+        step(std::false_type{}, g, 2);
+        step(std::false_type{}, g, 3);
+    }
+    step(std::false_type{}, g1, 0);
+    step(std::false_type{}, g1, 1);
+    step(std::false_type{}, g1, 2);
+    step(std::true_type{}, g1, 3);
+    static_assert(kLhKC == 4, "four K steps per chunk, two W slots");
+
+    // Epilogue: lane l holds D[vocabulary 16 tile + 4 (l/16) + e][row 16 rb + l%16].
+    // (Its lane and row values pass through empty asm statements here, so that
+    // the compiler cannot compute the store addresses before the K loop and
+    // hold them in registers across it.)
+    if constexpr (NT > 0) {
+        const bool any_argmax = a.argmax_period > 0;
+        int e16 = l16, eq = lq, erow0 = x.row0;
+        asm volatile("" : "+v"(e16), "+v"(eq), "+s"(erow0));
+#pragma unroll
+        for (int rb = 0; rb < kLhRB; ++rb) {
+            const int m = erow0 + rb * 16 + e16;
+            const bool argmax_row = any_argmax && m % a.argmax_period == 0;
+            unsigned long long key = 0ull;
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+                const int v = (tile0 + 8 * j) * 16 + 4 * eq;
+                float r[4];
+                uint32_t bits[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    bits[e] = f32_to_bf16_bits(acc[rb][j][e]);
+                    r[e] = bf16_bits_to_f32(bits[e]);
+                }
+                if (argmax_row) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const unsigned long long k = v + e < a.V ? lh_key(r[e], (uint32_t)(v + e)) : 0ull;
+                        key = k > key ? k : key;
+                    }
+                } else if (a.base != nullptr && m < a.M) {
+                    uint16_t* dst = a.base + (int64_t)m * a.ldo + v;
+                    if (a.vec_store && v + 4 <= a.V) {
+                        *reinterpret_cast<u32x2*>(dst) = u32x2{bits[0] | (bits[1] << 16), bits[2] | (bits[3] << 16)};
+                    } else {
+                        for (int e = 0; e < 4 && v + e < a.V; ++e) dst[e] = (uint16_t)bits[e];
+                    }
+                }
+            }
+            if (any_argmax) {
+                // over the four lanes that hold row m (l/16 = 0..3), then one LDS maximum per row
+                key = max(key, lh_shfl_xor(key, 16));
+                key = max(key, lh_shfl_xor(key, 32));
+                if (eq == 0 && argmax_row && m < a.M && key != 0ull)
+                    __hip_atomic_fetch_max(&x.s_keys[rb * 16 + e16], key, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_WORKGROUP);
+            }
+        }
+    }
+}
+
+__global__ __launch_bounds__(kLhThreads) void lm_head_kernel(LmHeadArgs a) {
+    __shared__ __attribute__((aligned(1024))) char ring[kLhRing][kLhChunkBytes];
+    __shared__ __attribute__((aligned(1024))) char wbuf[kLhWaves][2 * kLhNT * 1024];
+    __shared__ int s_last;
+    __shared__ unsigned long long s_keys[kLhRows];   // argmax keys of the workgroup's rows
+
+    LmHeadCtx x;
+    x.a = &a;
+    x.ring = ring;
+    x.s_keys = s_keys;
+    x.wslots = wbuf[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6)];
+    x.lane = threadIdx.x & 63;
+    x.wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    x.row0 = blockIdx.y * kLhRows;
+    x.ntiles = (a.V + 15) / 16;
+    x.nchunks = a.K / (kLhKC * 32);
+
+    // 16-row vocabulary tiles [T0, T1) of this workgroup, up to 40 per pass:
+    // in pass p wave w owns tiles T0 + 40 p + w + 8 j.
+    const int T0 = (int)(((int64_t)blockIdx.x * x.ntiles) / gridDim.x);
+    const int T1 = (int)(((int64_t)(blockIdx.x + 1) * x.ntiles) / gridDim.x);
+    const int npass = (T1 - T0 + kLhTilesPerPass - 1) / kLhTilesPerPass;
+    x.G = npass * x.nchunks;
+
     for (int r = threadIdx.x; r < kLhRows; r += kLhThreads) s_keys[r] = 0ull;   // published by the first barrier
-    WSet wa, wb;
+    // hidden chunk 0 (chunk g+1 is issued at the start of chunk g)
 #pragma unroll
-    for (int i = 0; i < kLhHLoads; ++i) issue_hidden_one(0, i);
-#pragma unroll
-    for (int q = 0; q < kLhWLoads; ++q) {
-        load_w_one(0, wa, q);
-        if (q < kLhHLoads) issue_hidden_one(1, q);
-    }
-    lh_wait_barrier<kLhWLoads + kLhHLoads>();               // hidden 0 landed
-    auto step = [&](int g, const WSet& cur, WSet& ahead) {
-        const int p = g / nchunks;                          // wave-uniform
-        if (tile_live(p, 2)) contract_issue(std::integral_constant<int, 2>{}, g, cur, g + 1, ahead, g + 2);
-        else if (tile_live(p, 0)) contract_issue(std::integral_constant<int, 1>{}, g, cur, g + 1, ahead, g + 2);
-        else contract_issue(std::integral_constant<int, 0>{}, g, cur, g + 1, ahead, g + 2);
-        lh_wait_barrier<kAfter>();                          // hidden g+1 landed everywhere
-    };
+    for (int j = 0; j < kLhHLoads; ++j) lh_issue_hidden(x, 0, j);
+
     for (int p = 0; p < npass; ++p) {
-        for (int c = 0; c < nchunks; c += 2) {
-            step(p * nchunks + c, wa, wb);
-            step(p * nchunks + c + 1, wb, wa);
+        const int first = T0 + p * kLhTilesPerPass;
+        const int n = min(kLhTilesPerPass, T1 - first);
+        const int nt = n > x.wave ? min(kLhNT, (n - x.wave + kLhWaves - 1) / kLhWaves) : 0;   // wave-uniform
+        const int tile0 = first + x.wave;
+        const int g0 = p * x.nchunks;
+        switch (nt) {
+            case 5: lh_pass<5>(x, g0, tile0); break;
+            case 4: lh_pass<4>(x, g0, tile0); break;
+            case 3: lh_pass<3>(x, g0, tile0); break;
+            case 2: lh_pass<2>(x, g0, tile0); break;
+            case 1: lh_pass<1>(x, g0, tile0); break;
+            default: lh_pass<0>(x, g0, tile0); break;
         }
-        epilogue(p);
     }
-    // the reloads past the walk are still in flight: no direct-to-LDS write may
-    // outlive the workgroup
+    static_assert(kLhNT == 5, "the switch covers 0 .. kLhNT tiles");
+    // every direct-to-LDS write has landed before the workgroup's LDS is reused or released
     __builtin_amdgcn_s_waitcnt(0x0070 | (0xf << 8));   // vmcnt(0)
 
     if (a.argmax_period <= 0) return;
     __syncthreads();   // every wave's LDS maxima are in s_keys
     unsigned long long seen = 0;
     for (int r = threadIdx.x; r < kLhRows; r += kLhThreads) {
-        const int m = row0 + r;
+        const int m = x.row0 + r;
         const unsigned long long key = s_keys[r];
         if (m < a.M && m % a.argmax_period == 0 && key != 0ull)
             seen |= __hip_atomic_fetch_max(&a.keys[(int64_t)(m / a.argmax_period) * a.key_stride], key,
@@ -354,7 +363,7 @@ __global__ __launch_bounds__(kLhThreads) void lm_head_kernel(LmHeadArgs a) {
 
 bool lm_head_supported(int64_t M, int64_t K, int64_t V, int64_t argmax_period) {
     if (M < 1 || M > (int64_t)kLhRows * 64 || V < 1 || V >= INT32_MAX) return false;
-    if (K < 1 || K >= (int64_t(1) << 26) || K % (64 * kLhKC) != 0) return false;   // an even chunk count
+    if (K < 1 || K >= (int64_t(1) << 26) || K % 256 != 0) return false;
     if (argmax_period < 0 || argmax_period >= (int64_t(1) << 24)) return false;
     return argmax_period == 0 || (M - 1) / argmax_period + 1 <= kMaxKeyRows;
 }
@@ -368,7 +377,7 @@ hipError_t launch_lm_head(const void* hidden, int64_t ldh, const void* W, int M,
     a.W = static_cast<const uint16_t*>(W);
     a.M = M; a.K = K; a.V = V;
     a.base = static_cast<uint16_t*>(base); a.ldo = ldo;
-    a.vec_store = (reinterpret_cast<uintptr_t>(base) & 15) == 0 && ldo % 8 == 0;
+    a.vec_store = (reinterpret_cast<uintptr_t>(base) & 7) == 0 && ldo % 4 == 0;
     a.argmax_period = argmax_period;
     a.out_ids = out_ids; a.out_score = out_score; a.ld_out = ld_out;
     a.counter = reinterpret_cast<unsigned int*>(w + kCountersOff);
@@ -377,7 +386,9 @@ hipError_t launch_lm_head(const void* hidden, int64_t ldh, const void* W, int M,
     a.key_stride = (int64_t)nrows * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
     const int groups = (M + kLhRows - 1) / kLhRows;
     const int ntiles = (V + 15) / 16;
-    const int gx = std::max(1, std::min(ntiles, device_cu_count() / groups));
+    // one workgroup per CU, at least two tiles per wave where the vocabulary allows
+    const int gx = std::max(1, std::min((ntiles + 2 * kLhWaves - 1) / (2 * kLhWaves),
+                                        std::max(1, device_cu_count() / groups)));
     hipLaunchKernelGGL(lm_head_kernel, dim3(gx, groups, 1), dim3(kLhThreads), 0, s, a);
     return hipGetLastError();
 }

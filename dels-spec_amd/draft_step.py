@@ -6,13 +6,15 @@ The graph path of ``spec_generate`` for one block (code/dflash.py:452-486):
     verify_ids[:, 1] = sample(base_logits[:, :1])             # plain argmax of position 0
     verify_ids[:, 2:k+1] = graph_runner(verify_ids[:, 1:2], base_logits[:, 1:k])
 
-The LM head and the first-position argmax are either (``lm_head="library"``,
-the default) a plain library GEMM (``torch.mm`` -> hipBLASLt, as ``nn.Linear``
-in the reference) followed by ``dels_argmax_rows``, or (``lm_head="fused"``) one
-launch of the hand-written ``dels_lm_head`` (W packed once, streamed from HBM
-once, the position-0 rows argmaxed inside the GEMM and never stored; hidden
-size a multiple of 256).  On the MI355X the library GEMM is faster at this
-shape (batch 8, block 16: 284 us against about 345 us), hence the default.
+The LM head and the first-position argmax are either (``lm_head="fused"``, the
+default wherever the shape allows it: hidden size a multiple of 256, batch * k
+<= 8192) one launch of the hand-written ``dels_lm_head`` (W packed once,
+streamed from HBM once, the position-0 rows argmaxed inside the GEMM and never
+stored), or (``lm_head="library"``) a plain library GEMM (``torch.mm`` ->
+hipBLASLt, as ``nn.Linear`` in the reference) followed by ``dels_argmax_rows``.
+On the MI355X the hand-written head is the faster one at the bench shape
+(batch 8, block 16, d 4096, V 151936: 226 us against 286 us for the library
+GEMM).  ``lm_head="auto"`` picks ``fused`` where it applies, else ``library``.
 The suffix rollout is ``dels_rollout_enqueue`` over the runner's packed
 weights, reading ``base_logits[:, 1:k]`` in place (row stride k * V).  All of
 it is captured once into one graph and replayed per block.
@@ -43,9 +45,9 @@ class DeLSDraftStep:
 
     def __init__(self, *, local_head, lm_head_weight: torch.Tensor, batch_size: int, k_draft: int,
                  vocab_size: int, alpha_values: list[float], beta_values: list[float],
-                 baseline_logits: Optional[torch.Tensor], device: torch.device, lm_head: str = "library"):
-        if lm_head not in ("library", "fused"):
-            raise ValueError(f"lm_head must be 'library' or 'fused', got {lm_head!r}")
+                 baseline_logits: Optional[torch.Tensor], device: torch.device, lm_head: str = "auto"):
+        if lm_head not in ("auto", "library", "fused"):
+            raise ValueError(f"lm_head must be 'auto', 'library' or 'fused', got {lm_head!r}")
         if k_draft < 2:
             raise ValueError(f"DeLSDraftStep needs k_draft >= 2 (at least one DeLS step), got {k_draft}.")
         self.runner = DeLSGraphRunner(local_head=local_head, batch_size=batch_size, steps=k_draft - 1,
@@ -60,8 +62,11 @@ class DeLSDraftStep:
         self.lm_head_weight = W.contiguous()
         d = int(W.shape[1])
         lib = _lib.load()
+        fused_ok = d % 256 == 0 and B * k <= 8192
+        if lm_head == "auto":
+            lm_head = "fused" if fused_ok else "library"
         self._fused_head = lm_head == "fused"
-        if self._fused_head and (d % 256 != 0 or B * k > 8192):
+        if self._fused_head and not fused_ok:
             raise ValueError("lm_head='fused' needs a hidden size that is a multiple of 256 and batch * k <= 8192")
         self._w_p = pack_lm_head(self.lm_head_weight) if self._fused_head else None
         self.batch_size, self.k_draft, self.vocab_size, self.hidden_size = B, k, V, d

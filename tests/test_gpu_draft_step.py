@@ -163,3 +163,28 @@ def test_draft_step_full_size(pkg, dev, lm_head):
     assert res["score_bad"] == 0, res
     step.close()
 
+
+
+def test_default_lm_head_is_the_hand_written_one_where_it_applies(pkg, dev):
+    """lm_head="auto" (the default) takes the hand-written LM head when the hidden size is
+    a multiple of 256, the library GEMM otherwise; both give the same first ids here."""
+    V = 5003
+    head = _Head(V, 32, 64, 64, "silu", False, seed=5, std=0.2).to(dev)
+    g = torch.Generator().manual_seed(11)
+    firsts = []
+    for d, fused in ((256, True), (200, False)):
+        print(f"case draft_step default lm_head d={d}", flush=True)
+        W = (torch.randn(V, d, generator=g) * 0.05).bfloat16()
+        st = pkg.DeLSDraftStep(local_head=head, lm_head_weight=W.to(dev), batch_size=2, k_draft=3, vocab_size=V,
+                               alpha_values=[0.1, 0.2], beta_values=[0.0, 0.0], baseline_logits=None, device=dev)
+        assert st._fused_head is fused
+        hid = torch.randn(2, 3, d, generator=g).bfloat16()
+        out = st(hid.to(dev))
+        torch.cuda.synchronize()
+        ref = (hid.float().reshape(6, d) @ W.float().T).reshape(2, 3, V)[:, 0]
+        firsts.append((out[:, 0].cpu(), ref))
+        st.close()
+    for got, ref in firsts:
+        top2 = torch.topk(ref, 2, dim=-1).values
+        pinned = (top2[:, 0] - top2[:, 1]) > 0.05 * top2[:, 0].abs()
+        assert torch.equal(got[pinned], torch.argmax(ref, dim=-1)[pinned])
