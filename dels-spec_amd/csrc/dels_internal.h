@@ -47,7 +47,8 @@ constexpr size_t kDataOff = kDecodeOff + kDecodeWordBytes;
 constexpr int kRankTiledMinRows = 64;
 
 struct SkinnyPlan {
-    bool tiled;        // rank projection by the LDS-tiled 64 x 64 kernel (many rows)
+    bool tiled;        // rank projection by the LDS-tiled kernel (many rows)
+    int tm, tn;        // its output tile (rows x cols)
     int wm, wn;        // 16x16 MFMA sub-tiles per wave (rows x cols)
     int m_wg, n_wg;    // workgroup grid (row tiles, col tiles)
     int ksplit;        // workgroups sharing one output tile along K

@@ -308,29 +308,38 @@ __global__ __launch_bounds__(256) void skinny_gemm_kernel(SkinnyKArgs a) {
 // The skinny kernel reads its operands straight from global memory, each
 // wave's load touching 32 B of 32 different rows; at M = 512 that re-reads h
 // and A sixteen times over through the caches and is latency bound (16 us at
-// the Qwen3-8B shape).  Here a workgroup owns a 64 x 64 output tile and a
-// range of 64-deep K chunks.  Each chunk's 64 x 64 slices of h and of A are
-// copied HBM -> LDS with direct-to-LDS loads of whole 128-byte lines (eight
-// rows per instruction), into a ring of kRgStages chunk buffers, so that
-// kRgStages - 1 chunks of loads are in flight; its four waves each contract a
-// 32 x 32 quadrant with v_mfma_f32_32x32x16_bf16 from LDS.  The 16-byte
-// pieces of a row are stored XOR-swizzled by row (piece q of row r in slot
-// q ^ (r % 8)), so the operand reads of 32 rows spread over all LDS banks.
-// K is split over 8 workgroups per tile so that the grid covers the device;
-// their fp32 partials go to the workspace with plain stores and a second
-// kernel sums them in split order (deterministic) and runs the epilogue.
+// the Qwen3-8B shape).  Here a workgroup owns a TM x TN output tile and a
+// range of 64-deep K chunks.  Each chunk's slices of h (TM rows) and of A (TN
+// rows) are copied HBM -> LDS with direct-to-LDS loads of whole 128-byte
+// lines (eight rows per instruction), into a ring of kRgStages chunk
+// buffers, so that kRgStages - 1 chunks of loads are in flight; each of its
+// (TM/32)(TN/32) waves contracts one 32 x 32 quadrant with
+// v_mfma_f32_32x32x16_bf16 from LDS.  The 16-byte pieces of a row are stored
+// XOR-swizzled by row (piece q of row r in slot q ^ (r % 8)), so the operand
+// reads of 32 rows spread over all LDS banks.
+// What bounds it is what the CUs pull from L2 (about 25 GB/s per CU under
+// load): each workgroup pulls (TM + TN) x its K range of operand bytes, so
+// bigger tiles pull less in total -- (M N K)(1/TM + 1/TN) -- but leave fewer
+// tiles, so K is split over more workgroups (ksplit) to cover the device and
+// the fp32 partials grow (ksplit x M x N x 4 bytes, written here, read by the
+// epilogue kernel).  The plan picks the shape.  The partials go to the
+// workspace with plain stores and a second kernel sums them in split order
+// (deterministic) and runs the epilogue.
 // Needs K % 64 == 0 and r % 8 == 0 (the plan falls back to the skinny kernel otherwise).
 // ---------------------------------------------------------------------------
 
-constexpr int kRgTile = 64;                 // output tile edge
 constexpr int kRgChunk = 64;                // K per LDS chunk
-constexpr int kRgStages = 4;                // chunk buffers in the LDS ring (two workgroups fit a CU)
+constexpr int kRgStages = 4;                // chunk buffers in the LDS ring
 
-// Direct-to-LDS loads per wave and chunk: h (8 instructions of 8 rows) and W
-// (row-major: 8 like h; MFMA-16 blocks: 8 of 1 KiB; e4m3 blocks: 16 of 256 B),
-// spread over the 4 waves.
-template <int WMODE>
-constexpr int rg_loads_per_wave() { return (8 + (WMODE == W_PACKED_E4M3 ? 16 : 8)) / 4; }
+// Direct-to-LDS loads per wave and chunk: h (TM/8 instructions of 8 rows) and
+// A (row-major: TN/8 like h; MFMA-16 blocks: TN/8 of 1 KiB; e4m3 blocks:
+// TN/4 of 256 B), spread over the (TM/32)(TN/32) waves.
+template <int WMODE, int TM, int TN>
+constexpr int rg_loads_per_wave() {
+    return (TM / 8 + (WMODE == W_PACKED_E4M3 ? TN / 4 : TN / 8)) / ((TM / 32) * (TN / 32));
+}
+template <int TM, int TN>
+constexpr int rg_threads() { return (TM / 32) * (TN / 32) * 64; }
 
 template <int N>
 __device__ __forceinline__ void rg_wait_barrier() {
@@ -341,63 +350,68 @@ __device__ __forceinline__ void rg_wait_barrier() {
     asm volatile("" ::: "memory");
 }
 
-template <int WMODE>
-__global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
-    constexpr int L = rg_loads_per_wave<WMODE>();
-    constexpr int kWBytes = WMODE == W_PACKED_E4M3 ? 4096 : 8192;
+template <int WMODE, int TM, int TN>
+__global__ __launch_bounds__((TM / 32) * (TN / 32) * 64) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
+    constexpr int kThreads = rg_threads<TM, TN>();
+    constexpr int kWaves = kThreads / 64;
+    constexpr int kHLoads = TM / 8;
+    constexpr int kWLoads = WMODE == W_PACKED_E4M3 ? TN / 4 : TN / 8;
+    constexpr int L = rg_loads_per_wave<WMODE, TM, TN>();
+    static_assert(L * kWaves == kHLoads + kWLoads, "loads must spread evenly over the waves");
+    constexpr int kWBytes = WMODE == W_PACKED_E4M3 ? TN * 64 : TN * 128;
     struct __attribute__((aligned(1024))) Chunk {
-        char h[8192];        // 64 rows x 128 B, pieces swizzled
-        char w[kWBytes];     // row-major: as h; blocked: 8 blocks (4 row blocks x 2 K blocks)
+        char h[TM * 128];    // TM rows x 128 B, pieces swizzled
+        char w[kWBytes];     // row-major: as h; blocked: (TN/16) row blocks x 2 K blocks
     };
     __shared__ Chunk ring[kRgStages];
-    // the output tile (pitch 68 floats) reuses the ring once the K loop is done
-    static_assert(sizeof(Chunk) * kRgStages >= kRgTile * (kRgTile + 4) * sizeof(float), "ring too small");
+    // the output tile (pitch TN + 4 floats) reuses the ring once the K loop is done
+    static_assert(sizeof(Chunk) * kRgStages >= TM * (TN + 4) * sizeof(float), "ring too small");
     float* red = reinterpret_cast<float*>(&ring[0]);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;    // quadrant of this wave
+    const int wm = wave / (TN / 32), wn = wave % (TN / 32);    // quadrant of this wave
     // Grid (ksplit, column tiles, row tiles): consecutive workgroups -- which
     // the dispatcher deals round-robin over the 8 XCDs -- take different K
-    // splits, so with ksplit = 8 each XCD works on one K slice of h and A and
-    // its L2 fetches that slice once instead of all of h and A.
+    // splits, so each XCD works on ksplit/8 K slices of h and A and its L2
+    // fetches those slices once instead of all of h and A.
     const int z = blockIdx.x;
-    const int n0 = blockIdx.y * kRgTile, m0 = blockIdx.z * kRgTile;
+    const int n0 = blockIdx.y * TN, m0 = blockIdx.z * TM;
     const int nchunks = a.K / kRgChunk;
     const int cps = (nchunks + a.ksplit - 1) / a.ksplit;
     const int c0 = z * cps, c1 = min(nchunks, c0 + cps);
     const int nch = max(0, c1 - c0);
 
-    // Load instruction g (0 .. 4L-1) of chunk c into slot S: g < 8 is h
-    // (rows 8g .. 8g+7), the rest W.  Rows past M or r repeat the last row
-    // (their results are never stored).
-    // Byte offsets are taken from the tile's first row (or row block), so they
-    // stay far below 2^32 whatever the matrix size.
+    // Load instruction g (0 .. kHLoads + kWLoads - 1) of chunk c into slot S:
+    // g < kHLoads is h (rows 8g .. 8g+7), the rest A.  Rows past M or r repeat
+    // the last row (their results are never stored).  Byte offsets are taken
+    // from the tile's first row (or row block), so they stay far below 2^32
+    // whatever the matrix size.
     const int prow = lane >> 3, piece = lane & 7;
     const uint16_t* hbase = a.x + (int64_t)m0 * a.ldx;
-    const int nbw = (n0 >> 4);   // first row block of W (blocked layouts)
+    const int nbw = (n0 >> 4);   // first row block of A (blocked layouts)
     const uint16_t* wbase = WMODE == W_ROWMAJOR ? a.w + (int64_t)n0 * a.ldw
                           : a.w + (int64_t)nbw * a.ksteps * (WMODE == W_PACKED ? 512 : 256);
     const int nbl = (a.wrows + 15) / 16 - 1 - nbw;   // last row block, relative to nbw
     auto issue = [&](int c, Chunk& S, int g) {
         const int k0 = c * kRgChunk;
-        if (g < 8) {
+        if (g < kHLoads) {
             const int row = 8 * g + prow;
             const int mr = min(m0 + row, a.M - 1) - m0;
             const int q = piece ^ (row & 7);   // the piece this lane fetches: slot `piece` holds piece q
             dma16(hbase, (uint32_t)(mr * a.ldx + k0 + 8 * q) * 2u, S.h + g * 1024);
         } else if constexpr (WMODE == W_ROWMAJOR) {
-            const int row = 8 * (g - 8) + prow;
+            const int row = 8 * (g - kHLoads) + prow;
             const int nr = min(n0 + row, a.wrows - 1) - n0;
             const int q = piece ^ (row & 7);
-            dma16(wbase, (uint32_t)(nr * a.ldw + k0 + 8 * q) * 2u, S.w + (g - 8) * 1024);
+            dma16(wbase, (uint32_t)(nr * a.ldw + k0 + 8 * q) * 2u, S.w + (g - kHLoads) * 1024);
         } else if constexpr (WMODE == W_PACKED) {
-            const int b = g - 8;                      // block (row block b/2, K block b%2)
+            const int b = g - kHLoads;                // block (row block b/2, K block b%2)
             const int blk = min(b >> 1, nbl) * a.ksteps + (k0 >> 5) + (b & 1);
             dma16(wbase, (uint32_t)(blk * 1024 + lane * 16), S.w + b * 1024);
         } else {
-            const int b = (g - 8) >> 1, half = (g - 8) & 1;   // 512-byte e4m3 blocks, two 256-byte halves
+            const int b = (g - kHLoads) >> 1, half = (g - kHLoads) & 1;   // 512-byte e4m3 blocks, two halves
             const int blk = min(b >> 1, nbl) * a.ksteps + (k0 >> 5) + (b & 1);
             dma4(wbase, (uint32_t)(blk * 512 + half * 256 + lane * 4), S.w + b * 512 + half * 256);
         }
@@ -459,12 +473,13 @@ __global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
         }
     }
 
-    // the quadrant into the tile red[m][n] (pitch 68 floats)
+    // the quadrant into the tile red[m][n] (pitch TN + 4 floats)
+    constexpr int kPitch = TN + 4;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int m = 32 * wm + 8 * (i >> 2) + 4 * kh + (i & 3);
-        red[m * (kRgTile + 4) + 32 * wn + rl] = acc[i];
+        red[m * kPitch + 32 * wn + rl] = acc[i];
     }
     __syncthreads();
 
@@ -474,11 +489,11 @@ __global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
         // stream, sums the splits in order (the kernel boundary makes every
         // partial visible to it) and runs the epilogue.
         float* mine = a.partial + (int64_t)z * a.M * a.ncols;
-        for (int e = tid; e < kRgTile * kRgTile / 4; e += 256) {
-            const int mm = e >> 4, nn = 4 * (e & 15);
+        for (int e = tid; e < TM * TN / 4; e += kThreads) {
+            const int mm = e / (TN / 4), nn = 4 * (e % (TN / 4));
             const int m = m0 + mm, n = n0 + nn;
             if (m >= a.M || n >= a.ncols) continue;
-            const float* src = &red[mm * (kRgTile + 4) + nn];
+            const float* src = &red[mm * kPitch + nn];
             // ncols is a multiple of 8, so the 4 columns are in range
             *reinterpret_cast<f32x4*>(mine + (int64_t)m * a.ncols + n) = f32x4{src[0], src[1], src[2], src[3]};
         }
@@ -488,14 +503,14 @@ __global__ __launch_bounds__(256) void rank_gemm_tiled_kernel(SkinnyKArgs a) {
     // Epilogue: rank = bf16(act(bf16(v * col_scale + bias))), two columns per store.
     {
 #pragma clang fp contract(off)
-        for (int e = tid; e < kRgTile * kRgTile / 2; e += 256) {
-            const int mm = e >> 5, nn = 2 * (e & 31);
+        for (int e = tid; e < TM * TN / 2; e += kThreads) {
+            const int mm = e / (TN / 2), nn = 2 * (e % (TN / 2));
             const int m = m0 + mm, n = n0 + nn;
             if (m >= a.M || n >= a.ncols) continue;
             uint32_t packed = 0;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                float v = red[mm * (kRgTile + 4) + nn + t];
+                float v = red[mm * kPitch + nn + t];
                 if (a.col_scale) v = v * a.col_scale[n + t];
                 if (a.bias) v = v + bf16_bits_to_f32(a.bias[n + t]);
                 v = round_bf16(v);
@@ -599,17 +614,23 @@ static inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 SkinnyPlan plan_skinny(int64_t rows, int64_t K, int64_t cols, bool gru) {
     SkinnyPlan p{};
     if (!gru && rows >= kRankTiledMinRows && K % kRgChunk == 0 && cols % 8 == 0) {
-        // LDS-tiled kernel: 64 x 64 tiles, K split so that about 256 workgroups run.
+        // LDS-tiled kernel.  Tiles of 128 rows x 64 columns from 256 rows on
+        // (64 x 64 below, where a 128-row tile would be mostly empty), K split
+        // 8 ways unless the tiles alone fill the device, never below two chunks
+        // per split.  At M = 512, r = 512, d = 4096 the shapes measured (GEMM
+        // kernel, rocprof average): 64x64 / 8 splits 9.45 us, 128x64 / 8 8.89,
+        // 128x128 / 16 10.44 (twice the partials), with the split-K epilogue
+        // 4.9-5.2 us in each case.
         p.tiled = true;
         p.wm = p.wn = 0;
-        p.m_wg = (int)cdiv(rows, kRgTile);
-        p.n_wg = (int)cdiv(cols, kRgTile);
+        p.tm = rows >= 256 ? 128 : 64;
+        p.tn = 64;
+        p.m_wg = (int)cdiv(rows, p.tm);
+        p.n_wg = (int)cdiv(cols, p.tn);
         p.ksteps = (int)cdiv(K, 32);
         const int nchunks = (int)(K / kRgChunk);
         const int tiles = p.m_wg * p.n_wg;
-        // 8 K splits (one K slice per XCD) unless the tiles alone fill the
-        // device; never below two chunks per split.
-        int ks = tiles >= 512 ? 1 : 8;
+        int ks = tiles >= 256 ? 1 : 8;
         ks = std::min(ks, std::max(1, nchunks / 2));
         p.ksplit = std::min(ks, kMaxKSplit);
         p.partial_bytes = p.ksplit > 1 ? (size_t)p.ksplit * rows * cols * sizeof(float) : 0;
@@ -659,6 +680,18 @@ static hipError_t launch_skinny(const SkinnyKArgs& ka, const SkinnyPlan& p, int 
     return hipGetLastError();
 }
 
+template <int TM, int TN>
+static hipError_t launch_rank_tiled(const SkinnyKArgs& ka, dim3 grid, int wmode, hipStream_t s) {
+    const dim3 block(rg_threads<TM, TN>());
+    if (wmode == W_PACKED)
+        hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED, TM, TN>), grid, block, 0, s, ka);
+    else if (wmode == W_PACKED_E4M3)
+        hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED_E4M3, TM, TN>), grid, block, 0, s, ka);
+    else
+        hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_ROWMAJOR, TM, TN>), grid, block, 0, s, ka);
+    return hipGetLastError();
+}
+
 static void fill_ws(SkinnyKArgs& ka, const SkinnyPlan& p, void* ws, size_t data_off) {
     char* w = static_cast<char*>(ws);
     ka.counters = reinterpret_cast<unsigned int*>(w + kCountersOff);
@@ -679,12 +712,11 @@ hipError_t launch_rank_proj(const RankArgs& a, const SkinnyPlan& p, void* ws, si
     const int wmode = a.a_scale ? W_PACKED_E4M3 : (a.a_packed ? W_PACKED : W_ROWMAJOR);
     if (p.tiled) {
         const dim3 grid(p.ksplit, p.n_wg, p.m_wg);
-        if (wmode == W_PACKED)
-            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED>), grid, dim3(256), 0, s, ka);
-        else if (wmode == W_PACKED_E4M3)
-            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_PACKED_E4M3>), grid, dim3(256), 0, s, ka);
-        else
-            hipLaunchKernelGGL((rank_gemm_tiled_kernel<W_ROWMAJOR>), grid, dim3(256), 0, s, ka);
+        hipError_t e0 = hipSuccess;
+        if (p.tm == 64 && p.tn == 64) e0 = launch_rank_tiled<64, 64>(ka, grid, wmode, s);
+        else if (p.tm == 128 && p.tn == 64) e0 = launch_rank_tiled<128, 64>(ka, grid, wmode, s);
+        else return hipErrorInvalidValue;
+        if (e0 != hipSuccess) return e0;
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || p.ksplit == 1) return e;
         const int64_t quads = (int64_t)ka.M * ka.ncols / 4;
