@@ -55,6 +55,8 @@ def parse_args():
                     help="add the whole draft block (target LM head + first argmax + DeLS rollout, one graph)")
     ap.add_argument("--also-fp8", action=argparse.BooleanOptionalAction, default=True,
                     help="add the fp8 variant (e4m3 A and B with per-channel scales) of the workload's shape")
+    ap.add_argument("--also-batched-lm-head", action=argparse.BooleanOptionalAction, default=True,
+                    help="also time the target LM head at M=512 (library GEMM and the hand-written kernel)")
     ap.add_argument("--also-domino", action=argparse.BooleanOptionalAction, default=True,
                     help="add one Domino correction step (code/kernel/domino.py:58-173) at the draft block's batch")
     ap.add_argument("--cpu-baseline", action=argparse.BooleanOptionalAction, default=True)
@@ -551,6 +553,49 @@ def bench_draft_step(pkg, args, dev, torch):
                                 "hbm_frac": ltotal / (us_lblock * 1e-6) / 1e9 / HBM_PEAK_GBS}}
 
 
+def bench_batched_lm_head(pkg, dev, torch):
+    """The target LM head that produces the M=512 record's base logits: 512 hidden rows
+    (d 4096) against W [151936, 4096] bf16, bf16 logits [512, 151936] written --
+    the library GEMM (hipBLASLt through torch.mm) and the hand-written lm_head_kernel
+    (four row groups of 128, each re-streaming W).  Informative: it prices a kernel
+    that would fuse this GEMM into the M=512 argmax (no base logits in HBM)."""
+    M, d, V = 512, 4096, 151936
+    g = torch.Generator(device=dev).manual_seed(512)
+    W = (torch.randn(V, d, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    hid = torch.randn(M, d, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    Wp = pkg.pack_lm_head(W)
+    cur = torch.cuda.current_stream(dev)
+
+    def timed(fn, n=10):
+        for _ in range(2):
+            fn()
+        times = []
+        for _ in range(5):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize(dev)
+            e0.record(cur)
+            for _ in range(n):
+                fn()
+            e1.record(cur)
+            torch.cuda.synchronize(dev)
+            times.append(e0.elapsed_time(e1) / n)
+        return replay_stats(times)["median"] * 1e3
+
+    us_lib = timed(lambda: torch.mm(hid, W.t(), out=out))
+    us_hw = timed(lambda: pkg.lm_head(hid, Wp, out=out))
+    flops = 2.0 * M * d * V
+    nbytes = 2 * V * d + 2 * M * d + 2 * M * V
+    del W, Wp, out
+    torch.cuda.empty_cache()
+    return {"workload": "target LM head at M=512: hidden [512, 4096] . W[151936, 4096]^T, bf16 logits written",
+            "us_library_gemm": us_lib, "library_TFLOPs": flops / (us_lib * 1e-6) / 1e12,
+            "library_mfma_frac": flops / (us_lib * 1e-6) / 1e12 / BF16_MFMA_PEAK_TFLOPS,
+            "us_hand_written": us_hw, "hand_written_TFLOPs": flops / (us_hw * 1e-6) / 1e12,
+            "logits_bytes": 2 * M * V, "algorithmic_bytes": nbytes}
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as fh:
@@ -736,6 +781,11 @@ def main():
             out["draft_step"] = bench_draft_step(pkg, args, dev, torch)
         except Exception as e:  # informative record only
             out["draft_step"] = {"error": repr(e)}
+    if args.also_batched_lm_head and args.also_m512 and args.workload != "qwen3_8b_m512":
+        try:
+            out["batched_lm_head"] = bench_batched_lm_head(pkg, dev, torch)
+        except Exception as e:  # informative record only
+            out["batched_lm_head"] = {"error": repr(e)}
     if args.also_domino and args.workload != "qwen3_8b_m512":
         try:
             out["domino"] = bench_domino(pkg, args, dev, torch)
