@@ -213,10 +213,11 @@ hipError_t launch_domino_argmax(const DominoArgs& a, void* ws, hipStream_t s) {
     fin.key_stride = (int64_t)a.M * 128 <= (int64_t)(kCtrlBytes - kKeysOff) ? 16 : 1;
     const int ntiles = (a.V + 15) / 16;
     const int groups = (a.M + 15) / 16;
-    // two workgroups per CU (8 waves; the operands of E <= 1024 take 64 KiB of LDS each): 71.2 -> 69.8 us
-    // per step at 8 rows, E = 1024 (three per CU no longer fit the LDS: 89 us)
-    const int gx = std::max(1, std::min((ntiles + 3) / 4, (2 * device_cu_count() + groups - 1) / groups));
+    // two workgroups per CU where both fit the LDS (8 waves; the operands of E <= 1024 take 64 KiB each):
+    // 71.2 -> 69.8 us per step at 8 rows, E = 1024; more than fit at once is slower (three: 89 us)
     const size_t lds = domino_lds_bytes(a.E);
+    const int per_cu = lds <= 64 * 1024 ? 2 : 1;
+    const int gx = std::max(1, std::min((ntiles + 3) / 4, (per_cu * device_cu_count() + groups - 1) / groups));
     if (a.base_dtype == 1) return launch_domino_for_base<bf16_t>(a, fin, gx, groups, lds, s);
     if (a.base_dtype == 2) return launch_domino_for_base<f16_t>(a, fin, gx, groups, lds, s);
     return launch_domino_for_base<float>(a, fin, gx, groups, lds, s);
