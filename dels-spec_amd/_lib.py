@@ -107,6 +107,8 @@ SIGNATURES = {
     "dels_fused_argmax": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _i64, _int, _ptr, _int, _fptr, _i64, _fptr, _i64,
                                  _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_debug_set_decode_spin_limit": (_int, [_int]),
+    "dels_debug_set_rollout_resident": (_int, [_int]),
+    "dels_debug_set_resident_spin_limit": (_int, [_int]),
     "dels_lowrank_argmax_ws_bytes": (_sz, [_i64, _i64, _i64, _i64]),
     "dels_lowrank_argmax": (_int, [_ptr, _i64, _ptr, _i64, _int, _ptr, _int, _ptr, _i64, _int, _ptr, _i64, _int, _ptr,
                                    _int,

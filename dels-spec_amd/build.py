@@ -22,7 +22,8 @@ LIB_PATH = os.path.join(LIB_DIR, LIB_NAME)
 SOURCES = ["capi.hip", "skinny_gemm.hip", "fused_argmax.hip", "fused_argmax_f32.hip", "fused_argmax_bf16.hip",
            "fused_argmax_f16.hip", "fused_argmax_tiled_f32.hip", "fused_argmax_tiled_bf16.hip",
            "fused_argmax_tiled_f16.hip", "lowrank_decode_f32.hip", "lowrank_decode_bf16.hip",
-           "lowrank_decode_f16.hip", "pack.hip", "sample.hip", "domino_argmax.hip", "lm_head.hip"]
+           "lowrank_decode_f16.hip", "pack.hip", "sample.hip", "domino_argmax.hip", "lm_head.hip",
+           "rollout_resident.hip"]
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32 (kept off on this target).
 HIP_FLAGS = [

@@ -255,6 +255,24 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     uint16_t* h_next = static_cast<uint16_t*>(p->h_b);
     const size_t esz = dtype_size(p->base_dtype);
     const bool packed = p->weights_layout == DELS_LAYOUT_MFMA16;
+    if (rollout_resident_enabled() && rollout_resident_eligible(B, G, r, V, p->steps, packed)) {
+        // every step in one launch with B held on chip (rollout_resident.hip)
+        ResidentRolloutArgs ra{};
+        ra.w_hh = g.w_hh; ra.b_hh = g.b_hh;
+        ra.A = static_cast<const uint16_t*>(p->rank_w); ra.rank_b = static_cast<const uint16_t*>(p->rank_b);
+        ra.act = p->act;
+        ra.B = static_cast<const uint16_t*>(p->lm_w);
+        ra.gi_table = g.gi_table; ra.ld_gi = g.ld_gi; ra.table_rows = g.table_rows;
+        ra.prefix = p->prefix_ids;
+        ra.base = p->base; ra.ld_base = p->ld_base ? p->ld_base : p->steps * (int64_t)V;
+        ra.base_dtype = p->base_dtype;
+        ra.prior = p->prior; ra.prior_dtype = p->prior_dtype;
+        ra.alpha = p->alpha; ra.beta = p->beta;
+        ra.batch = B; ra.G = G; ra.V = V; ra.steps = p->steps;
+        ra.out_ids = p->out_ids; ra.out_scores = p->out_scores;
+        hipError_t e = launch_rollout_resident(ra, ws, s);
+        return e == hipSuccess ? DELS_OK : hip_fail(e, "resident rollout launch");
+    }
     const bool use_decode = G >= kRolloutDecodeMinG && decode_eligible(B, G, r, packed, packed);
     // every step advances the GRU inside its decode launch, the first one from
     // the zero state on the prefix ids: no GRU launch at all
@@ -763,6 +781,8 @@ int dels_fused_argmax(const void* rank, int64_t ldrank, const void* B, int64_t l
 }
 
 int dels_debug_set_decode_spin_limit(int limit) { return set_decode_spin_limit(limit); }
+int dels_debug_set_rollout_resident(int enable) { return set_rollout_resident(enable); }
+int dels_debug_set_resident_spin_limit(int limit) { return set_resident_spin_limit(limit); }
 
 size_t dels_lowrank_argmax_ws_bytes(int64_t M, int64_t d, int64_t r, int64_t V) {
     if (!rows_ok(M) || !inner_ok(d) || !rows_ok(r) || !vocab_ok(V)) return 0;

@@ -20,6 +20,9 @@ namespace dels {
 //    by the decode kernels only, so each word holds zero or the tag of an
 //    earlier decode launch on this workspace -- never leftover data of another
 //    entry point that could pass for the current launch's tag.
+//  * [kResidentOff, kDataOff): the resident rollout's tagged words (the state
+//    and the rank of each step) and argmax slot words, written by that kernel
+//    only, for the same reason.
 //  * [kDataOff, ...): data regions of the other kernels (split-K partials, the
 //    rank, quantised operands); they may hold anything between calls.
 // Calls with different shapes or entry points can therefore share one
@@ -39,7 +42,21 @@ constexpr int kDecodeMaxRank = 512;            // largest rank r the decode step
 constexpr size_t kDecodeWordBytes = align256((size_t)kDecodeWGs * 256 * 8) +
                                     align256((size_t)16 * (kDecodeMaxRank / 2) * 8);
 constexpr size_t kDecodeOff = kCtrlBytes;
-constexpr size_t kDataOff = kDecodeOff + kDecodeWordBytes;
+
+// The rollout with B resident on chip (rollout_resident.hip): r = 256, G <= 1024,
+// batch <= 16, 64 .. 256 workgroups; its words {tag, two bf16} of the state
+// [16][G/2] and the rank [16][r/2], then the argmax slot words [2][16][nwg].
+constexpr int kResidentRank = 256;
+constexpr int kResidentMaxG = 1024;
+constexpr int kResidentLdsTiles = 6;           // vocabulary tiles per workgroup in LDS beyond the registers
+constexpr int kResidentMaxSteps = 64;
+constexpr int kResidentMaxWGs = 256;
+constexpr size_t kResidentHWordBytes = align256((size_t)16 * (kResidentMaxG / 2) * 8);
+constexpr size_t kResidentRankWordBytes = align256((size_t)16 * (kResidentRank / 2) * 8);
+constexpr size_t kResidentSlotBytes = align256((size_t)2 * 16 * kResidentMaxWGs * 8);
+constexpr size_t kResidentWordBytes = kResidentHWordBytes + kResidentRankWordBytes + kResidentSlotBytes;
+constexpr size_t kResidentOff = kDecodeOff + kDecodeWordBytes;
+constexpr size_t kDataOff = kResidentOff + kResidentWordBytes;
 
 // ---- skinny GEMM: rank projection and fused GRU step -----------------------
 
@@ -170,6 +187,26 @@ hipError_t launch_domino_argmax(const DominoArgs& a, void* ws, hipStream_t s);
 // Both weights packed, r/32 in {2, 4, 8, 16}, d a multiple of 32 and at most
 // 32 K blocks per split of the rank projection.
 bool decode_eligible(int64_t M, int64_t d, int64_t r, bool a_packed, bool b_packed);
+
+// ---- the rollout with B resident on chip (one launch for every step) -------------
+struct ResidentRolloutArgs {
+    const uint16_t* w_hh; const uint16_t* b_hh;
+    const uint16_t* A; const uint16_t* rank_b; int act;
+    const uint16_t* B;
+    const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
+    const int64_t* prefix;
+    const void* base; int64_t ld_base; int base_dtype;
+    const void* prior; int prior_dtype;
+    const float* alpha; const float* beta;
+    int64_t batch, G, V, steps;
+    int64_t* out_ids; float* out_scores;
+};
+bool rollout_resident_eligible(int64_t batch, int64_t G, int64_t r, int64_t V, int64_t steps, bool packed);
+hipError_t launch_rollout_resident(const ResidentRolloutArgs& a, void* ws, hipStream_t s);
+int resident_spin_limit();
+int set_resident_spin_limit(int limit);   // returns the previous limit
+int set_rollout_resident(int enable);   // returns the previous setting (1 = used where eligible)
+bool rollout_resident_enabled();
 // The fp8 decode step (A e4m3 K32, B e4m3 K128): as above with r in {128, 256, 512}.
 bool decode8_eligible(int64_t M, int64_t d, int64_t r);
 // A rollout step with the local head's GRU fused into the decode launch:

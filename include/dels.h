@@ -24,11 +24,14 @@
  *    matching *_ws_bytes() function returns, 256-byte aligned, zero-filled
  *    once before first use (dels_workspace_init).  Every entry point lays it
  *    out alike: a 64 KiB control area that kernels return to the state they
- *    found it in -- zeros, apart from one word that the fused decode step
- *    advances once per launch (a launch generation) -- so no call needs a
+ *    found it in -- zeros, apart from one word that the fused decode step and
+ *    the one-launch rollout advance once per launch (a launch generation) -- so no call needs a
  *    memset; then 544 KiB that only the fused decode step writes (its rank
- *    hand-off words, each tagged with a launch generation); then data regions
- *    that may hold anything between calls.  One workspace may therefore serve
+ *    hand-off words, each tagged with a launch generation) and 144 KiB that
+ *    only the one-launch rollout writes (its state and rank words, tagged with
+ *    the launch generation and the step, and its argmax slot words, which each
+ *    launch clears before use); then data regions that may hold
+ *    anything between calls.  One workspace may therefore serve
  *    every entry point and shape in turn; calls that share it must not
  *    overlap in time (same stream is fine).
  *  - Extents: rows, batch, batch * steps, r, G and E below 2^24, hidden sizes
@@ -196,6 +199,22 @@ int dels_lowrank_argmax_noalloc(const void* h, int64_t ldh, const void* A, int64
  * computation) and returns the previous one.  Not thread-safe.
  */
 int dels_debug_set_decode_spin_limit(int limit);
+
+/*
+ * Test hook (no counterpart in the reference).  Where the shape allows it
+ * (weights in the MFMA-16 layout, r = 256, batch <= 16, G <= 1024 a multiple of
+ * twice the CU count, the vocabulary's share fitting a CU), dels_rollout_enqueue
+ * and dels_graph_create run every step of the rollout in one launch that keeps
+ * the low-rank head resident on chip; enable = 0 selects the per-step launches
+ * instead (for later calls), 1 restores the default.  Returns the previous
+ * setting.  Not thread-safe.
+ */
+int dels_debug_set_rollout_resident(int enable);
+/* Test hook: the waits of that one-launch rollout re-read each other's results
+ * at most `limit` times (default 65536) before the launch gives up; a launch
+ * that gives up writes -1 ids for the steps it could not finish, and the next
+ * launch starts clean.  Returns the previous limit.  Not thread-safe. */
+int dels_debug_set_resident_spin_limit(int limit);
 
 /*
  * Plain argmax of each row of logits: sample() at temperature 0

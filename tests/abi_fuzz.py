@@ -110,7 +110,9 @@ def main() -> int:
                     args.append(value(t))
             out = fn(*args)
             calls += 1
-            if res is L._int and name not in ("dels_abi_version", "dels_debug_set_decode_spin_limit"):
+            if res is L._int and name not in ("dels_abi_version", "dels_debug_set_decode_spin_limit",
+                                              "dels_debug_set_rollout_resident",
+                                              "dels_debug_set_resident_spin_limit"):
                 if out not in statuses:
                     print(f"abi_fuzz: {name}{tuple(args)} returned {out}", flush=True)
                     return 1
@@ -120,6 +122,8 @@ def main() -> int:
                     print(f"abi_fuzz: {name} returned a graph handle without a device", flush=True)
                     return 1
     lib.dels_debug_set_decode_spin_limit(16384)
+    lib.dels_debug_set_rollout_resident(1)
+    lib.dels_debug_set_resident_spin_limit(65536)
     print(f"abi_fuzz: {calls} calls over {len(L.SIGNATURES)} entry points, no finding", flush=True)
     return 0
 

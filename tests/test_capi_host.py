@@ -68,9 +68,10 @@ def test_workspace_sizes(pkg):
     assert w >= lib.dels_fused_argmax_ws_bytes(16, 512, 151936) + 16 * 512 * 2
     assert w % 256 == 0
     assert lib.dels_rollout_ws_bytes(8, 1024, 512, 151936) >= lib.dels_gru_step_ws_bytes(8, 1024)
-    # every layout starts with the 64 KiB control area and the 544 KiB that only
-    # the fused decode step writes, so one workspace serves every entry point
-    reserved = 65536 + 544 * 1024
+    # every layout starts with the 64 KiB control area, the 544 KiB that only
+    # the fused decode step writes and the 144 KiB that only the one-launch
+    # rollout writes, so one workspace serves every entry point
+    reserved = 65536 + 544 * 1024 + 144 * 1024
     assert lib.dels_fused_argmax_ws_bytes(1, 8, 1) == reserved
     assert lib.dels_argmax_rows_ws_bytes(1, 1) == reserved
     for n in (lib.dels_rank_proj_ws_bytes(1, 64, 64), lib.dels_gru_step_ws_bytes(1, 64),
