@@ -220,6 +220,19 @@ __device__ __forceinline__ bool rr_slot_maxima(const RrArgs& a, const unsigned l
     return !__syncthreads_or(!got);
 }
 
+// One step of a maximum over the 16 lanes of each DPP row of 64-bit argmax keys
+// (pack_argmax): every lane takes the larger of its key and that of the lane K
+// below it in its row (lanes with none read key 0, the lowest).  After K = 1,
+// 2, 4, 8 lane 15 of a row holds the row's best.
+template <int K>
+__device__ __forceinline__ void rr_row_max(unsigned long long& k) {
+    constexpr int kRowShr = 0x110 + K;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)k, kRowShr, 0xf, 0xf, true);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(k >> 32), kRowShr, 0xf, 0xf, true);
+    const unsigned long long o = ((unsigned long long)hi << 32) | lo;
+    k = o > k ? o : k;
+}
+
 template <typename BaseT, typename PriorT>
 __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) {
 #pragma clang fp contract(off)
@@ -229,8 +242,7 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
     __shared__ __attribute__((aligned(16))) uint16_t s_rank[16 * kRrRPitch];
     __shared__ __attribute__((aligned(16))) float s_red[kRrWaves * 256];
     __shared__ float s_prior[(kRrWaves * kRrRegTiles + kResidentLdsTiles) * 16];
-    __shared__ float s_val[kRrWaves][16];
-    __shared__ int s_idx[kRrWaves][16];
+    __shared__ unsigned long long s_key[kRrWaves][16];    // each wave's best key of each row
     __shared__ float s_gh[16 * 16];
     __shared__ float s_ab[2][kResidentMaxSteps];          // alpha, beta of each step
     __shared__ float s_bias[32];                          // b_hh of the operand rows, rank bias of the tile
@@ -267,54 +279,7 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
     const int nlds = max(0, ntl - kRrWaves * kRrRegTiles);
     const bool has_lds_tile = wave < nlds;
 
-    // ---- resident operands -------------------------------------------------------
-    bf16x8 bt[kRrRegTiles][kRrKs];
-#pragma unroll
-    for (int j = 0; j < kRrRegTiles; ++j) {
-        // a tile that is not this wave's loads the last tile (in bounds) and keeps zeros
-        const int ti = wave + 8 * j;
-        const int t = min(T0 + ti, a.ntiles - 1);
-        const uint32_t keep = ti < ntl ? ~0u : 0u;
-#pragma unroll
-        for (int s = 0; s < kRrKs; ++s)
-            bt[j][s] = masked_bf16x8(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-                                         a.B + ((int64_t)t * kRrKs + s) * 512 + lane * 8)),
-                                     keep);
-    }
-    if (rank_wg) {
-        // A rows 16 w .. 16 w + 15: the MFMA-16 blocks of that row block, in order
-        for (int i = threadIdx.x; i < KB * 64; i += kRrThreads) {
-            const int kb = i >> 6, l = i & 63;
-            *reinterpret_cast<u32x4*>(s_union + kb * 1024 + l * 16) =
-                *reinterpret_cast<const u32x4*>(a.A + ((int64_t)w * KB + kb) * 512 + l * 8);
-        }
-    } else {
-        for (int i = threadIdx.x; i < nlds * kRrKs * 64; i += kRrThreads) {
-            const int e = i / (kRrKs * 64), rem = i - e * (kRrKs * 64), s = rem >> 6, l = rem & 63;
-            const int t = T0 + kRrWaves * kRrRegTiles + e;
-            *reinterpret_cast<u32x4*>(s_union + (e * kRrKs + s) * 1024 + l * 16) =
-                *reinterpret_cast<const u32x4*>(a.B + ((int64_t)t * kRrKs + s) * 512 + l * 8);
-        }
-    }
-    // W_hh rows of units u0 .. u0 + upw - 1: operand row j = g * upw + i holds row
-    // g * G + u0 + i of W_hh (rows past 3 upw are zero)
-    const int u0 = w * a.upw;
-    for (int i = threadIdx.x; i < KB * 64; i += kRrThreads) {
-        const int kb = i >> 6, l = i & 63;
-        const int j = l & 15, oct = l >> 4;
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (j < 3 * a.upw) {
-            const int g = j / a.upw, row = g * G + u0 + (j - g * a.upw);
-            v = *reinterpret_cast<const u32x4*>(a.w_hh + ((int64_t)(row >> 4) * KB + kb) * 512 + ((row & 15) + 16 * oct) * 8);
-        }
-        *reinterpret_cast<u32x4*>(s_whh + kb * 1024 + l * 16) = v;
-    }
-    // the prior of every column of the workgroup's tiles (widened), the state zero
-    for (int i = threadIdx.x; i < ntl * 16; i += kRrThreads) {
-        const int v = min(T0 * 16 + i, V - 1);
-        if constexpr (is_no_prior<PriorT>::value) s_prior[i] = 0.f;
-        else s_prior[i] = widen_raw<PriorT>(load_raw(prior + v));
-    }
+    const int u0 = w * a.upw;   // this workgroup's first GRU unit
     for (int i = threadIdx.x; i < 16 * kRrHPitch / 2; i += kRrThreads) reinterpret_cast<uint32_t*>(s_h)[i] = 0u;
     for (int i = threadIdx.x; i < 16 * kRrRPitch / 2; i += kRrThreads) reinterpret_cast<uint32_t*>(s_rank)[i] = 0u;
     for (int i = threadIdx.x; i < a.steps; i += kRrThreads) {
@@ -463,6 +428,59 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
     bool ok = true;
     compute_gh(true);
     gru_publish(a.prefix, 1, rr_tag(gen, 0));
+
+    // ---- resident operands, loaded while the prefix state travels (a read
+    // waits for every load issued before it, so the state went out first):
+    // the LDS operands, then this wave's register tiles of B
+    if (rank_wg) {
+        // A rows 16 w .. 16 w + 15: the MFMA-16 blocks of that row block, in order
+        for (int i = threadIdx.x; i < KB * 64; i += kRrThreads) {
+            const int kb = i >> 6, l = i & 63;
+            *reinterpret_cast<u32x4*>(s_union + kb * 1024 + l * 16) =
+                *reinterpret_cast<const u32x4*>(a.A + ((int64_t)w * KB + kb) * 512 + l * 8);
+        }
+    } else {
+        for (int i = threadIdx.x; i < nlds * kRrKs * 64; i += kRrThreads) {
+            const int e = i / (kRrKs * 64), rem = i - e * (kRrKs * 64), s = rem >> 6, l = rem & 63;
+            const int t = T0 + kRrWaves * kRrRegTiles + e;
+            *reinterpret_cast<u32x4*>(s_union + (e * kRrKs + s) * 1024 + l * 16) =
+                *reinterpret_cast<const u32x4*>(a.B + ((int64_t)t * kRrKs + s) * 512 + l * 8);
+        }
+    }
+    // W_hh rows of units u0 .. u0 + upw - 1: operand row j = g * upw + i holds row
+    // g * G + u0 + i of W_hh (rows past 3 upw are zero)
+    for (int i = threadIdx.x; i < KB * 64; i += kRrThreads) {
+        const int kb = i >> 6, l = i & 63;
+        const int j = l & 15, oct = l >> 4;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (j < 3 * a.upw) {
+            const int g = j / a.upw, row = g * G + u0 + (j - g * a.upw);
+            v = *reinterpret_cast<const u32x4*>(a.w_hh + ((int64_t)(row >> 4) * KB + kb) * 512 + ((row & 15) + 16 * oct) * 8);
+        }
+        *reinterpret_cast<u32x4*>(s_whh + kb * 1024 + l * 16) = v;
+    }
+    // the prior of every column of the workgroup's tiles (widened)
+    for (int i = threadIdx.x; i < ntl * 16; i += kRrThreads) {
+        const int v = min(T0 * 16 + i, V - 1);
+        if constexpr (is_no_prior<PriorT>::value) s_prior[i] = 0.f;
+        else s_prior[i] = widen_raw<PriorT>(load_raw(prior + v));
+    }
+    // the register tiles after the LDS operands (whose stores wait for their loads)
+    asm volatile("" ::: "memory");
+    bf16x8 bt[kRrRegTiles][kRrKs];
+#pragma unroll
+    for (int j = 0; j < kRrRegTiles; ++j) {
+        // a tile that is not this wave's loads the last tile (in bounds) and keeps zeros
+        const int ti = wave + 8 * j;
+        const int t = min(T0 + ti, a.ntiles - 1);
+        const uint32_t keep = ti < ntl ? ~0u : 0u;
+#pragma unroll
+        for (int s = 0; s < kRrKs; ++s)
+            bt[j][s] = masked_bf16x8(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+                                         a.B + ((int64_t)t * kRrKs + s) * 512 + lane * 8)),
+                                     keep);
+    }
+
     ok = read_state(rr_tag(gen, 0));
 
     int s = 0;
@@ -474,8 +492,6 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
         int lcol = col, lkg = kg;
         asm volatile("" : "+v"(lcol), "+v"(lkg));
         if (rank_wg) rank_publish(tag);
-        // next step's gh while the rank travels
-        if (s + 1 < a.steps) compute_gh(false);
         // base values of this wave's tiles (issued before the rank wait): the
         // wave-uniform start of each tile's columns plus one per-lane offset per row
         uint32_t braw[kRrRegTiles + 1][4];
@@ -525,35 +541,41 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
         int bidx[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) { best[q] = -__builtin_inff(); bidx[q] = INT_MAX; }
+        // a lane's column grows with its tile number, so a later tile takes the
+        // lead only on a larger score, or on an equal one while nothing has
+        // (the first -inf); written with bitwise tests, no branches
 #pragma unroll
         for (int j = 0; j <= kRrRegTiles; ++j) {
             const int ti = j < kRrRegTiles ? wave + 8 * j : kRrWaves * kRrRegTiles + wave;
             const bool live = j < kRrRegTiles ? ti < ntl : lds_tile;   // wave-uniform
             const int tc = min(ti, max(ntl - 1, 0));
             const int v = (T0 + tc) * 16 + lcol;
+            const bool livev = live & (v < V);
             const float pv = s_prior[tc * 16 + lcol];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
                 float sc = __builtin_fmaf(acc[j][q], al, widen_raw<BaseT>(braw[j][q]));
                 if (use_prior) sc = __builtin_fmaf(-be, pv, sc);
-                const bool take = live & (v < V) & argmax_better(sc, v, best[q], bidx[q]);
+                const bool take = livev & ((sc > best[q]) | ((sc == best[q]) & (bidx[q] == INT_MAX)));
                 best[q] = take ? sc : best[q];
                 bidx[q] = take ? v : bidx[q];
             }
         }
-        // over the 16 columns, then (below) the waves
+        // over the 16 columns of each row as argmax keys (a lane without a
+        // candidate holds -inf at index INT_MAX, below every real one; DPP row
+        // shifts: lane 15 of a row ends with the row's best), then (below) the waves
+        unsigned long long key[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-#pragma unroll
-            for (int off = 1; off < 16; off <<= 1) {
-                const float ov = __shfl_xor(best[q], off, 64);
-                const int oi = __shfl_xor(bidx[q], off, 64);
-                if (argmax_better(ov, oi, best[q], bidx[q])) { best[q] = ov; bidx[q] = oi; }
-            }
+            key[q] = pack_argmax(best[q], (uint32_t)bidx[q]);
+            rr_row_max<1>(key[q]);
+            rr_row_max<2>(key[q]);
+            rr_row_max<4>(key[q]);
+            rr_row_max<8>(key[q]);
         }
-        if (col == 0) {
+        if (col == 15) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) { s_val[wave][4 * kg + q] = best[q]; s_idx[wave][4 * kg + q] = bidx[q]; }
+            for (int q = 0; q < 4; ++q) s_key[wave][4 * kg + q] = key[q];
         }
         __syncthreads();
         // the workgroup's best of each row into its slot word for the step
@@ -561,18 +583,20 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
         unsigned long long* slot_set = a.slots + (s & 1) * kRrSlotSet;
         if ((int)threadIdx.x < M) {
             const int m = threadIdx.x;
-            float bv = s_val[0][m];
-            int bi = s_idx[0][m];
+            unsigned long long k = s_key[0][m];   // order(score) << 32 | ~index
 #pragma unroll
-            for (int ww = 1; ww < kRrWaves; ++ww)
-                if (argmax_better(s_val[ww][m], s_idx[ww][m], bv, bi)) { bv = s_val[ww][m]; bi = s_idx[ww][m]; }
-            unsigned long long word = low2;
-            if (bi != INT_MAX) {
-                const unsigned long long k = pack_argmax(bv, (uint32_t)bi);   // order(score) << 32 | ~index
-                word |= (k & 0xffffffff00000000ull) | ((unsigned long long)((uint32_t)k & 0x3fffffffu) << 2);
-            }
+            for (int ww = 1; ww < kRrWaves; ++ww) k = max(k, s_key[ww][m]);
+            // no candidate (index INT_MAX) leaves the index field zero: index
+            // 2^30 - 1, past every vocabulary, below every real candidate
+            const unsigned long long word =
+                low2 | (k & 0xffffffff00000000ull) | ((unsigned long long)((uint32_t)k & 0x3fffffffu) << 2);
             __hip_atomic_store(slot_set + w * 16 + m, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+
+        // next step's gh while the slot words travel (every workgroup: placed
+        // before the rank wait it would delay the rank workgroups' argmax, and
+        // with it every workgroup's slot read)
+        if (s + 1 < a.steps) compute_gh(false);
 
         // ---- the step's ids (every workgroup: its GRU units need them) ---------------
         const bool need = s + 1 < a.steps || w == 0;
