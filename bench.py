@@ -471,8 +471,9 @@ def bench_draft_step(pkg, args, dev, torch):
     The block as DeLSDraftStep builds it by default: the hand-written LM head
     (lm_head_kernel, the position-0 argmax fused, its logits never written) and the
     14-step rollout.  Algorithmic bytes: W once, hidden, the base rows of positions
-    1..k-1 written, the first ids; per DeLS step the low-rank head, rank projection,
-    base rows and prior; per GRU step W_hh and the input-table rows.  The
+    1..k-1 written, the first ids; the rollout's weights once (the low-rank head, rank
+    projection, W_hh and prior stay on chip for the whole rollout, which is one launch
+    at this shape); per step the base rows, the input-table rows and the ids.  The
     `library_lm_head` record times the same block with the library GEMM (hipBLASLt
     through torch.mm, as nn.Linear) followed by the position-0 argmax."""
     wl = pkg.synth.draft_block_workload(dev)
@@ -513,8 +514,8 @@ def bench_draft_step(pkg, args, dev, torch):
             st.replay()
         return run
 
-    step_bytes = 2 * V * r + 2 * r * G + 2 * B * V + 2 * V + 12 * B      # low-rank head, A, base rows, prior, outputs
-    gru_bytes = 2 * 3 * G * G + 2 * B * 3 * G + 4 * B * G                  # W_hh, input-table rows, state
+    weight_bytes = 2 * V * r + 2 * r * G + 2 * 3 * G * G + 2 * V           # low-rank head, A, W_hh, prior: once
+    step_bytes = 2 * B * V + 2 * B * 3 * G + 12 * B                        # base rows, input-table rows, outputs
 
     # the default block: the hand-written LM head
     step = make("auto")
@@ -528,7 +529,7 @@ def bench_draft_step(pkg, args, dev, torch):
                                           out_score=first_sc))
     step.close()
     head_bytes = 2 * V * d + 2 * B * k * d + 2 * B * (k - 1) * V + 12 * B
-    total = head_bytes + steps * step_bytes + steps * gru_bytes
+    total = head_bytes + weight_bytes + steps * step_bytes
 
     # the same block with the library GEMM + row argmax
     lstep = make("library")
@@ -536,7 +537,7 @@ def bench_draft_step(pkg, args, dev, torch):
     us_gemm = timed(lambda i: torch.mm(hiddens[i % 3].view(B * k, d), W.t(), out=lstep.static_base.view(B * k, V)))
     lstep.close()
     gemm_bytes = 2 * V * d + 2 * B * k * d + 2 * B * k * V
-    ltotal = gemm_bytes + 2 * B * V + steps * step_bytes + steps * gru_bytes
+    ltotal = gemm_bytes + 2 * B * V + weight_bytes + steps * step_bytes
     return {"workload": "draft block: batch 8, block 16 (k_draft 15), d 4096, V 151936, local head G 1024 r 256",
             "lm_head": "lm_head_kernel (hand-written, position-0 argmax fused)",
             "us_per_block": us_block, "draft_tokens_per_s": B * k / (us_block * 1e-6),
