@@ -18,12 +18,14 @@ _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 # one, say); by default the in-tree build is loaded.
 LIB_PATH = os.environ.get("DELS_LIBRARY_PATH") or os.path.join(_PKG_DIR, "_lib", "libdels_mi355x.so")
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DELS_OK = 0
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ACT_IDENTITY, ACT_SILU = 0, 1
 LAYOUT_ROWMAJOR, LAYOUT_MFMA16 = 0, 1
 LAYOUT_FP8_K128, LAYOUT_FP8_K32 = 2, 3
+# the Domino correction MLP's middle layer (DELS_MIDDLE_*): name -> code
+MIDDLE_CODES = {"silu": 0, "identity": 1, "relu": 2, "gelu": 3, "gelu_tanh": 4, "tanh": 5, "sigmoid": 6}
 NOALLOC_SCRATCH_BYTES = 16 << 20      # DELS_NOALLOC_SCRATCH_BYTES
 
 _i64 = ctypes.c_int64
@@ -73,6 +75,7 @@ class DominoRolloutParams(ctypes.Structure):
         ("h_a", _ptr), ("h_b", _ptr),
         ("z", _ptr), ("s", _ptr),
         ("ws", _ptr), ("ws_bytes", _sz),
+        ("middle", _int),
     ]
 
 
@@ -138,7 +141,7 @@ SIGNATURES = {
     "dels_lm_head": (_int, [_ptr, _i64, _ptr, _i64, _i64, _i64, _ptr, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_domino_argmax_ws_bytes": (_sz, [_i64, _i64, _i64]),
     "dels_domino_argmax": (_int, [_ptr, _i64, _ptr, _i64, _ptr, _ptr, _int, _ptr, _i64, _int, ctypes.c_float,
-                                  _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
+                                  _int, _i64, _i64, _i64, _ptr, _ptr, _i64, _ptr, _sz, _ptr]),
     "dels_domino_rollout_ws_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "dels_domino_rollout_enqueue": (_int, [ctypes.POINTER(DominoRolloutParams), _ptr]),
     "dels_domino_graph_create": (_int, [ctypes.POINTER(DominoRolloutParams), ctypes.POINTER(_ptr)]),

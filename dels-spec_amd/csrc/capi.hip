@@ -516,8 +516,8 @@ static DominoLayout domino_layout(int64_t batch, int64_t steps, int64_t D, int64
 
 static int check_domino_step(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
                              const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase,
-                             int base_dtype, float alpha, int64_t M, int64_t E, int64_t V, const int64_t* out_ids,
-                             int64_t ld_out) {
+                             int base_dtype, float alpha, int middle, int64_t M, int64_t E, int64_t V,
+                             const int64_t* out_ids, int64_t ld_out) {
     if (M < 0 || E <= 0 || V <= 0) return fail(DELS_ERR_INVALID_ARGUMENT, "bad shape M=%lld E=%lld V=%lld",
                                                 (long long)M, (long long)E, (long long)V);
     if (V >= INT32_MAX || M > kMaxKeyRows) return fail(DELS_ERR_UNSUPPORTED, "Domino step: M <= %d, V < 2^31-1",
@@ -526,6 +526,8 @@ static int check_domino_step(const void* z, int64_t ldz, const void* sv, int64_t
         return fail(DELS_ERR_UNSUPPORTED, "Domino step: E=%lld must be a multiple of 32 and at most %d",
                     (long long)E, kDominoMaxE);
     if (!(alpha == alpha)) return fail(DELS_ERR_INVALID_ARGUMENT, "guidance alpha is NaN");
+    if (middle < DELS_MIDDLE_SILU || middle > DELS_MIDDLE_SIGMOID)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "unknown Domino middle layer %d (DELS_MIDDLE_*)", middle);
     if (M == 0) return DELS_OK;
     if (!z || !sv) return fail(DELS_ERR_INVALID_ARGUMENT, "z or s is NULL");
     if ((M > 1 && (ldz < E || lds < E)) || ldz < 0 || lds < 0)
@@ -546,8 +548,8 @@ static int check_domino_step(const void* z, int64_t ldz, const void* sv, int64_t
 
 static DominoArgs domino_args(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
                               const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase,
-                              int base_dtype, float alpha, int64_t M, int64_t E, int64_t V, int64_t* out_ids,
-                              float* out_score, int64_t ld_out) {
+                              int base_dtype, float alpha, int middle, int64_t M, int64_t E, int64_t V,
+                              int64_t* out_ids, float* out_score, int64_t ld_out) {
     DominoArgs d{};
     d.z = static_cast<const uint16_t*>(z); d.ldz = ldz;
     d.s = static_cast<const uint16_t*>(sv); d.lds = lds;
@@ -555,6 +557,7 @@ static DominoArgs domino_args(const void* z, int64_t ldz, const void* sv, int64_
     d.bias = fc2_bias; d.bias_dtype = fc2_bias_dtype;
     d.base = base; d.ldbase = ldbase; d.base_dtype = base_dtype;
     d.alpha = alpha;
+    d.middle = middle;
     d.M = (int)M; d.E = (int)E; d.V = (int)V;
     d.out_ids = out_ids; d.out_score = out_score; d.ld_out = ld_out;
     return d;
@@ -583,8 +586,8 @@ static int check_domino_rollout(const dels_domino_rollout* p) {
     if (p->ld_base != 0 && p->ld_base < p->steps * p->V)
         return fail(DELS_ERR_INVALID_ARGUMENT, "rollout ld_base %lld < steps * V", (long long)p->ld_base);
     if ((rc = check_domino_step(p->z, p->steps * p->E, p->s, p->E, p->fc2_w, p->fc2_bias, p->fc2_bias_dtype, p->base,
-                                p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->alpha, p->batch, p->E,
-                                p->V, p->out_ids, p->steps)) != DELS_OK)
+                                p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->alpha, p->middle,
+                                p->batch, p->E, p->V, p->out_ids, p->steps)) != DELS_OK)
         return rc;
     const DominoLayout L = domino_layout(p->batch, p->steps, p->D, p->G, p->E);
     if (!skinny_supported(L.z_plan) || !skinny_supported(L.s_plan) || !skinny_supported(L.gru_plan))
@@ -649,7 +652,8 @@ static int enqueue_domino(const dels_domino_rollout* p, hipStream_t s) {
         const DominoArgs d = domino_args(static_cast<const char*>(p->z) + (size_t)t * E * 2, (int64_t)S * E, p->s, E,
                                          p->fc2_w, p->fc2_bias, p->fc2_bias_dtype,
                                          static_cast<const char*>(p->base) + (size_t)t * V * esz,
-                                         p->ld_base ? p->ld_base : (int64_t)S * V, p->base_dtype, p->alpha, B, E, V,
+                                         p->ld_base ? p->ld_base : (int64_t)S * V, p->base_dtype, p->alpha,
+                                         p->middle, B, E, V,
                                          p->out_ids + t, p->out_scores ? p->out_scores + t : nullptr, S);
         e = launch_domino_argmax(d, ws, s);
         if (e != hipSuccess) return hip_fail(e, "Domino step launch");
@@ -1199,15 +1203,15 @@ size_t dels_domino_argmax_ws_bytes(int64_t, int64_t, int64_t) { return kDataOff;
 
 int dels_domino_argmax(const void* z, int64_t ldz, const void* sv, int64_t lds, const void* fc2_w,
                        const void* fc2_bias, int fc2_bias_dtype, const void* base, int64_t ldbase, int base_dtype,
-                       float alpha, int64_t M, int64_t E, int64_t V, int64_t* out_ids, float* out_score,
+                       float alpha, int middle, int64_t M, int64_t E, int64_t V, int64_t* out_ids, float* out_score,
                        int64_t ld_out, void* ws, size_t ws_bytes, void* stream) {
-    int rc = check_domino_step(z, ldz, sv, lds, fc2_w, fc2_bias, fc2_bias_dtype, base, ldbase, base_dtype, alpha, M,
-                               E, V, out_ids, ld_out);
+    int rc = check_domino_step(z, ldz, sv, lds, fc2_w, fc2_bias, fc2_bias_dtype, base, ldbase, base_dtype, alpha,
+                               middle, M, E, V, out_ids, ld_out);
     if (rc != DELS_OK) return rc;
     if (M == 0) return DELS_OK;
     if ((rc = check_ws(ws, ws_bytes, kDataOff)) != DELS_OK) return rc;
     const DominoArgs d = domino_args(z, ldz, sv, lds, fc2_w, fc2_bias, fc2_bias_dtype, base, ldbase, base_dtype, alpha,
-                                     M, E, V, out_ids, out_score, ld_out);
+                                     middle, M, E, V, out_ids, out_score, ld_out);
     hipError_t e = launch_domino_argmax(d, ws, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? DELS_OK : hip_fail(e, "Domino step launch");
 }

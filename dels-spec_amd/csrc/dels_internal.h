@@ -45,7 +45,8 @@ constexpr size_t kDecodeOff = kCtrlBytes;
 
 // The rollout with B resident on chip (rollout_resident.hip): r = 256, G <= 1024,
 // batch <= 16, 64 .. 256 workgroups; its words {tag, two bf16} of the state
-// [16][G/2] and the rank [16][r/2], then the argmax slot words [2][16][nwg].
+// (16 rows x G/2 words at most) and of the rank (16 x r/2), each producer's
+// words on 128-byte lines of their own, then the argmax slot words [2][nwg][16].
 constexpr int kResidentRank = 256;
 constexpr int kResidentMaxG = 1024;
 constexpr int kResidentLdsTiles = 6;           // vocabulary tiles per workgroup in LDS beyond the registers
@@ -174,6 +175,7 @@ struct DominoArgs {
     const void* bias; int bias_dtype;          // fc2 bias [V] (nullptr: none), dtype code as base
     const void* base; int64_t ldbase; int base_dtype;
     float alpha;
+    int middle;                                // DELS_MIDDLE_*: the elementwise layer between fc1 and fc2
     int M, E, V;
     int64_t* out_ids; float* out_score; int64_t ld_out;
 };

@@ -1,10 +1,13 @@
-// Domino correction step: SiLU(z + s) . fc2^T (+ fc2 bias), scaled by the
+// Domino correction step: f(z + s) . fc2^T (+ fc2 bias), scaled by the
 // guidance alpha, plus the base logits, then the vocabulary argmax -- the
 // fused kernel of the Domino runner (code/kernel/domino.py:58-173: its
-// _fused_mlp_bias_argmax_kernel and _reduce_argmax_kernel in one launch).
+// _fused_mlp_bias_argmax_kernel and _reduce_argmax_kernel in one launch; f is
+// SiLU there, and any of the middle layers of DELS_MIDDLE_* here, which the
+// reference runs as its unfused step, 404-431).
 //
 // For row m (< 16 per row group) and vocabulary index v:
-//     mid[m, k] = p * sigmoid(p),  p = fp32(z[m, k]) + fp32(s[m, k])      (fp32, never rounded)
+//     mid[m, k] = f(p),  p = fp32(z[m, k]) + fp32(s[m, k])                (fp32, never rounded)
+//                 (SiLU: p * sigmoid(p))
 //     dot[m, v] = sum_k fp32(fc2[v, k]) * mid[m, k]                       (fp32 accumulate)
 //     score     = fma(dot (+ bias[v]), alpha, base[m, v])
 // and per row the lowest v attaining the maximum.
@@ -26,6 +29,7 @@
 #include <climits>
 #include <mutex>
 
+#include "../../include/dels.h"
 #include "dels_device.h"
 #include "dels_internal.h"
 #include "fused_argmax_gemv.h"
@@ -35,6 +39,43 @@ namespace dels {
 namespace {
 
 constexpr int kDomKC = 16;   // K steps (of 32) per register set
+
+// The middle layer f of the correction MLP in fp32 (DELS_MIDDLE_*; `middle` is
+// uniform over the launch).  GELU is x/2 (1 + erf(x / sqrt 2)) and its tanh
+// form x/2 (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), as nn.GELU defines them.
+template <int MIDDLE>
+__device__ __forceinline__ float domino_middle(float p) {
+#pragma clang fp contract(off)
+    if constexpr (MIDDLE == DELS_MIDDLE_IDENTITY) return p;
+    else if constexpr (MIDDLE == DELS_MIDDLE_RELU) return p > 0.f ? p : (p == p ? 0.f : p);
+    else if constexpr (MIDDLE == DELS_MIDDLE_GELU) return 0.5f * p * (1.f + erff(p * 0.70710678118654752f));
+    else if constexpr (MIDDLE == DELS_MIDDLE_GELU_TANH)
+        return 0.5f * p * (1.f + tanhf(0.79788456080286536f * (p + 0.044715f * (p * p * p))));
+    else if constexpr (MIDDLE == DELS_MIDDLE_TANH) return tanhf(p);
+    else if constexpr (MIDDLE == DELS_MIDDLE_SIGMOID) return sigmoid_f32(p);
+    else return p * sigmoid_f32(p);   // DELS_MIDDLE_SILU
+}
+
+// mid = f(z + s) of the 16 rows m0 .. m0 + 15 into the hi/lo operand layout in
+// LDS (see the kernel); one loop per middle layer, so none carries a branch on it.
+template <int MIDDLE>
+__device__ __forceinline__ void domino_fill_operands(const DominoArgs& a, int m0, int kpad, uint16_t* ops) {
+#pragma clang fp contract(off)
+    for (int i = threadIdx.x; i < 16 * kpad; i += 256) {
+        const int row = i / kpad, k = i - row * kpad;
+        const int m = m0 + row;
+        float mid = 0.f;
+        if (m < a.M && k < a.E) {
+            const float p = bf16_bits_to_f32(a.z[(int64_t)m * a.ldz + k]) + bf16_bits_to_f32(a.s[(int64_t)m * a.lds + k]);
+            mid = domino_middle<MIDDLE>(p);
+        }
+        const uint16_t hi = f32_to_bf16_bits(mid);
+        const uint16_t lo = f32_to_bf16_bits(mid - bf16_bits_to_f32(hi));
+        const int ks = k >> 5, ln = row + 16 * ((k & 31) >> 3), e = k & 7;
+        ops[((ks * 2 + 0) * 64 + ln) * 8 + e] = hi;
+        ops[((ks * 2 + 1) * 64 + ln) * 8 + e] = lo;
+    }
+}
 
 template <typename BaseT, typename BiasT>
 struct DomRegs {
@@ -58,26 +99,21 @@ __global__ __launch_bounds__(256) void domino_argmax_kernel(DominoArgs a, Argmax
     const int m0 = blockIdx.y * 16;
     const int ksteps = a.E / 32;
 
-    // mid = SiLU(z + s) of the 16 rows, split into bf16 hi/lo A operands: K step
+    // mid = f(z + s) of the 16 rows, split into bf16 hi/lo A operands: K step
     // ks, part p (0 hi, 1 lo) is the KiB at ((ks * 2 + p) * 64 + lane) * 16 with
     // lane = row + 16 * (k % 32 / 8), element k % 8.  K is padded with zeros to
     // whole register sets (and rows past M are zero), so the contraction below
     // runs every step of a set unconditionally: padded steps multiply zeros.
     uint16_t* ops = reinterpret_cast<uint16_t*>(dyn_lds);
     const int kpad = ((ksteps + kDomKC - 1) / kDomKC) * kDomKC * 32;
-    for (int i = threadIdx.x; i < 16 * kpad; i += 256) {
-        const int row = i / kpad, k = i - row * kpad;
-        const int m = m0 + row;
-        float mid = 0.f;
-        if (m < a.M && k < a.E) {
-            const float p = bf16_bits_to_f32(a.z[(int64_t)m * a.ldz + k]) + bf16_bits_to_f32(a.s[(int64_t)m * a.lds + k]);
-            mid = p * sigmoid_f32(p);
-        }
-        const uint16_t hi = f32_to_bf16_bits(mid);
-        const uint16_t lo = f32_to_bf16_bits(mid - bf16_bits_to_f32(hi));
-        const int ks = k >> 5, ln = row + 16 * ((k & 31) >> 3), e = k & 7;
-        ops[((ks * 2 + 0) * 64 + ln) * 8 + e] = hi;
-        ops[((ks * 2 + 1) * 64 + ln) * 8 + e] = lo;
+    switch (a.middle) {   // uniform
+        case DELS_MIDDLE_IDENTITY: domino_fill_operands<DELS_MIDDLE_IDENTITY>(a, m0, kpad, ops); break;
+        case DELS_MIDDLE_RELU: domino_fill_operands<DELS_MIDDLE_RELU>(a, m0, kpad, ops); break;
+        case DELS_MIDDLE_GELU: domino_fill_operands<DELS_MIDDLE_GELU>(a, m0, kpad, ops); break;
+        case DELS_MIDDLE_GELU_TANH: domino_fill_operands<DELS_MIDDLE_GELU_TANH>(a, m0, kpad, ops); break;
+        case DELS_MIDDLE_TANH: domino_fill_operands<DELS_MIDDLE_TANH>(a, m0, kpad, ops); break;
+        case DELS_MIDDLE_SIGMOID: domino_fill_operands<DELS_MIDDLE_SIGMOID>(a, m0, kpad, ops); break;
+        default: domino_fill_operands<DELS_MIDDLE_SILU>(a, m0, kpad, ops); break;
     }
     __syncthreads();
 

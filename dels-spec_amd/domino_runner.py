@@ -9,7 +9,7 @@ guidance_alpha=None) -> int64[B, steps]`` returning a fresh tensor, and the
 
 The rollout (code/kernel/domino.py:379-436) -- the hidden-state half of the
 correction MLP's first layer for all steps at once, the GRU over the prefix
-ids, then per step the GRU-state half, the fused SiLU/fc2/alpha/base argmax
+ids, then per step the GRU-state half, the fused middle/fc2/alpha/base argmax
 and a GRU step on the chosen id -- is captured once through the C ABI
 (``dels_domino_graph_create``) and replayed per call.
 
@@ -17,8 +17,12 @@ Differences from the reference, both from running every layer on the same
 kernels: the prefix GRU runs as one table-gather GRU cell per prefix id (the
 reference calls ``nn.GRU`` on the prefix embeddings, whose internal precision
 the library chooses; every later step of the reference uses the same cell as
-here), and only a SiLU middle layer is supported (the reference's fused path
-also requires it; for other middles it runs an unfused eager path).
+here); and the middle layer of the correction MLP is fused whatever it is
+among SiLU, Identity, ReLU, GELU (erf or tanh), Tanh and Sigmoid, in fp32 --
+the reference fuses SiLU only and runs the others as an unfused eager step
+in the model's dtype (code/kernel/domino.py:404-431), so for those its
+scores are bf16-rounded where these are not.  Other middle modules are
+refused.
 """
 
 from __future__ import annotations
@@ -51,10 +55,33 @@ def unwrap_correction_mlp(embed_proj: nn.Module) -> tuple[nn.Linear, nn.Module, 
 
 
 def _is_silu(middle: nn.Module) -> bool:
+    return middle_name(middle) == "silu"
+
+
+def middle_name(middle: nn.Module) -> str | None:
+    """The fused kernel's name (``_lib.MIDDLE_CODES``) of the correction MLP's
+    middle layer -- a single elementwise module, or a Sequential of one or none
+    -- or None when it is not one the kernel fuses."""
+    if isinstance(middle, nn.Sequential):
+        kids = list(middle.children())
+        if not kids:
+            return "identity"
+        if len(kids) != 1:
+            return None
+        middle = kids[0]
     if isinstance(middle, nn.SiLU):
-        return True
-    kids = list(middle.children()) if isinstance(middle, nn.Sequential) else []
-    return len(kids) == 1 and isinstance(kids[0], nn.SiLU)
+        return "silu"
+    if isinstance(middle, nn.Identity):
+        return "identity"
+    if isinstance(middle, nn.ReLU):
+        return "relu"
+    if isinstance(middle, nn.GELU):
+        return {"none": "gelu", "tanh": "gelu_tanh"}.get(middle.approximate)
+    if isinstance(middle, nn.Tanh):
+        return "tanh"
+    if isinstance(middle, nn.Sigmoid):
+        return "sigmoid"
+    return None
 
 
 class DraftCorrectionGraphRunner:
@@ -84,10 +111,11 @@ class DraftCorrectionGraphRunner:
                 f"Correction MLP input dim mismatch: got {fc1.in_features}, "
                 f"expected {expected_in} = hidden_dim + gru_hidden_dim.")
         self._middle_is_silu = _is_silu(self.middle)
-        self._can_triton_fuse = self._middle_is_silu
-        if not self._middle_is_silu:
-            raise ValueError("The native Domino runner fuses a SiLU middle layer only "
-                             f"(embed_proj middle is {type(self.middle).__name__}).")
+        self._middle = middle_name(self.middle)
+        self._can_triton_fuse = self._middle is not None
+        if self._middle is None:
+            raise ValueError("The native Domino runner fuses a middle layer of SiLU, Identity, ReLU, GELU, "
+                             f"Tanh or Sigmoid (embed_proj middle is {self.middle!r}).")
         gru = draft_model.prefix_gru
         if gru.num_layers != 1 or gru.bidirectional:
             raise AssertionError("Domino graph runner supports only a single unidirectional GRU.")
@@ -189,6 +217,7 @@ class DraftCorrectionGraphRunner:
         p.h_a, p.h_b = self._h_a.data_ptr(), self._h_b.data_ptr()
         p.z, p.s = self._z.data_ptr(), self._s.data_ptr()
         p.ws, p.ws_bytes = self._ws.data_ptr(), self._ws.numel()
+        p.middle = _lib.MIDDLE_CODES[self._middle]
         return p
 
     def replay(self) -> None:

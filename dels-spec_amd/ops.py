@@ -458,14 +458,18 @@ def lm_head(hidden: torch.Tensor, weight: Weight, *, out: Optional[torch.Tensor]
 
 
 def domino_argmax(z: torch.Tensor, s: torch.Tensor, fc2_weight: Weight, base_logits: torch.Tensor,
-                  guidance_alpha: float, fc2_bias: Optional[torch.Tensor] = None, *,
+                  guidance_alpha: float, fc2_bias: Optional[torch.Tensor] = None, *, middle: str = "silu",
                   out_ids: Optional[torch.Tensor] = None,
                   out_score: Optional[torch.Tensor] = None) -> tuple[torch.Tensor, torch.Tensor]:
-    """One Domino correction step (code/kernel/domino.py:58-173, 438-482):
-    ``argmax_v fma(SiLU(z + s) . fc2[v] (+ fc2_bias[v]), alpha, base[v])`` per row, with
-    ``SiLU(z + s)`` kept in fp32.  ``z``, ``s`` [M, E] bf16 (any row stride);
+    """One Domino correction step (code/kernel/domino.py:58-173, 404-431, 438-482):
+    ``argmax_v fma(f(z + s) . fc2[v] (+ fc2_bias[v]), alpha, base[v])`` per row, with
+    ``f(z + s)`` kept in fp32; ``f`` is the correction MLP's middle layer, one of
+    ``silu`` (the reference's fused case), ``identity``, ``relu``, ``gelu``,
+    ``gelu_tanh``, ``tanh``, ``sigmoid``.  ``z``, ``s`` [M, E] bf16 (any row stride);
     ``fc2_weight`` [V, E] (a ``PackedWeight``, or a bf16 matrix packed on the fly);
     ``base_logits`` [M, V].  Returns ``(ids int64[M], score fp32[M])``."""
+    if middle not in _lib.MIDDLE_CODES:
+        raise ValueError(f"middle must be one of {sorted(_lib.MIDDLE_CODES)}, got {middle!r}")
     _require_bf16_matrix(z, "z")
     M, E = z.shape
     _require_bf16_matrix(s, "s", rows=M, cols=E)
@@ -486,8 +490,8 @@ def domino_argmax(z: torch.Tensor, s: torch.Tensor, fc2_weight: Weight, base_log
     _lib.check(lib.dels_domino_argmax(
         z.data_ptr(), z.stride(0), s.data_ptr(), s.stride(0), fc2_weight.data.data_ptr(),
         bias.data_ptr() if bias is not None else None, _DTYPES[bias.dtype] if bias is not None else 0,
-        base.data_ptr(), base.stride(0), _DTYPES[base.dtype], float(guidance_alpha), M, E, V,
-        out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(), _stream_ptr(dev)),
+        base.data_ptr(), base.stride(0), _DTYPES[base.dtype], float(guidance_alpha), _lib.MIDDLE_CODES[middle],
+        M, E, V, out_ids.data_ptr(), out_score.data_ptr(), ld_out, ws.data_ptr(), ws.numel(), _stream_ptr(dev)),
         "dels_domino_argmax")
     return out_ids, out_score
 

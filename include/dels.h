@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define DELS_ABI_VERSION 2
+#define DELS_ABI_VERSION 3
 
 /* status codes */
 #define DELS_OK 0
@@ -70,6 +70,22 @@ extern "C" {
 /* rank activations (code/dels.py:14) */
 #define DELS_ACT_IDENTITY 0
 #define DELS_ACT_SILU 1
+
+/*
+ * Middle layer of the Domino correction MLP (the layers between fc1 and fc2 of
+ * embed_proj, code/kernel/domino.py:15-51, 404-431), applied elementwise in
+ * fp32 to p = z + s.  SILU is the reference's fused case (0, so a zeroed
+ * rollout struct keeps it); the others are the modules its unfused step runs:
+ * nn.Identity, nn.ReLU, nn.GELU() (erf), nn.GELU(approximate="tanh"),
+ * nn.Tanh, nn.Sigmoid.
+ */
+#define DELS_MIDDLE_SILU 0
+#define DELS_MIDDLE_IDENTITY 1
+#define DELS_MIDDLE_RELU 2
+#define DELS_MIDDLE_GELU 3
+#define DELS_MIDDLE_GELU_TANH 4
+#define DELS_MIDDLE_TANH 5
+#define DELS_MIDDLE_SIGMOID 6
 
 /*
  * Weight layouts.  DELS_LAYOUT_ROWMAJOR: [rows, cols] row-major with a leading
@@ -391,7 +407,8 @@ int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int6
  * code/kernel/domino.py:58-173, 438-482): for rows m < M of z and s [M, E]
  * bf16 (the hidden-state and GRU-state parts of the correction MLP's first
  * layer),
- *   mid[m, k] = p * sigmoid(p),  p = fp32(z[m, k]) + fp32(s[m, k])   (fp32)
+ *   mid[m, k] = f(p),  p = fp32(z[m, k]) + fp32(s[m, k])   (fp32; f the
+ *               middle layer, DELS_MIDDLE_*: SILU is p * sigmoid(p))
  *   dot[m, v] = fp32(mid[m] . fc2[v])   (+ fc2_bias[v] when given)
  *   id_m = lowest argmax_v fma(dot[m, v], alpha, base[m, v]).
  * fc2 [V, E] bf16 in the MFMA-16 layout (dels_pack_operand); E a multiple of
@@ -402,7 +419,7 @@ int dels_lm_head(const void* hidden, int64_t ldh, const void* W, int64_t M, int6
 size_t dels_domino_argmax_ws_bytes(int64_t M, int64_t E, int64_t V);
 int dels_domino_argmax(const void* z, int64_t ldz, const void* s, int64_t lds, const void* fc2_w,
                        const void* fc2_bias, int fc2_bias_dtype,
-                       const void* base, int64_t ldbase, int base_dtype, float alpha,
+                       const void* base, int64_t ldbase, int base_dtype, float alpha, int middle,
                        int64_t M, int64_t E, int64_t V,
                        int64_t* out_ids, float* out_score, int64_t ld_out,
                        void* ws, size_t ws_bytes, void* stream);
@@ -445,6 +462,7 @@ typedef struct dels_domino_rollout {
     void* s;                /* [batch, E] bf16 scratch */
     void* ws;
     size_t ws_bytes;
+    int middle;             /* DELS_MIDDLE_* of the correction MLP's middle layer (0: SiLU) */
 } dels_domino_rollout;
 
 size_t dels_domino_rollout_ws_bytes(int64_t batch, int64_t steps, int64_t D, int64_t G, int64_t E, int64_t V);

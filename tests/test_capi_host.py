@@ -55,7 +55,7 @@ def test_rollout_struct_layout_matches_header(pkg):
 
 def test_abi_version_and_strerror(pkg):
     lib = pkg._lib.load()
-    assert lib.dels_abi_version() == pkg._lib.ABI_VERSION == 2
+    assert lib.dels_abi_version() == pkg._lib.ABI_VERSION == 3
     assert lib.dels_strerror(0) == b"success"
     assert lib.dels_strerror(-3) == b"misaligned operand"
     assert lib.dels_strerror(-99) == b"unknown status"
@@ -125,6 +125,14 @@ def test_argument_errors_return_codes(pkg):
     assert rc == -1 and b"layout" in lib.dels_last_error()
     assert lib.dels_packed_bytes(17, 40) == 2 * 2 * 1024
     assert lib.dels_pack_operand(0x1000, 40, 17, 40, 0x8000, 1024, None) == -1
+    # Domino step: an unknown middle layer code (DELS_MIDDLE_*) is refused before any operand is read
+    for bad in (-1, 7):
+        rc = lib.dels_domino_argmax(0x1000, 64, 0x2000, 64, 0x3000, None, 0, 0x4000, 100, 0, 1.0, bad, 2, 64, 100,
+                                    0x5000, None, 1, 0x6000, 1 << 20, None)
+        assert rc == -1 and b"middle layer" in lib.dels_last_error()
+    q = pkg._lib.DominoRolloutParams()
+    q.steps, q.batch, q.prefix_len, q.middle = 1, 1, 1, 9
+    assert lib.dels_domino_rollout_enqueue(ctypes.byref(q), None) != 0
 
 
 def test_python_errors_before_the_gpu(pkg):

@@ -38,6 +38,26 @@ def test_domino_step_matches_oracle(pkg, dev, M, E, V, bias_dt, base_dt):
     assert res["id_mismatch_pinned"] == 0 and res["score_bad"] == 0, res
 
 
+@pytest.mark.parametrize("middle,M,E,V", [(m, 8, 512, 30011) for m in DO.MIDDLES if m != "silu"] +
+                         [("gelu", 16, 1024, 151936)])
+def test_domino_step_middle_layers_match_oracle(pkg, dev, middle, M, E, V):
+    """The fused step with each middle layer of the correction MLP that the reference runs as
+    its unfused step (code/kernel/domino.py:404-431), against the oracle's fp32 formula."""
+    print(f"case domino step middle={middle} M={M} E={E} V={V}", flush=True)
+    g = torch.Generator().manual_seed(M * 5 + E + len(middle))
+    z = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    s = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    fc2 = (torch.randn(V, E, generator=g) * 0.1).to(torch.bfloat16)   # the MLP term outweighs base
+    base = (torch.randn(M, V, generator=g) * 3).to(torch.bfloat16)
+    bias = torch.randn(V, generator=g).to(torch.bfloat16)
+    ids, score = pkg.domino_argmax(z.to(dev), s.to(dev), pkg.pack_operand(fc2.to(dev)), base.to(dev), 0.9,
+                                   bias.to(dev), middle=middle)
+    torch.cuda.synchronize()
+    rid, rbest, rsec = DO.domino_step(_f(z), _f(s), _f(fc2), _f(bias), _f(base), 0.9, middle=middle)
+    res = oracle.check_parity(ids.cpu().numpy(), score.cpu().numpy(), rid, rbest, rsec, score_atol=1e-4)
+    assert res["id_mismatch_pinned"] == 0 and res["score_bad"] == 0, res
+
+
 def test_domino_step_strided_inputs_and_outputs(pkg, dev):
     g = torch.Generator().manual_seed(3)
     M, E, V = 6, 128, 5000
@@ -57,9 +77,10 @@ def test_domino_step_strided_inputs_and_outputs(pkg, dev):
 
 
 class _Draft(nn.Module):
-    def __init__(self, D, G, E, V, fc1_bias, fc2_bias, g, gru_bias=False):
+    def __init__(self, D, G, E, V, fc1_bias, fc2_bias, g, gru_bias=False, middle=None):
         super().__init__()
-        self.embed_proj = nn.Sequential(nn.Linear(D + G, E, bias=fc1_bias), nn.SiLU(), nn.Linear(E, V, bias=fc2_bias))
+        self.embed_proj = nn.Sequential(nn.Linear(D + G, E, bias=fc1_bias), middle if middle is not None else nn.SiLU(),
+                                        nn.Linear(E, V, bias=fc2_bias))
         self.prefix_gru = nn.GRU(D, G, num_layers=1, batch_first=True, bias=gru_bias)
         with torch.no_grad():
             for p in self.parameters():
@@ -75,17 +96,22 @@ class _Target(nn.Module):
             self.model.embed_tokens.weight.copy_(torch.randn(V, D, generator=g))
 
 
-@pytest.mark.parametrize("B,S,P,D,G,E,V,fc1_bias,fc2_bias,gru_bias", [
-    (2, 6, 2, 256, 128, 256, 3001, True, True, False),
-    (1, 14, 2, 4096, 1024, 1024, 151936, False, False, False),
-    (3, 5, 3, 512, 256, 512, 20011, True, False, True),     # GRU with b_ih and b_hh
+@pytest.mark.parametrize("B,S,P,D,G,E,V,fc1_bias,fc2_bias,gru_bias,middle", [
+    (2, 6, 2, 256, 128, 256, 3001, True, True, False, "silu"),
+    (1, 14, 2, 4096, 1024, 1024, 151936, False, False, False, "silu"),
+    (3, 5, 3, 512, 256, 512, 20011, True, False, True, "silu"),     # GRU with b_ih and b_hh
+    (2, 6, 2, 256, 128, 256, 3001, True, True, False, "gelu"),      # middles the reference runs unfused
+    (3, 5, 2, 512, 256, 512, 20011, True, False, True, "gelu_tanh"),
+    (2, 4, 2, 256, 128, 256, 3001, False, True, False, "relu"),
 ])
-def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, fc2_bias, gru_bias):
+def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, fc2_bias, gru_bias, middle):
     """The hipGraph rollout against the oracle's, fed the device's own ids (each step is then
     checked on its own history): ids under the margin rule, scores within 1e-3."""
-    print(f"case domino rollout B={B} S={S} P={P} D={D} G={G} E={E} V={V} gru_bias={gru_bias}", flush=True)
+    print(f"case domino rollout B={B} S={S} P={P} D={D} G={G} E={E} V={V} gru_bias={gru_bias} middle={middle}",
+          flush=True)
     g = torch.Generator().manual_seed(11 + V)
-    draft = _Draft(D, G, E, V, fc1_bias, fc2_bias, g, gru_bias).to(torch.bfloat16)
+    module = {"silu": nn.SiLU(), "gelu": nn.GELU(), "gelu_tanh": nn.GELU(approximate="tanh"), "relu": nn.ReLU()}
+    draft = _Draft(D, G, E, V, fc1_bias, fc2_bias, g, gru_bias, module[middle]).to(torch.bfloat16)
     target = _Target(V, D, g).to(torch.bfloat16)
     runner = pkg.DraftCorrectionGraphRunner(draft_model=draft.to(dev), target_model=target.to(dev), batch_size=B,
                                             steps=S, hidden_dim=D, gru_hidden_dim=G, vocab_size=V,
@@ -106,7 +132,7 @@ def test_runner_rollout_teacher_forced(pkg, dev, B, S, P, D, G, E, V, fc1_bias, 
         w_z=W1[:, :D], fc1_bias=None if not fc1_bias else _f(draft.embed_proj[0].bias), w_s=W1[:, D:],
         fc2=_f(draft.embed_proj[2].weight), fc2_bias=None if not fc2_bias else _f(draft.embed_proj[2].bias),
         alpha=0.8, embed=_f(target.model.embed_tokens.weight), W_ih=_f(draft.prefix_gru.weight_ih_l0),
-        forced_ids=ids)
+        forced_ids=ids, middle=middle)
     scores = runner.static_scores.cpu().numpy()
     res = oracle.check_parity(ids.reshape(-1), scores.reshape(-1), ref_ids.reshape(-1), ref_sc.reshape(-1),
                               ref_sec.reshape(-1), score_atol=1e-3)

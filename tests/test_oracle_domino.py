@@ -13,9 +13,14 @@ def _bf16(t):
     return t.to(torch.bfloat16).float()
 
 
-def _mlp(D, G, E, V, fc2_bias, seed):
+# the middle layers the kernels fuse, as the torch modules a model would hold
+MIDDLE_MODULES = {"silu": nn.SiLU(), "identity": nn.Identity(), "relu": nn.ReLU(), "gelu": nn.GELU(),
+                  "gelu_tanh": nn.GELU(approximate="tanh"), "tanh": nn.Tanh(), "sigmoid": nn.Sigmoid()}
+
+
+def _mlp(D, G, E, V, fc2_bias, seed, middle="silu"):
     g = torch.Generator().manual_seed(seed)
-    mlp = nn.Sequential(nn.Linear(D + G, E, bias=False), nn.SiLU(), nn.Linear(E, V, bias=fc2_bias))
+    mlp = nn.Sequential(nn.Linear(D + G, E, bias=False), MIDDLE_MODULES[middle], nn.Linear(E, V, bias=fc2_bias))
     with torch.no_grad():
         mlp[0].weight.copy_(_bf16(torch.randn(E, D + G, generator=g) * 0.05))
         mlp[2].weight.copy_(_bf16(torch.randn(V, E, generator=g) * 0.05))
@@ -24,13 +29,15 @@ def _mlp(D, G, E, V, fc2_bias, seed):
     return mlp
 
 
-@pytest.mark.parametrize("fc2_bias", [False, True])
-def test_step_matches_torch_modules(fc2_bias):
-    """The reference's unfused formula on torch modules in fp32 (code/dflash.py:619-626):
-    base + alpha * embed_proj(cat[z_h, s_h]) -- against the oracle fed with the two halves
-    of the first layer, under the margin rule."""
+@pytest.mark.parametrize("fc2_bias,middle", [(False, "silu"), (True, "silu")] +
+                         [(True, m) for m in DO.MIDDLES if m != "silu"])
+def test_step_matches_torch_modules(fc2_bias, middle):
+    """The reference's unfused formula on torch modules in fp32 (code/dflash.py:619-626,
+    code/kernel/domino.py:404-431): base + alpha * embed_proj(cat[z_h, s_h]) with the given
+    middle module -- against the oracle fed with the two halves of the first layer, under
+    the margin rule."""
     D, G, E, V, M, alpha = 48, 32, 64, 997, 9, 0.8
-    mlp = _mlp(D, G, E, V, fc2_bias, seed=1)
+    mlp = _mlp(D, G, E, V, fc2_bias, seed=1, middle=middle)
     g = torch.Generator().manual_seed(2)
     zh, sh = torch.randn(M, D, generator=g), torch.randn(M, G, generator=g)
     base = torch.randn(M, V, generator=g) * 3
@@ -41,9 +48,39 @@ def test_step_matches_torch_modules(fc2_bias):
     z = (zh.double() @ torch.tensor(W1[:, :D]).double().T).float().numpy()
     s = (sh.double() @ torch.tensor(W1[:, D:]).double().T).float().numpy()
     bias = mlp[2].bias.detach().numpy() if fc2_bias else None
-    ids, best, second = DO.domino_step(z, s, mlp[2].weight.detach().numpy(), bias, base.numpy(), alpha)
+    ids, best, second = DO.domino_step(z, s, mlp[2].weight.detach().numpy(), bias, base.numpy(), alpha,
+                                       middle=middle)
     res = oracle.check_parity(want, logits.gather(1, torch.tensor(want)[:, None])[:, 0].numpy(), ids, best, second)
     assert res["id_mismatch_pinned"] == 0 and res["score_bad"] == 0, res
+
+
+@pytest.mark.parametrize("middle", [m for m in DO.MIDDLES if m != "silu"])
+def test_middle_layers_match_torch_modules_elementwise(middle):
+    """Each middle layer of the oracle against its torch module evaluated in float64 on the
+    same fp32 inputs (ordinary values, zeros, large magnitudes): equal after rounding to fp32
+    within one fp32 ulp, or 1e-12 absolute (the two float64 formulas may differ in their last
+    bits, and the tanh form of GELU cancels to ~1e-16 for large negative inputs)."""
+    rng = np.random.default_rng(11)
+    p = np.concatenate([rng.standard_normal(4000) * 3, [0.0, -0.0, 1e-30, -1e-30, 12.5, -12.5, 40.0, -40.0]])
+    p = p.astype(np.float32)
+    got = DO.domino_mid(p, np.zeros_like(p), middle)
+    want = MIDDLE_MODULES[middle](torch.tensor(p, dtype=torch.float64)).numpy().astype(np.float32)
+    np.testing.assert_allclose(got, want, rtol=1.2e-7, atol=1e-12)
+    # a planted mistake the check must see: GELU with x / 2 for the erf argument instead of x / sqrt(2)
+    if middle == "gelu":
+        from scipy.special import erf
+        wrong = (0.5 * p.astype(np.float64) * (1 + erf(p.astype(np.float64) / 2))).astype(np.float32)
+        assert not np.allclose(wrong, want, rtol=1.2e-7, atol=1e-12)
+
+
+def test_middle_name_of_modules(pkg):
+    """The runner's map from the correction MLP's middle modules to the fused kernel's codes."""
+    from importlib import import_module
+    mn = import_module(pkg.__name__ + ".domino_runner").middle_name
+    for name, mod in MIDDLE_MODULES.items():
+        assert mn(mod) == name and mn(nn.Sequential(mod)) == name
+    assert mn(nn.Sequential()) == "identity"
+    assert mn(nn.LeakyReLU()) is None and mn(nn.Sequential(nn.SiLU(), nn.Dropout())) is None
 
 
 def test_step_closed_forms():
@@ -142,7 +179,7 @@ class _Target(nn.Module):
     (nn.Sequential(nn.SiLU(), nn.Linear(48, 64)), ValueError, "first layer must be nn.Linear"),
     (nn.Sequential(nn.Linear(48, 64), nn.SiLU()), ValueError, "last layer must be nn.Linear"),
     (nn.Sequential(nn.Linear(40, 64), nn.SiLU(), nn.Linear(64, 64)), ValueError, "input dim mismatch"),
-    (nn.Sequential(nn.Linear(48, 64), nn.GELU(), nn.Linear(64, 64)), ValueError, "SiLU middle"),
+    (nn.Sequential(nn.Linear(48, 64), nn.LeakyReLU(), nn.Linear(64, 64)), ValueError, "fuses a middle layer"),
 ])
 def test_runner_argument_checks(pkg, embed_proj, exc, msg):
     """The reference's checks and messages (code/kernel/domino.py:15-51, 268-275), raised before
