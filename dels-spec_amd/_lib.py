@@ -53,6 +53,7 @@ class RolloutParams(ctypes.Structure):
         ("h_a", _ptr), ("h_b", _ptr),
         ("rank", _ptr),
         ("ws", _ptr), ("ws_bytes", _sz),
+        ("ld_prefix", _i64), ("ld_out", _i64),
     ]
 
 

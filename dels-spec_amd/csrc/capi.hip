@@ -218,6 +218,11 @@ static int check_rollout(const dels_rollout* p) {
         return fail(DELS_ERR_UNSUPPORTED, "rollout: steps and r below 2^24, V below 2^31-1");
     if (p->act != DELS_ACT_IDENTITY && p->act != DELS_ACT_SILU)
         return fail(DELS_ERR_INVALID_ARGUMENT, "unknown rank activation %d", p->act);
+    if (p->ld_prefix < 0 || !ld_ok({p->ld_prefix, p->ld_out}))
+        return fail(DELS_ERR_INVALID_ARGUMENT, "rollout ld_prefix / ld_out out of range");
+    if (p->ld_out != 0 && p->ld_out < p->steps)
+        return fail(DELS_ERR_INVALID_ARGUMENT, "rollout ld_out %lld < steps %lld", (long long)p->ld_out,
+                    (long long)p->steps);
     int rc = check_gru_args(p->gi_table, p->ld_gi, p->table_rows, p->prefix_ids, p->h_a, p->G, p->w_hh,
                             p->weights_layout, p->batch, p->G, p->h_b, p->G);
     if (rc != DELS_OK) return rc;
@@ -228,7 +233,7 @@ static int check_rollout(const dels_rollout* p) {
     if ((rc = check_argmax_args(p->rank, p->r, p->lm_w, p->r, p->weights_layout, p->base,
                                 p->ld_base ? p->ld_base : p->steps * p->V, p->base_dtype, p->prior,
                                 p->prior_dtype, p->alpha, 0, p->beta, 0, p->batch, p->r, p->V, p->out_ids,
-                                p->steps, true)) != DELS_OK)
+                                p->ld_out ? p->ld_out : p->steps, true)) != DELS_OK)
         return rc;
     const RolloutLayout L = rollout_layout(p->batch, p->G, p->r, p->V);
     if (!skinny_supported(L.rank_plan) || !skinny_supported(L.gru_plan))
@@ -240,6 +245,8 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     const RolloutLayout L = rollout_layout(p->batch, p->G, p->r, p->V);
     char* ws = static_cast<char*>(p->ws);
     const int B = (int)p->batch, G = (int)p->G, r = (int)p->r, V = (int)p->V;
+    const int64_t ldp = p->ld_prefix ? p->ld_prefix : 1;         // prefix id of row b at [b * ldp]
+    const int64_t ldo = p->ld_out ? p->ld_out : p->steps;        // id of row b, step s at [b * ldo + s]
 
     GruArgs g{};
     g.gi_table = static_cast<const uint16_t*>(p->gi_table);
@@ -263,13 +270,13 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         ra.act = p->act;
         ra.B = static_cast<const uint16_t*>(p->lm_w);
         ra.gi_table = g.gi_table; ra.ld_gi = g.ld_gi; ra.table_rows = g.table_rows;
-        ra.prefix = p->prefix_ids;
+        ra.prefix = p->prefix_ids; ra.ld_prefix = ldp;
         ra.base = p->base; ra.ld_base = p->ld_base ? p->ld_base : p->steps * (int64_t)V;
         ra.base_dtype = p->base_dtype;
         ra.prior = p->prior; ra.prior_dtype = p->prior_dtype;
         ra.alpha = p->alpha; ra.beta = p->beta;
         ra.batch = B; ra.G = G; ra.V = V; ra.steps = p->steps;
-        ra.out_ids = p->out_ids; ra.out_scores = p->out_scores;
+        ra.out_ids = p->out_ids; ra.out_scores = p->out_scores; ra.ld_out = ldo;
         hipError_t e = launch_rollout_resident(ra, ws, s);
         return e == hipSuccess ? DELS_OK : hip_fail(e, "resident rollout launch");
     }
@@ -281,7 +288,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
     if (!fuse_gru) {
         // h0 = GRU(gi_table[prefix], 0)   (code/kernel/dels.py:426-433)
         g.tokens = p->prefix_ids;
-        g.tok_stride = 1;
+        g.tok_stride = ldp;
         g.h_in = nullptr;
         g.ldh_in = G;
         g.h_out = h_cur;
@@ -311,7 +318,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
         aa.M = B; aa.r = r; aa.V = V;
         aa.out_ids = p->out_ids + step;
         aa.out_score = p->out_scores ? p->out_scores + step : nullptr;
-        aa.ld_out = p->steps;
+        aa.ld_out = ldo;
 
         if (fuse_gru) {
             // h = GRU(gi_table[previous ids], h) -- step 0: GRU(gi_table[prefix], 0)
@@ -320,11 +327,11 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
             dg.gi_table = g.gi_table; dg.ld_gi = g.ld_gi; dg.table_rows = g.table_rows;
             dg.w_hh = g.w_hh; dg.b_hh = g.b_hh;
             if (step == 0) {
-                dg.tokens = p->prefix_ids; dg.tok_stride = 1;
+                dg.tokens = p->prefix_ids; dg.tok_stride = ldp;
                 dg.h_prev = nullptr; dg.h_out = h_cur;
                 ra.h = h_cur;
             } else {
-                dg.tokens = p->out_ids + (step - 1); dg.tok_stride = p->steps;
+                dg.tokens = p->out_ids + (step - 1); dg.tok_stride = ldo;
                 dg.h_prev = h_cur; dg.h_out = h_next;
                 ra.h = h_next;
             }
@@ -344,7 +351,7 @@ static int enqueue_rollout(const dels_rollout* p, hipStream_t s) {
 
         if (step + 1 < p->steps && !fuse_gru) {
             g.tokens = p->out_ids + step;
-            g.tok_stride = p->steps;
+            g.tok_stride = ldo;
             g.h_in = h_cur;
             g.h_out = h_next;
             e = launch_gru_step(g, L.gru_plan, ws, L.part_off, s);

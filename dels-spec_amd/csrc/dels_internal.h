@@ -196,12 +196,12 @@ struct ResidentRolloutArgs {
     const uint16_t* A; const uint16_t* rank_b; int act;
     const uint16_t* B;
     const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
-    const int64_t* prefix;
+    const int64_t* prefix; int64_t ld_prefix;
     const void* base; int64_t ld_base; int base_dtype;
     const void* prior; int prior_dtype;
     const float* alpha; const float* beta;
     int64_t batch, G, V, steps;
-    int64_t* out_ids; float* out_scores;
+    int64_t* out_ids; float* out_scores; int64_t ld_out;   // row m, step s at [m * ld_out + s]
 };
 bool rollout_resident_eligible(int64_t batch, int64_t G, int64_t r, int64_t V, int64_t steps, bool packed);
 hipError_t launch_rollout_resident(const ResidentRolloutArgs& a, void* ws, hipStream_t s);

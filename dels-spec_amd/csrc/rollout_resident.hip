@@ -74,14 +74,15 @@ struct RrArgs {
     int act;
     const uint16_t* B;                              // [V, r] MFMA-16 blocks
     const uint16_t* gi_table; int64_t ld_gi; int64_t table_rows;
-    const int64_t* prefix;                          // [M]
+    const int64_t* prefix; int64_t ld_prefix;       // row m at prefix[m * ld_prefix]
     const void* base; int64_t ld_base;              // row m, step s at base + m * ld_base + s * V (elements)
     const void* prior;
     const float* alpha; const float* beta;          // [steps]
     int M, G, V, steps, ntiles, upw;                // upw: GRU units per workgroup
     int mp_shift;                                   // log2 of M rounded up to a power of two
     int np_shift;                                   // log2(upw / 2): state words per row and workgroup
-    int64_t* out_ids; float* out_scores;            // [M, steps]
+    int64_t* out_ids; float* out_scores;            // row m, step s at [m * ld_out + s]
+    int64_t ld_out;
     unsigned int* counters;                         // control area
     unsigned long long* h_words;                    // per workgroup: rows x upw/2 words, on lines of its own
     unsigned long long* rank_words;                 // per rank workgroup: rows x 8 words
@@ -427,7 +428,7 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
     // ---- prefix: h_0 = GRU(gi_table[prefix], 0) --------------------------------
     bool ok = true;
     compute_gh(true);
-    gru_publish(a.prefix, 1, rr_tag(gen, 0));
+    gru_publish(a.prefix, a.ld_prefix, rr_tag(gen, 0));
 
     // ---- resident operands, loaded while the prefix state travels (a read
     // waits for every load issued before it, so the state went out first):
@@ -618,8 +619,8 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
                         val = f32_from_order_key((uint32_t)(key >> 32));
                     }
                     if (w == 0) {
-                        a.out_ids[(int64_t)m * a.steps + s] = id;
-                        if (a.out_scores) a.out_scores[(int64_t)m * a.steps + s] = val;
+                        a.out_ids[(int64_t)m * a.ld_out + s] = id;
+                        if (a.out_scores) a.out_scores[(int64_t)m * a.ld_out + s] = val;
                     }
                 }
                 s_ids[m] = id;
@@ -638,8 +639,8 @@ __global__ __launch_bounds__(kRrThreads) void rollout_resident_kernel(RrArgs a) 
             for (int i = threadIdx.x; i < M * a.steps; i += kRrThreads) {
                 const int m = i / a.steps, st = i - m * a.steps;
                 if (st >= s) {
-                    a.out_ids[(int64_t)m * a.steps + st] = -1;
-                    if (a.out_scores) a.out_scores[(int64_t)m * a.steps + st] = -__builtin_inff();
+                    a.out_ids[(int64_t)m * a.ld_out + st] = -1;
+                    if (a.out_scores) a.out_scores[(int64_t)m * a.ld_out + st] = -__builtin_inff();
                 }
             }
         }
@@ -713,7 +714,7 @@ hipError_t launch_rollout_resident(const ResidentRolloutArgs& r, void* ws, hipSt
     a.A = r.A; a.rank_b = r.rank_b; a.act = r.act;
     a.B = r.B;
     a.gi_table = r.gi_table; a.ld_gi = r.ld_gi; a.table_rows = r.table_rows;
-    a.prefix = r.prefix;
+    a.prefix = r.prefix; a.ld_prefix = r.ld_prefix;
     a.base = r.base; a.ld_base = r.ld_base;
     a.prior = r.prior;
     a.alpha = r.alpha; a.beta = r.beta;
@@ -725,7 +726,7 @@ hipError_t launch_rollout_resident(const ResidentRolloutArgs& r, void* ws, hipSt
     while ((1 << a.mp_shift) < a.M) ++a.mp_shift;
     a.np_shift = 0;
     while ((2 << a.np_shift) < a.upw) ++a.np_shift;   // upw / 2 = 1 << np_shift (upw a power of two)
-    a.out_ids = r.out_ids; a.out_scores = r.out_scores;
+    a.out_ids = r.out_ids; a.out_scores = r.out_scores; a.ld_out = r.ld_out;
     a.counters = reinterpret_cast<unsigned int*>(w + kCountersOff);
     a.h_words = reinterpret_cast<unsigned long long*>(w + kResidentOff);
     a.rank_words = reinterpret_cast<unsigned long long*>(w + kResidentOff + kResidentHWordBytes);

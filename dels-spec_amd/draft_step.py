@@ -72,11 +72,12 @@ class DeLSDraftStep:
         self.batch_size, self.k_draft, self.vocab_size, self.hidden_size = B, k, V, d
         self.static_hidden = torch.zeros(B, k, d, dtype=torch.bfloat16, device=device)
         self.static_base = torch.empty(B, k, V, dtype=torch.bfloat16, device=device)
-        self.static_first = torch.zeros(B, dtype=torch.int64, device=device)
-        self.static_first_score = torch.zeros(B, dtype=torch.float32, device=device)
-        self.static_rest = torch.zeros(B, k - 1, dtype=torch.int64, device=device)
-        self.static_rest_scores = torch.zeros(B, k - 1, dtype=torch.float32, device=device)
+        # the block's ids and scores: column 0 from the LM head's argmax, columns 1..k-1
+        # from the rollout, each written in place (the rollout reads its prefix ids there)
         self.static_out = torch.zeros(B, k, dtype=torch.int64, device=device)
+        self.static_scores = torch.zeros(B, k, dtype=torch.float32, device=device)
+        self.static_first, self.static_rest = self.static_out[:, 0], self.static_out[:, 1:]
+        self.static_first_score, self.static_rest_scores = self.static_scores[:, 0], self.static_scores[:, 1:]
         self._ws = new_workspace(device, max(lib.dels_rollout_ws_bytes(B, self.runner.gru_hidden_dim,
                                                                         self.runner.rank_dim, V),
                                              lib.dels_argmax_rows_ws_bytes(B, V),
@@ -93,19 +94,17 @@ class DeLSDraftStep:
             # base logits of positions 1..k-1 and the argmax of position 0 (rows b * k), one launch
             _lib.check(lib.dels_lm_head(self.static_hidden.data_ptr(), d, self._w_p.data.data_ptr(), B * k, d, V,
                                         self.static_base.data_ptr(), V, k, self.static_first.data_ptr(),
-                                        self.static_first_score.data_ptr(), 1, self._ws.data_ptr(),
+                                        self.static_first_score.data_ptr(), k, self._ws.data_ptr(),
                                         self._ws.numel(), stream.cuda_stream), "dels_lm_head")
         else:
             # base logits of the whole block: [B*k, d] . W^T, as nn.Linear
             torch.mm(self.static_hidden.view(B * k, d), self.lm_head_weight.t(),
                      out=self.static_base.view(B * k, V))
             _lib.check(lib.dels_argmax_rows(self.static_base.data_ptr(), k * V, _lib.DTYPE_BF16, B, V,
-                                            self.static_first.data_ptr(), self.static_first_score.data_ptr(), 1,
+                                            self.static_first.data_ptr(), self.static_first_score.data_ptr(), k,
                                             self._ws.data_ptr(), self._ws.numel(), stream.cuda_stream),
                        "dels_argmax_rows")
         _lib.check(lib.dels_rollout_enqueue(ctypes.byref(self._params), stream.cuda_stream), "dels_rollout_enqueue")
-        self.static_out[:, 0].copy_(self.static_first)
-        self.static_out[:, 1:].copy_(self.static_rest)
 
     def _capture(self) -> None:
         side = torch.cuda.Stream(device=self.device)

@@ -135,7 +135,9 @@ class DeLSGraphRunner:
     def _rollout_params(self, base: torch.Tensor, ld_base: int, prefix_ids: torch.Tensor, out_ids: torch.Tensor,
                         out_scores: torch.Tensor, ws: torch.Tensor) -> "_lib.RolloutParams":
         """The C rollout description over these weights, reading ``base`` rows ``ld_base`` elements apart
-        (steps * V for a [B, steps, V] tensor) and writing ``out_ids``/``out_scores`` [B, steps]."""
+        (steps * V for a [B, steps, V] tensor) and writing ``out_ids``/``out_scores`` [B, steps].  The
+        prefix ids and the outputs may be strided views (rows ``stride(0)`` apart, unit column stride;
+        ids and scores with the same row stride)."""
         B, G, r, V, S = self.batch_size, self.gru_hidden_dim, self.rank_dim, self.vocab_size, self.steps
         prior = self.baseline_logits if self.has_baseline else None
         dtype = self.baseline_logits.dtype
@@ -155,12 +157,16 @@ class DeLSGraphRunner:
         p.beta = self._beta.data_ptr()
         p.batch, p.steps, p.G, p.r, p.V = B, S, G, r, V
         p.weights_layout = _lib.LAYOUT_MFMA16 if self._packed else _lib.LAYOUT_ROWMAJOR
+        if out_scores.stride(0) != out_ids.stride(0) or out_ids.stride(-1) != 1 or out_scores.stride(-1) != 1:
+            raise ValueError("out_ids and out_scores need unit column stride and the same row stride")
         p.prefix_ids = prefix_ids.data_ptr()
+        p.ld_prefix = int(prefix_ids.stride(0))
         p.base = base.data_ptr()
         p.base_dtype = _DTYPES[base.dtype]
         p.ld_base = int(ld_base)
         p.out_ids = out_ids.data_ptr()
         p.out_scores = out_scores.data_ptr()
+        p.ld_out = int(out_ids.stride(0))
         p.h_a = self._h_a.data_ptr()
         p.h_b = self._h_b.data_ptr()
         p.rank = self._rank.data_ptr()

@@ -349,18 +349,20 @@ typedef struct dels_rollout {
     const float* beta;      /* [steps] fp32 */
     int64_t batch, steps, G, r, V;
     int weights_layout;     /* DELS_LAYOUT_* of w_hh, rank_w and lm_w */
-    const int64_t* prefix_ids; /* [batch] int64 */
+    const int64_t* prefix_ids; /* [batch] int64: row b at prefix_ids[b * ld_prefix] */
     const void* base;       /* [batch, steps, V]: row b, step s at base + (b * ld_base + s * V) */
     int base_dtype;
     int64_t ld_base;        /* elements between batch rows of base (0: steps * V) */
-    int64_t* out_ids;       /* [batch, steps] int64 */
-    float* out_scores;      /* [batch, steps] fp32 or NULL */
+    int64_t* out_ids;       /* [batch, steps] int64: row b, step s at out_ids[b * ld_out + s] */
+    float* out_scores;      /* [batch, steps] fp32 or NULL, rows ld_out apart as out_ids */
     void* h_a;              /* [batch, G] bf16 state buffers (ping-pong) */
     void* h_b;
     void* rank;             /* [batch, r] bf16 scratch for the rank (unused when the
                                step runs as one fused launch: packed weights, batch <= 16) */
     void* ws;
     size_t ws_bytes;
+    int64_t ld_prefix;      /* elements between batch rows of prefix_ids (0: 1) */
+    int64_t ld_out;         /* elements between batch rows of out_ids / out_scores (0: steps; else >= steps) */
 } dels_rollout;
 
 size_t dels_rollout_ws_bytes(int64_t batch, int64_t G, int64_t r, int64_t V);

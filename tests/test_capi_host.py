@@ -117,6 +117,13 @@ def test_argument_errors_return_codes(pkg):
     assert b"steps > 0" in lib.dels_last_error()
     h = ctypes.c_void_p()
     assert lib.dels_graph_create(ctypes.byref(p), ctypes.byref(h)) == -1 and not h.value
+    # output rows closer than steps apart, or a negative prefix stride, are refused
+    p2 = pkg._lib.RolloutParams()
+    p2.steps, p2.batch, p2.r, p2.V, p2.G, p2.act = 4, 2, 64, 100, 64, 0
+    p2.ld_out = 3
+    assert lib.dels_rollout_enqueue(ctypes.byref(p2), None) == -1 and b"ld_out" in lib.dels_last_error()
+    p2.ld_out, p2.ld_prefix = 0, -1
+    assert lib.dels_rollout_enqueue(ctypes.byref(p2), None) == -1 and b"ld_prefix" in lib.dels_last_error()
     assert lib.dels_graph_launch(None, None) == -1
     assert lib.dels_graph_destroy(None) == 0
     # unknown weight layout; packing into a too-small buffer

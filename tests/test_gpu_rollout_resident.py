@@ -128,3 +128,42 @@ def test_resident_rollout_gives_up_cleanly_and_recovers(pkg, dev):
     assert bool((ids >= 0).all())
     _check_against_oracle(head, prefix, base, prior, alphas, betas, "silu", ids, scores, False, False)
     runner.close()
+
+
+@pytest.mark.parametrize("resident", [True, False])
+def test_strided_prefix_ids_and_outputs(pkg, dev, resident):
+    """Prefix ids read from a column of a wider tensor (ld_prefix) and ids/scores written
+    into columns of wider tensors (ld_out), as the draft block writes its rollout into its
+    own output: the same values as the contiguous rollout, nothing written beside them."""
+    import ctypes
+    nb, steps, G, r, V = 4, 5, 1024, 256, 30011
+    print(f"case strided rollout nb={nb} steps={steps} resident={resident}", flush=True)
+    head = _Head(V, 64, G, r, "silu", False, seed=21, std=0.02).to(dev)
+    g = torch.Generator().manual_seed(22)
+    prior = torch.log_softmax(torch.randn(V, generator=g), 0)
+    alphas, betas = [0.9] * steps, [0.2] * steps
+    prefix = torch.randint(0, V, (nb, 1), generator=g)
+    base = (torch.randn(nb, steps, V, generator=g) * 0.5).to(torch.bfloat16)
+    lib = pkg._lib.load()
+    prev = lib.dels_debug_set_rollout_resident(1 if resident else 0)
+    try:
+        runner = pkg.DeLSGraphRunner(local_head=head, batch_size=nb, steps=steps, vocab_size=V, alpha_values=alphas,
+                                     beta_values=betas, baseline_logits=prior, device=dev)
+        want = runner(prefix.to(dev), base.to(dev)).clone()
+        want_sc = runner.static_scores.clone()
+        big_prefix = torch.full((nb, 3), -5, dtype=torch.int64, device=dev)
+        big_prefix[:, 1] = prefix[:, 0].to(dev)
+        big_out = torch.full((nb, steps + 3), -7, dtype=torch.int64, device=dev)
+        big_sc = torch.full((nb, steps + 3), -7.0, dtype=torch.float32, device=dev)
+        p = runner._rollout_params(runner.static_base_logits, steps * V, big_prefix[:, 1], big_out[:, 2:2 + steps],
+                                   big_sc[:, 2:2 + steps], runner._ws)
+        assert p.ld_prefix == 3 and p.ld_out == steps + 3
+        pkg._lib.check(lib.dels_rollout_enqueue(ctypes.byref(p), torch.cuda.current_stream(dev).cuda_stream),
+                       "dels_rollout_enqueue")
+        torch.cuda.synchronize()
+    finally:
+        lib.dels_debug_set_rollout_resident(prev)
+    assert torch.equal(big_out[:, 2:2 + steps], want) and torch.equal(big_sc[:, 2:2 + steps], want_sc)
+    assert bool((big_out[:, :2] == -7).all()) and bool((big_out[:, 2 + steps:] == -7).all())
+    assert bool((big_sc[:, :2] == -7.0).all()) and bool((big_sc[:, 2 + steps:] == -7.0).all())
+    runner.close()
