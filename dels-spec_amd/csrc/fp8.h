@@ -50,6 +50,16 @@ __device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
     return sign | code;
 }
 
+// Four floats, each of magnitude below 464, to e4m3 bytes (a in the lowest)
+// with gfx950's v_cvt_pk_fp8_f32, two per instruction.  Over every float of
+// magnitude below 464, both signs, the instruction (low- and high-word forms)
+// gives exactly the bytes of f32_to_e4m3 above (an exhaustive check on the
+// MI355X); absmax-scaled values (|v| <= 448) are always in that range.
+__device__ __forceinline__ uint32_t f32x4_to_e4m3(float a, float b, float c, float d) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true);
+}
+
 // e4m3fn byte -> bf16 bits (exact).  NaN codes are not produced by absmax
 // quantisation and are not expected here.
 __device__ __forceinline__ uint32_t e4m3_to_bf16_bits(uint32_t q) {
@@ -118,10 +128,8 @@ __device__ __forceinline__ void quantize_rank_coop(const uint16_t* rows, int64_t
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t x0 = raw[i][2 * h], x1 = raw[i][2 * h + 1];
-            w[h] = f32_to_e4m3(__uint_as_float(x0 << 16) * inv) |
-                   (f32_to_e4m3(__uint_as_float(x0 & 0xffff0000u) * inv) << 8) |
-                   (f32_to_e4m3(__uint_as_float(x1 << 16) * inv) << 16) |
-                   (f32_to_e4m3(__uint_as_float(x1 & 0xffff0000u) * inv) << 24);
+            w[h] = f32x4_to_e4m3(__uint_as_float(x0 << 16) * inv, __uint_as_float(x0 & 0xffff0000u) * inv,
+                                 __uint_as_float(x1 << 16) * inv, __uint_as_float(x1 & 0xffff0000u) * inv);
         }
         *reinterpret_cast<u32x2*>(s_rq + m * (R + 16) + seg * PER + 8 * i) = u32x2{w[0], w[1]};
     }

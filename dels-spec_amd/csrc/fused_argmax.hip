@@ -283,10 +283,8 @@ __global__ __launch_bounds__(256) void quantize_rank_e4m3_kernel(const uint16_t*
 #pragma unroll
     for (int hw = 0; hw < 2; ++hw) {
         const uint32_t x0 = v[2 * hw], x1 = v[2 * hw + 1];
-        w[hw] = f32_to_e4m3(__uint_as_float(x0 << 16) * inv) |
-                (f32_to_e4m3(__uint_as_float(x0 & 0xffff0000u) * inv) << 8) |
-                (f32_to_e4m3(__uint_as_float(x1 << 16) * inv) << 16) |
-                (f32_to_e4m3(__uint_as_float(x1 & 0xffff0000u) * inv) << 24);
+        w[hw] = f32x4_to_e4m3(__uint_as_float(x0 << 16) * inv, __uint_as_float(x0 & 0xffff0000u) * inv,
+                              __uint_as_float(x1 << 16) * inv, __uint_as_float(x1 & 0xffff0000u) * inv);
     }
     if (ok) *reinterpret_cast<u32x2*>(rank_q + (int64_t)m * r + 8 * lane) = u32x2{w[0], w[1]};
     if (lane == 0) rank_scale[m] = amax > 0.f ? amax / kE4M3Max : 1.f;

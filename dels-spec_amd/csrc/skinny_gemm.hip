@@ -593,9 +593,7 @@ __global__ __launch_bounds__(256) void rank_splitk_epilogue_kernel(SkinnyKArgs a
         __syncthreads();
         if (a.ncols == 512) amax = __builtin_fmaxf(s_amax[wave], s_amax[wave ^ 1]);
         const float inv = amax > 0.f ? kE4M3Max / amax : 1.f;
-        uint32_t qw = 0;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) qw |= f32_to_e4m3(xs[q] * inv) << (8 * q);
+        const uint32_t qw = f32x4_to_e4m3(xs[0] * inv, xs[1] * inv, xs[2] * inv, xs[3] * inv);
         if (valid) {
             *reinterpret_cast<uint32_t*>(a.out_q + (int64_t)m * a.ncols + n) = qw;
             if (n == 0) a.out_qscale[m] = amax > 0.f ? amax / kE4M3Max : 1.f;
