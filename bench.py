@@ -28,6 +28,7 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -231,9 +232,12 @@ def per_step_us(st, steps):
     return {k: (v * 1e3 / steps if k != "replays" else v) for k, v in st.items()}
 
 
-def bench_workload(pkg, name, args, dev, torch):
+def bench_workload(pkg, name, args, dev, torch, base_dtype=None):
+    """``base_dtype``: base logits of that dtype instead of the configuration's (same values, cast)."""
     nsets = args.sets
     x0 = pkg.synth.config_inputs(name)
+    if base_dtype is not None:
+        x0 = dataclasses.replace(x0, base=x0.base.to(base_dtype))
     per = set_bytes(x0)
     if nsets <= 0:
         nsets = max(3, -(-512 * 2**20 // per))
@@ -777,6 +781,17 @@ def main():
             out["m512"]["argmax_algorithmic_bytes"] = r512["argmax_bytes"]
         except Exception as e:  # informative record only
             out["m512"] = {"error": repr(e)}
+        try:   # the same shape with fp32 base logits (the configuration runs bf16 ones, as the runtime does)
+            r32, _ = bench_workload(pkg, "qwen3_8b_m512", argparse.Namespace(**{**vars(args), "sets": 0,
+                                                                                  "steps": min(args.steps, 100)}),
+                                    dev, torch, base_dtype=torch.float32)
+            out["m512_fp32_base"] = {k: r32[k] for k in ("rows_per_s", "us_per_step", "us_per_step_spread",
+                                                         "us_fused_argmax", "argmax_GBs", "argmax_hbm_frac",
+                                                         "argmax_mfma_frac", "hbm_frac_step", "mfma_frac_step")}
+            out["m512_fp32_base"]["argmax_algorithmic_bytes"] = r32["argmax_bytes"]
+            out["m512_fp32_base"]["step_bytes"] = r32["step_bytes"]
+        except Exception as e:  # informative record only
+            out["m512_fp32_base"] = {"error": repr(e)}
     if args.also_draft_step and args.workload != "qwen3_8b_m512":
         try:
             out["draft_step"] = bench_draft_step(pkg, args, dev, torch)

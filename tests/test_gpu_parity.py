@@ -95,6 +95,7 @@ TILED_CASES = [
     (256, 512, 30000, torch.float16, None, True),
     (300, 512, 50008, torch.bfloat16, torch.float32, True),
     (512, 512, 151936, torch.bfloat16, torch.bfloat16, True),
+    (512, 512, 151936, torch.float32, torch.bfloat16, True),    # the batched shape with fp32 base logits
     (512, 256, 151936, torch.float32, torch.float16, False),
 ]
 
