@@ -99,6 +99,20 @@ def test_resident_rollout_against_oracle(pkg, dev, nb, steps, G, r, V, bdt, with
     _check_against_oracle(head, prefix, base, prior, alphas, betas, act, pids, pscores, gru_bias, rank_bias)
 
 
+def _largest_resident_vocab(cus):
+    """The largest vocabulary the one-launch rollout takes on `cus` CUs (r = 256): its 16
+    rank workgroups hold 8 waves x 4 tiles of 16 vocabulary rows in registers, every other
+    workgroup those and 6 more tiles in LDS."""
+    return (16 * 32 + (cus - 16) * 38) * 16
+
+
+def test_resident_rollout_at_the_largest_vocabulary(pkg, dev):
+    """Every workgroup holding all the tiles it can, the last one ragged (V % 16 = 7)."""
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    V = _largest_resident_vocab(cus) - 9
+    test_resident_rollout_against_oracle(pkg, dev, 2, 4, 1024, 256, V, torch.bfloat16, True, "silu", False, False)
+
+
 def test_resident_rollout_gives_up_cleanly_and_recovers(pkg, dev):
     """With the waits' re-read limit at zero the launch cannot finish: it writes -1
     ids and still ends; the next launch (limit restored) on the same workspace
