@@ -690,7 +690,7 @@ def main():
             print(json.dumps({"config": name, **res}), flush=True)
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build targets one GPU: the fused argmax shards by rows or by "
+        print(json.dumps({"error": "one GPU per run: the fused argmax shards by rows or by "
                                    "vocabulary without collectives on the hot path; run with --gpus 1"}))
         sys.exit(2)
     import torch

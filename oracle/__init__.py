@@ -2,7 +2,7 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the shipped package imports this
 directory: only ``tests/``, ``__graft_entry__.smoke()`` and the CPU-baseline
-leg of ``bench.py`` use it, and only as the checker (or as the timed CPU
+leg of ``bench.py`` use it, and only to test results against (or as the timed CPU
 baseline), never as a fallback for the HIP path.
 """
 

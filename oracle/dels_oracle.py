@@ -1,6 +1,6 @@
 """CPU oracle: a numpy restatement of DeLS-Spec's draft-token selection path.
 
-TEST INFRASTRUCTURE ONLY -- the checker for the HIP path, never shipped and
+TEST INFRASTRUCTURE ONLY -- what the HIP path is tested against, never shipped and
 never called by the package.  Every function cites the reference lines it
 restates (paths relative to the dt-3t/DeLS-Spec repository root).
 

@@ -1,6 +1,6 @@
 """CPU oracle of the Domino correction path (code/kernel/domino.py).
 
-TEST INFRASTRUCTURE ONLY -- the checker for the HIP Domino kernel and rollout.
+TEST INFRASTRUCTURE ONLY -- the reference the HIP Domino kernel and rollout are tested against.
 
 Step semantics restated from _fused_mlp_bias_argmax_kernel and
 _reduce_argmax_kernel (code/kernel/domino.py:58-173):

@@ -1,6 +1,6 @@
 """CPU oracle of temperature sampling (code/dflash.py:31-38).
 
-TEST INFRASTRUCTURE ONLY -- the checker for the HIP sampling kernel.
+TEST INFRASTRUCTURE ONLY -- the reference the HIP sampling kernel is tested against.
 
 The reference draws ``torch.multinomial(softmax(logits / T), 1)``.  The GPU
 path draws the same distribution by a Gumbel-max, and this module restates it
