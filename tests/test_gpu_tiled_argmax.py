@@ -152,3 +152,26 @@ def test_tiled_many_rows_gather_argmax_markov_rows(pkg, dev):
     torch.cuda.synchronize()
     rank = f(E)[np.clip(tok.numpy(), 0, rows - 1)]
     assert_parity(ids, score, rank, f(W), f(base), f(prior), f(alpha), f(beta))
+
+
+def test_many_rows_argmax_with_views_the_tiled_kernel_cannot_stream(pkg, dev):
+    """At M >= 64 the tiled kernel moves base and prior rows with 16- and 4-byte
+    direct-to-LDS loads; views without that alignment -- a base starting one
+    element into its rows (ldbase % 8 != 0) and a 16-bit prior starting one
+    element into its buffer -- go to the GEMV kernel instead, with the same result."""
+    M, r, V = 80, 512, 30016
+    g = torch.Generator().manual_seed(21)
+    x = pkg.synth.lowrank_inputs(M, 64, r, V, base_dtype=torch.bfloat16, prior_dtype=torch.bfloat16,
+                                 per_position=True, seed=21)
+    rank = (torch.randn(M, r, generator=g) * 1.5).to(torch.bfloat16)
+    full = torch.zeros(M, V + 3, dtype=torch.bfloat16)
+    full[:, 1:V + 1] = x.base
+    pbuf = torch.zeros(V + 1, dtype=torch.bfloat16)
+    pbuf[1:] = x.prior
+    based = full.to(dev)[:, 1:V + 1]
+    priord = pbuf.to(dev)[1:]
+    assert based.data_ptr() % 16 != 0 and based.stride(0) % 8 != 0 and priord.data_ptr() % 4 != 0
+    Bp = pkg.pack_operand(x.B.to(dev))
+    ids, score = pkg.fused_argmax(rank.to(dev), Bp, based, priord, x.alpha.to(dev), x.beta.to(dev))
+    torch.cuda.synchronize()
+    assert_parity(ids, score, f(rank), f(x.B), f(x.base), f(x.prior), f(x.alpha), f(x.beta))
